@@ -1,0 +1,198 @@
+/*
+ * tmsample_hip.h -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * This library replaces TensorMark's host sampler and its GPU token kernels
+ * with batched HIP kernels.  Every entry point is plain C: device pointers,
+ * sizes, a hipStream_t, and an int status.  No exceptions and no C++ types
+ * cross this boundary.
+ *
+ * Interfaces replaced (paths are relative to the TensorMark tree):
+ *   tmsample::Opts                  tensormark/tmsample.h:31-35
+ *   tmsample::apply_repeat_penalty  tensormark/tmsample.h:52-63
+ *   tmsample::sample                tensormark/tmsample.h:173-200
+ *   sample_token (mask -> penalty -> sample composition)
+ *                                   tensormark/llama_chat.cpp:146-153, 184-209, 787-791
+ *   tm_metal_tok_argmax / tm_metal_tok_sample (GPU token kernels)
+ *                                   tensormark/llama.h:58-63, tensormark/metal_shim.mm:29-35
+ *   spec_generate_greedy's verify rule (greedy limit of tms_spec_verify)
+ *                                   tensormark/llama.h:5127-5131
+ *
+ * Per-row semantics of tms_sample_batch, in order:
+ *   1. grammar mask: ids whose bit is clear become -inf
+ *      (bit (id & 31) of word id >> 5, LSB first);
+ *   2. repetition penalty over the last repeat_last_n ids of the row's
+ *      history, compounding once per occurrence (v > 0 ? v / p : v * p);
+ *   3. frequency/presence penalty: v -= (float)count * freq + presence;
+ *   4. greedy: the first maximum (lowest id) of the penalised row;
+ *   5. otherwise lg = v / temperature (fp32 division), top-k by
+ *      (lg descending, id ascending), pr = exp((double)lg - (double)lg_max)
+ *      summed in order, top-p cut (cum >= top_p), min-p cut
+ *      (pr >= min_p), then an inverse-CDF draw over the survivors with
+ *      libstdc++ discrete_distribution arithmetic.  The uniform comes from
+ *      two 32-bit words (w0, w1): u = (w0 + w1 * 2^32) / 2^64 in double,
+ *      clamped below 1.  The words are Philox4x32-10 outputs 0 and 1 for
+ *      key = (seed lo, seed hi) and counter = (offset lo, offset hi, 0, 0),
+ *      or caller-supplied (`draws`).
+ */
+#ifndef TMSAMPLE_HIP_H
+#define TMSAMPLE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMS_ABI_VERSION 1
+
+/* Return codes of the entry points. */
+enum {
+    TMS_OK = 0,
+    TMS_ERR_INVALID_ARG = -1,   /* null pointer, bad size, unknown dtype */
+    TMS_ERR_CAPACITY = -2,      /* batch or vocab above the context's maxima */
+    TMS_ERR_HIP = -3,           /* a HIP runtime call failed */
+    TMS_ERR_NO_DEVICE = -4
+};
+
+/* Per-row status written to out_status. */
+enum {
+    TMS_ROW_OK = 0,
+    TMS_ROW_BAD_PARAMS = 1,   /* temperature <= 0 or non-finite on a sampled row */
+    TMS_ROW_ALL_MASKED = 2,   /* every id is -inf after mask and penalties */
+    TMS_ROW_NONFINITE = 3,    /* NaN or +inf after masking, or lg overflowed */
+    TMS_ROW_UNSUPPORTED = 4   /* top-p-only row with too many candidates */
+};
+
+enum {
+    TMS_DTYPE_F32 = 0,
+    TMS_DTYPE_F16 = 1,
+    TMS_DTYPE_BF16 = 2
+};
+
+/*
+ * Per-row sampler parameters.  The first three fields are tmsample::Opts
+ * (tensormark/tmsample.h:31-35) field for field; repeat_penalty and
+ * repeat_last_n are the `penalty` and `window` arguments of
+ * apply_repeat_penalty (tensormark/tmsample.h:52-53); `greedy` is the
+ * `greedy` argument of tmsample::sample (tensormark/tmsample.h:173-174).
+ * min_p, frequency_penalty, presence_penalty, seed and offset have no
+ * counterpart in the reference.
+ */
+typedef struct tms_row_params {
+    float temperature;        /* divides the logits; must be > 0 unless greedy */
+    int32_t top_k;            /* <= 0 or > vocab means the whole vocabulary */
+    float top_p;              /* smallest prefix with cumulative mass >= top_p */
+    float min_p;              /* keep pr >= min_p * pr_max; <= 0 disables */
+    float repeat_penalty;     /* <= 1 disables, as in the reference */
+    int32_t repeat_last_n;    /* window over the row's history */
+    float frequency_penalty;  /* 0 disables */
+    float presence_penalty;   /* 0 disables */
+    int32_t greedy;           /* non-zero: argmax, no temperature, no draw */
+    uint32_t flags;           /* reserved, must be 0 */
+    uint64_t seed;            /* Philox4x32-10 key */
+    uint64_t offset;          /* Philox4x32-10 counter words 0 and 1 */
+} tms_row_params;
+
+/* Opaque context: owns the device workspace for one device. */
+typedef struct tms_context tms_context;
+
+typedef struct tms_sample_args {
+    const void* logits;       /* device, [batch][row_stride] of dtype */
+    int32_t dtype;            /* TMS_DTYPE_* */
+    int32_t batch;
+    int32_t vocab;
+    int32_t topk_cap;         /* columns of out_topk_ids / out_topk_probs */
+    int64_t row_stride;       /* elements between rows, >= vocab */
+    const tms_row_params* params;   /* device, [batch] */
+    const int32_t* recent;    /* device, [batch][recent_stride] token history, nullable */
+    const int32_t* n_recent;  /* device, [batch] valid history length, nullable =
+                                 every row holds recent_stride ids */
+    int64_t recent_stride;
+    const uint32_t* mask;     /* device, [batch][mask_stride] allowed bits, nullable */
+    int64_t mask_stride;      /* words per row, >= ceil(vocab / 32) */
+    const uint32_t* draws;    /* device, [batch][2] words (w0, w1) used instead
+                                 of Philox, nullable */
+    int32_t* out_tokens;      /* device, [batch]; -1 on a row error */
+    int32_t* out_status;      /* device, [batch], TMS_ROW_* */
+    int32_t* out_keep;        /* device, [batch], nullable: survivors drawn from
+                                 (0 for greedy rows and errors) */
+    int32_t* out_topk_ids;    /* device, [batch][topk_cap], nullable: sorted
+                                 top-k ids, -1 padded */
+    float* out_topk_probs;    /* device, [batch][topk_cap], nullable:
+                                 pr / z of the same entries */
+} tms_sample_args;
+
+typedef struct tms_spec_args {
+    const void* target_logits;    /* device, [batch][k + 1][vocab] of dtype */
+    const void* draft_logits;     /* device, [batch][k][vocab] of dtype */
+    int32_t dtype;
+    int32_t batch;
+    int32_t k;                    /* draft tokens per sequence, 1..16 */
+    int32_t vocab;
+    const int32_t* draft_tokens;  /* device, [batch][k] */
+    const tms_row_params* params; /* device, [batch]: temperature, seed, offset */
+    const uint32_t* draws;        /* device, [batch][k + 1][2], nullable: words for
+                                     the k accept tests and the final draw */
+    int32_t* out_accepted;        /* device, [batch]: accepted draft count */
+    int32_t* out_token;           /* device, [batch]: residual or bonus token */
+    int32_t* out_status;          /* device, [batch], TMS_ROW_* */
+} tms_spec_args;
+
+/* Library version (TMS_ABI_VERSION). */
+int tms_abi_version(void);
+
+/* Static text for a TMS_* return code or TMS_ROW_* status. */
+const char* tms_status_string(int code);
+
+/*
+ * Create a context on `device` for batches up to max_batch rows of up to
+ * max_vocab ids.  Allocates the workspace (per-row counters and candidate
+ * lists) once; the sampling calls allocate nothing.  A context serves one
+ * stream at a time: concurrent calls on one context race on its workspace.
+ * Replaces the library-owned state the reference keeps in its Metal token
+ * slots (tensormark/metal.h:3191-3228).
+ */
+int tms_create(int device, int max_batch, int max_vocab, tms_context** out);
+int tms_destroy(tms_context* ctx);
+
+/* Device bytes the context's workspace holds. */
+size_t tms_workspace_bytes(const tms_context* ctx);
+
+/*
+ * Batched mask -> penalties -> temperature -> top-k -> softmax -> top-p /
+ * min-p -> draw, one launch, stream-ordered, no host synchronisation.
+ * Replaces sample_token (tensormark/llama_chat.cpp:146-153) with the grammar
+ * restriction of tensormark/llama_chat.cpp:184-209, i.e. the composition of
+ * apply_repeat_penalty (tensormark/tmsample.h:52-63) and tmsample::sample
+ * (tensormark/tmsample.h:173-200); greedy rows replace tm_metal_tok_argmax
+ * (tensormark/llama.h:58-59).
+ */
+int tms_sample_batch(tms_context* ctx, const tms_sample_args* args, hipStream_t stream);
+
+/*
+ * Speculative verify: for each sequence, accept draft i while
+ * u_i < p_t(x_i) / p_d(x_i); at the first rejection draw from
+ * normalize(max(p_t - p_d, 0)); if all k are accepted draw a bonus token
+ * from the target row k.  Softmax weights are exp(lg - max) quantised to
+ * multiples of 2^-44 and summed exactly in 64-bit integers.  The greedy
+ * limit (one-hot p_t and p_d) is the argmax-match rule of
+ * spec_generate_greedy (tensormark/llama.h:5127-5131).
+ */
+int tms_spec_verify(tms_context* ctx, const tms_spec_args* args, hipStream_t stream);
+
+/*
+ * Test hooks.  Run the device Philox4x32-10 on n (counter[4], key[2])
+ * tuples packed as 6 words each and write 4 words each; evaluate the device
+ * double exp on n inputs (which = 0: the HIP math library, 1: the
+ * library's own exp used by tms_spec_verify).
+ */
+int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipStream_t stream);
+int tms_debug_exp(const double* in, double* out, int n, int which, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMSAMPLE_HIP_H */

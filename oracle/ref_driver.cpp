@@ -1,0 +1,132 @@
+// ref_driver.cpp -- C entry points around the reference's own tmsample.h.
+//
+// TEST INFRASTRUCTURE ONLY.  Compiled by oracle/Makefile against the header
+// where it lies in the reference tree (-I$(REF)); the output goes to
+// oracle/_ref/ and is never committed.  It lets the tests pin the C oracle
+// against the compiled reference and lets bench.py time the reference
+// sampler on the host as the CPU baseline.
+//
+// The composition below is sample_token with the grammar restriction in
+// front (tensormark/llama_chat.cpp:787-791, 146-153, 184-209): the mask
+// writes -inf, then tmsample::apply_repeat_penalty, then tmsample::sample.
+
+#include "tmsample.h"
+
+#include <chrono>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <random>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// A 32-bit URNG that replays scripted words, for driving libstdc++'s
+// distribution code with chosen inputs.
+struct Script {
+    using result_type = std::uint32_t;
+    const std::uint32_t* w;
+    int n, i = 0;
+    static constexpr result_type min() { return 0; }
+    static constexpr result_type max() { return 0xFFFFFFFFu; }
+    result_type operator()() { return i < n ? w[i++] : 0u; }
+};
+
+void restrict_row(std::vector<float>& lg, const std::uint32_t* mask) {
+    if (!mask) return;
+    for (std::size_t i = 0; i < lg.size(); ++i)
+        if (!((mask[i >> 5] >> (i & 31)) & 1u)) lg[i] = -std::numeric_limits<float>::infinity();
+}
+
+int one_row(const float* logits, int V, float T, int top_k, float top_p, int greedy,
+            std::mt19937& rng, const std::int32_t* recent, int n_recent, int window,
+            float penalty, const std::uint32_t* mask) {
+    std::vector<float> lg(logits, logits + V);
+    restrict_row(lg, mask);
+    if (recent) tmsample::apply_repeat_penalty(lg, recent, n_recent, window, penalty);
+    return tmsample::sample(lg, V, tmsample::Opts{T, top_k, top_p}, greedy != 0, rng);
+}
+
+}  // namespace
+
+extern "C" {
+
+// std::generate_canonical<double, 53> on the words (w0, w1).
+double ref_canonical(std::uint32_t w0, std::uint32_t w1) {
+    const std::uint32_t w[2] = {w0, w1};
+    Script s{w, 2};
+    return std::generate_canonical<double, 53>(s);
+}
+
+// std::discrete_distribution<int>(pr, pr + n) drawn with the words (w0, w1);
+// *consumed = words the draw took from the generator.
+int ref_discrete(const double* pr, int n, std::uint32_t w0, std::uint32_t w1, int* consumed) {
+    const std::uint32_t w[2] = {w0, w1};
+    Script s{w, 2};
+    std::discrete_distribution<int> d(pr, pr + n);
+    const int r = d(s);
+    *consumed = s.i;
+    return r;
+}
+
+// tmsample::apply_repeat_penalty on a copy of row, written back.
+void ref_apply_repeat_penalty(float* row, int V, const std::int32_t* recent, int n_recent,
+                              int window, float penalty) {
+    std::vector<float> lg(row, row + V);
+    tmsample::apply_repeat_penalty(lg, recent, n_recent, window, penalty);
+    std::memcpy(row, lg.data(), sizeof(float) * static_cast<std::size_t>(V));
+}
+
+// One sample_token step with an mt19937 seeded by `seed`.  Reports the first
+// two words the generator would give (*w0, *w1) and how many it consumed.
+int ref_sample(const float* logits, int V, float T, int top_k, float top_p, int greedy,
+               std::uint32_t seed, const std::int32_t* recent, int n_recent, int window,
+               float penalty, const std::uint32_t* mask, std::uint32_t* w0, std::uint32_t* w1,
+               int* consumed) {
+    std::mt19937 rng(seed);
+    std::mt19937 probe = rng;
+    *w0 = probe();
+    *w1 = probe();
+    std::mt19937 after0 = rng;
+    const int tok = one_row(logits, V, T, top_k, top_p, greedy, rng, recent, n_recent, window,
+                            penalty, mask);
+    int n = 0;
+    while (n < 4 && !(after0 == rng)) { after0(); ++n; }
+    *consumed = n;
+    return tok;
+}
+
+// CPU baseline: sample B rows with `threads` workers, `reps` times; returns
+// the best wall time of one pass in seconds.  Rows are independent, so they
+// are dealt round-robin to the workers.
+double ref_bench(const float* logits, int B, int V, float T, int top_k, float top_p,
+                 const std::int32_t* recent, int recent_stride, int window, float penalty,
+                 const std::uint32_t* mask, int mask_stride, int threads, int reps,
+                 std::int32_t* tokens) {
+    if (threads < 1) threads = 1;
+    double best = 1e30;
+    for (int r = 0; r < reps; ++r) {
+        const auto t0 = std::chrono::steady_clock::now();
+        std::vector<std::thread> pool;
+        for (int w = 0; w < threads; ++w)
+            pool.emplace_back([&, w] {
+                std::mt19937 rng(1234u + static_cast<unsigned>(w));
+                for (int b = w; b < B; b += threads)
+                    tokens[b] = one_row(logits + static_cast<std::size_t>(b) * V, V, T, top_k,
+                                        top_p, 0, rng,
+                                        recent ? recent + static_cast<std::size_t>(b) * recent_stride
+                                               : nullptr,
+                                        recent_stride, window, penalty,
+                                        mask ? mask + static_cast<std::size_t>(b) * mask_stride
+                                             : nullptr);
+            });
+        for (auto& t : pool) t.join();
+        const double dt =
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        if (dt < best) best = dt;
+    }
+    return best;
+}
+
+}  // extern "C"

@@ -1,0 +1,431 @@
+/*
+ * tms_oracle.c -- CPU restatement of TensorMark's token-sampling path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP library, never part of
+ * it.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it.  Built with -O2 -ffp-contract=off so every float and double
+ * operation below is one IEEE operation in source order.
+ *
+ * What pins each function (checked in tests/test_oracle.py):
+ *   tmo_philox4x32_10       Random123 known-answer vectors (Salmon et al., SC'11).
+ *   tmo_canonical           libstdc++ std::generate_canonical<double,53> driven by
+ *                           a scripted generator, through oracle/_ref.
+ *   tmo_apply_mask          bitmask <-> allowed-list invariant; the -inf rule of
+ *                           GrammarFilter::restrict (llama_chat.cpp:206-207).
+ *   tmo_apply_repeat_penalty  compiled reference apply_repeat_penalty (oracle/_ref)
+ *                           and the closed form for counts 1..3.
+ *   tmo_apply_freq_presence closed form v - (c*freq + presence); brute force.
+ *                           No reference counterpart: parity unpinned by the
+ *                           reference, pinned by the closed form only.
+ *   tmo_sample_row          compiled reference tmsample::sample (oracle/_ref) on
+ *                           tie-free rows (token, keep); committed golden vectors
+ *                           (tests/golden/); brute-force enumeration on tiny V.
+ *                           min-p: closed form only (absent from the reference).
+ *   tmo_exp64, tmo_q44, tmo_spec_*  build-defined (no reference counterpart):
+ *                           exp64 against glibc exp within 2 ulp; spec verify
+ *                           against its one-hot (greedy) limit, p_t == p_d
+ *                           (always accept), brute-force rejection sampling
+ *                           marginals on V <= 8.
+ */
+#include "tms_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum { ROW_OK = 0, ROW_BAD_PARAMS = 1, ROW_ALL_MASKED = 2, ROW_NONFINITE = 3 };
+
+/* ------------------------------------------------------------------ Philox */
+
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+ * easy as 1, 2, 3", SC'11): ten rounds of two 32x32->64 multiplies with the
+ * key bumped by the Weyl constants between rounds. */
+void tmo_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* The two words a row's draw uses: key = seed, counter = (offset, stream, 0). */
+void tmo_row_words(uint64_t seed, uint64_t offset, uint32_t stream, uint32_t* w0, uint32_t* w1) {
+    const uint32_t ctr[4] = {(uint32_t)offset, (uint32_t)(offset >> 32), stream, 0u};
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    tmo_philox4x32_10(ctr, key, o);
+    *w0 = o[0];
+    *w1 = o[1];
+}
+
+/* std::generate_canonical<double, 53> over a 32-bit engine, as libstdc++
+ * computes it (/usr/include/c++/11/bits/random.tcc:3348-3380): two draws,
+ * sum = 0 + w0 * 1, sum += w1 * 2^32, ret = sum / 2^64, clamped below 1. */
+double tmo_canonical(uint32_t w0, uint32_t w1) {
+    double sum = 0.0;
+    sum += (double)w0 * 1.0;
+    sum += (double)w1 * 4294967296.0;
+    double ret = sum / 18446744073709551616.0;
+    if (ret >= 1.0) ret = nextafter(1.0, 0.0);
+    return ret;
+}
+
+/* ------------------------------------------------------------- transforms */
+
+/* GrammarFilter::restrict (tensormark/llama_chat.cpp:184-209): every id the
+ * allowed set lacks becomes -inf.  The allowed set travels as a bitmask,
+ * bit (id & 31) of word id >> 5.  The stall narrowing (llama_chat.cpp:
+ * 193-205) stays with the host that builds the mask. */
+void tmo_apply_mask(float* row, int V, const uint32_t* mask) {
+    if (!mask) return;
+    for (int i = 0; i < V; ++i)
+        if (!((mask[i >> 5] >> (i & 31)) & 1u)) row[i] = -INFINITY;
+}
+
+/* tmsample::apply_repeat_penalty (tensormark/tmsample.h:52-63): for each of the
+ * last `window` ids in range, v = v > 0 ? v / p : v * p, once per occurrence. */
+void tmo_apply_repeat_penalty(float* row, int V, const int32_t* recent, int n_recent,
+                              int window, float penalty) {
+    if (penalty <= 1.0f || window <= 0 || n_recent <= 0) return;
+    const int from = n_recent > window ? n_recent - window : 0;
+    for (int i = from; i < n_recent; ++i) {
+        const int t = recent[i];
+        if (t < 0 || t >= V) continue;
+        const float v = row[t];
+        row[t] = v > 0.f ? v / penalty : v * penalty;
+    }
+}
+
+/* Frequency/presence penalty (no reference counterpart; the llama.cpp
+ * convention): v -= (float)count * freq + presence over the same window. */
+void tmo_apply_freq_presence(float* row, int V, const int32_t* recent, int n_recent,
+                             int window, float freq, float presence) {
+    if ((freq == 0.0f && presence == 0.0f) || window <= 0 || n_recent <= 0) return;
+    const int from = n_recent > window ? n_recent - window : 0;
+    int* cnt = (int*)calloc((size_t)V, sizeof(int));
+    for (int i = from; i < n_recent; ++i) {
+        const int t = recent[i];
+        if (t >= 0 && t < V) cnt[t]++;
+    }
+    for (int i = 0; i < V; ++i)
+        if (cnt[i] > 0) {
+            const float t1 = (float)cnt[i] * freq;
+            const float t = t1 + presence;
+            row[i] = row[i] - t;
+        }
+    free(cnt);
+}
+
+/* --------------------------------------------------------------- sampling */
+
+typedef struct { float v; int id; } ent;
+
+/* The reference's order (tmsample.h:181-183: lg[a] > lg[b]) made total:
+ * equal values go lowest id first. */
+static int better(const ent* a, const ent* b) {
+    return a->v > b->v || (a->v == b->v && a->id < b->id);
+}
+
+static int cmp_ent(const void* pa, const void* pb) {
+    const ent* a = (const ent*)pa;
+    const ent* b = (const ent*)pb;
+    if (better(a, b)) return -1;
+    if (better(b, a)) return 1;
+    return 0;
+}
+
+/* The K best of lg[0..V) in order; nth_element + sort of the prefix in the
+ * reference (tmsample.h:179-183). */
+static void select_topk(const float* lg, int V, int K, ent* out) {
+    if ((long)K * 8 < V) {
+        int n = 0;
+        for (int i = 0; i < V; ++i) {
+            ent e = {lg[i], i};
+            if (n == K && !better(&e, &out[K - 1])) continue;
+            int pos = n < K ? n : K - 1;
+            while (pos > 0 && better(&e, &out[pos - 1])) {
+                out[pos] = out[pos - 1];
+                --pos;
+            }
+            out[pos] = e;
+            if (n < K) ++n;
+        }
+        return;
+    }
+    ent* all = (ent*)malloc((size_t)V * sizeof(ent));
+    for (int i = 0; i < V; ++i) { all[i].v = lg[i]; all[i].id = i; }
+    qsort(all, (size_t)V, sizeof(ent), cmp_ent);
+    memcpy(out, all, (size_t)K * sizeof(ent));
+    free(all);
+}
+
+/* tmsample::sample (tensormark/tmsample.h:173-200), with the draw of
+ * std::discrete_distribution (/usr/include/c++/11/bits/random.tcc:2656-2712)
+ * spelled out: sum = accumulate(pr[0..keep)), p = pr / sum,
+ * cp = partial_sum(p), cp.back() = 1, j = lower_bound(cp, u); keep == 1
+ * draws nothing.  Additions: the row status codes, the lowest-id tie order,
+ * top_k <= 0 meaning V, and the min-p cut. */
+int tmo_sample_row(const float* row, int V, const tmo_row_params* p, uint32_t w0, uint32_t w1,
+                   int32_t* token, int32_t* keep, int32_t* topk_ids, float* topk_probs,
+                   int topk_cap) {
+    *token = -1;
+    *keep = 0;
+    for (int j = 0; j < topk_cap; ++j) {
+        if (topk_ids) topk_ids[j] = -1;
+        if (topk_probs) topk_probs[j] = 0.0f;
+    }
+    if (!p->greedy && !(p->temperature > 0.0f && p->temperature <= FLT_MAX))
+        return ROW_BAD_PARAMS;
+    int nfin = 0;
+    for (int i = 0; i < V; ++i) {
+        const float v = row[i];
+        if (isnan(v) || v == INFINITY) return ROW_NONFINITE;
+        if (v != -INFINITY) ++nfin;
+    }
+    if (nfin == 0) return ROW_ALL_MASKED;
+
+    if (p->greedy) {
+        /* std::max_element: the first maximum (tmsample.h:175-176). */
+        int best = 0;
+        for (int i = 1; i < V; ++i)
+            if (row[best] < row[i]) best = i;
+        *token = best;
+        if (topk_cap > 0) {
+            if (topk_ids) topk_ids[0] = best;
+            if (topk_probs) topk_probs[0] = 1.0f;
+        }
+        return ROW_OK;
+    }
+
+    const int K = (p->top_k <= 0 || p->top_k > V) ? V : p->top_k;
+    float* lg = (float*)malloc((size_t)V * sizeof(float));
+    for (int i = 0; i < V; ++i) lg[i] = row[i] / p->temperature;
+    ent* top = (ent*)malloc((size_t)K * sizeof(ent));
+    select_topk(lg, V, K, top);
+    free(lg);
+
+    const float mx = top[0].v;
+    if (mx == INFINITY) { free(top); return ROW_NONFINITE; }
+    double* pr = (double*)malloc((size_t)K * sizeof(double));
+    double* zp = (double*)malloc((size_t)K * sizeof(double));
+    double z = 0;
+    for (int k = 0; k < K; ++k) {
+        pr[k] = exp((double)top[k].v - (double)mx);
+        z += pr[k];
+        zp[k] = z;
+    }
+    double cum = 0;
+    int kp = K;
+    for (int k = 0; k < K; ++k) {
+        cum += pr[k] / z;
+        if (cum >= (double)p->top_p) { kp = k + 1; break; }
+    }
+    if (p->min_p > 0.0f) {
+        int m = 1;
+        while (m < kp && pr[m] >= (double)p->min_p) ++m;
+        kp = m;
+    }
+    *keep = kp;
+    int j = 0;
+    if (kp >= 2) {
+        const double sum = zp[kp - 1];
+        const double u = tmo_canonical(w0, w1);
+        double cp = 0;
+        j = kp - 1;
+        for (int i = 0; i < kp; ++i) {
+            const double q = pr[i] / sum;
+            cp = (i == 0) ? q : cp + q;
+            const double c = (i == kp - 1) ? 1.0 : cp;
+            if (!(c < u)) { j = i; break; }
+        }
+    }
+    *token = top[j].id;
+    const int n = topk_cap < K ? topk_cap : K;
+    for (int i = 0; i < n; ++i) {
+        if (topk_ids) topk_ids[i] = top[i].id;
+        if (topk_probs) topk_probs[i] = (float)(pr[i] / z);
+    }
+    free(pr);
+    free(zp);
+    free(top);
+    return ROW_OK;
+}
+
+/* The per-row composition of sample_token with the grammar restriction
+ * (tensormark/llama_chat.cpp:787-791 then 146-153): mask, repetition
+ * penalty, frequency/presence, sample. */
+void tmo_sample_batch(const float* logits, int B, int V, int64_t row_stride,
+                      const tmo_row_params* params, const int32_t* recent,
+                      const int32_t* n_recent, int64_t recent_stride, const uint32_t* mask,
+                      int64_t mask_stride, const uint32_t* draws, int32_t* tokens,
+                      int32_t* status, int32_t* keep, int32_t* topk_ids, float* topk_probs,
+                      int topk_cap) {
+    float* row = (float*)malloc((size_t)V * sizeof(float));
+    for (int b = 0; b < B; ++b) {
+        const tmo_row_params* p = &params[b];
+        memcpy(row, logits + (int64_t)b * row_stride, (size_t)V * sizeof(float));
+        if (mask) tmo_apply_mask(row, V, mask + (int64_t)b * mask_stride);
+        if (recent) {
+            const int32_t* r = recent + (int64_t)b * recent_stride;
+            const int n = n_recent ? n_recent[b] : (int)recent_stride;
+            tmo_apply_repeat_penalty(row, V, r, n, p->repeat_last_n, p->repeat_penalty);
+            tmo_apply_freq_presence(row, V, r, n, p->repeat_last_n, p->frequency_penalty,
+                                    p->presence_penalty);
+        }
+        uint32_t w0, w1;
+        if (draws) {
+            w0 = draws[2 * b];
+            w1 = draws[2 * b + 1];
+        } else {
+            tmo_row_words(p->seed, p->offset, 0u, &w0, &w1);
+        }
+        int32_t kp = 0;
+        status[b] = tmo_sample_row(row, V, p, w0, w1, &tokens[b], &kp,
+                                   topk_ids ? topk_ids + (int64_t)b * topk_cap : NULL,
+                                   topk_probs ? topk_probs + (int64_t)b * topk_cap : NULL,
+                                   topk_cap);
+        if (keep) keep[b] = kp;
+    }
+    free(row);
+}
+
+/* ---------------------------------------------------- speculative verify */
+
+/* exp(x) from range reduction and a polynomial (Cody & Waite, "Software
+ * Manual for the Elementary Functions", 1980): x = k ln2 + r with
+ * |r| <= ln2/2, ln2 split into a double and its residual, e^r by its Taylor
+ * series to degree 13 in Horner form, then scaling by 2^k.  Used by the
+ * build-defined speculative verify so that the device and this oracle
+ * evaluate bit-identical weights; every step is one IEEE operation. */
+double tmo_exp64(double x) {
+    if (isnan(x)) return x;
+    if (x == -INFINITY || x < -746.0) return 0.0;
+    if (x > 709.782712893384) return INFINITY;
+    const double inv_ln2 = 1.4426950408889634;
+    const double ln2_hi = 0x1.62e42fefa39efp-1;
+    const double ln2_lo = 0x1.abc9e3b39803fp-56;
+    const double kd = floor(x * inv_ln2 + 0.5);
+    double r = fma(-kd, ln2_hi, x);
+    r = fma(-kd, ln2_lo, r);
+    static const double c[14] = {
+        1.0, 1.0, 1.0 / 2, 1.0 / 6, 1.0 / 24, 1.0 / 120, 1.0 / 720, 1.0 / 5040,
+        1.0 / 40320, 1.0 / 362880, 1.0 / 3628800, 1.0 / 39916800, 1.0 / 479001600,
+        1.0 / 6227020800.0};
+    double q = c[13];
+    for (int i = 12; i >= 0; --i) q = fma(q, r, c[i]);
+    int k = (int)kd;
+    if (k > 1023) {
+        q = q * 2.0;
+        k -= 1;
+    }
+    if (k < -1020) {
+        q = q * 0x1p-200;
+        k += 200;
+    }
+    union { double d; uint64_t u; } s;
+    s.u = (uint64_t)(k + 1023) << 52;
+    return q * s.d;
+}
+
+/* Weights on a 2^-44 grid: round(y * 2^44), half up. */
+int64_t tmo_q44(double y) {
+    return (int64_t)floor(y * 17592186044416.0 + 0.5);
+}
+
+/* Softmax weights of one row: lg = v / T, m = max lg,
+ * e_i = q44(exp64(lg_i - m)), Z = sum e_i (exact). */
+int tmo_spec_weights(const float* row, int V, float temperature, int64_t* e, int64_t* Z,
+                     float* m) {
+    float mx = -INFINITY;
+    for (int i = 0; i < V; ++i) {
+        const float v = row[i];
+        if (isnan(v) || v == INFINITY) return ROW_NONFINITE;
+        const float l = v / temperature;
+        if (l > mx) mx = l;
+    }
+    if (mx == -INFINITY) return ROW_ALL_MASKED;
+    if (mx == INFINITY) return ROW_NONFINITE;
+    int64_t z = 0;
+    for (int i = 0; i < V; ++i) {
+        const float l = row[i] / temperature;
+        e[i] = tmo_q44(tmo_exp64((double)l - (double)mx));
+        z += e[i];
+    }
+    *Z = z;
+    *m = mx;
+    return ROW_OK;
+}
+
+/* Smallest id whose inclusive prefix weight exceeds floor(u * W). */
+static int inverse_cdf(const int64_t* w, int V, int64_t W, double u) {
+    int64_t t = (int64_t)floor(u * (double)W);
+    if (t > W - 1) t = W - 1;
+    int64_t acc = 0;
+    for (int i = 0; i < V; ++i) {
+        acc += w[i];
+        if (acc > t) return i;
+    }
+    return V - 1;
+}
+
+/* Speculative accept/reject for one sequence (Leviathan, Kalman, Matias,
+ * "Fast Inference from Transformers via Speculative Decoding", 2023; Chen et
+ * al. 2023).  No reference counterpart beyond the greedy limit
+ * (tensormark/llama.h:5127-5131).  words holds k + 1 word pairs: pair i
+ * (i < k) is the accept test of draft i, pair k the final draw. */
+int tmo_spec_verify_seq(const float* target, const float* draft, int V, int k,
+                        const int32_t* draft_tokens, float temperature,
+                        const uint32_t* words, int32_t* accepted, int32_t* token) {
+    *accepted = 0;
+    *token = -1;
+    if (!(temperature > 0.0f && temperature <= FLT_MAX)) return ROW_BAD_PARAMS;
+    int64_t* et = (int64_t*)malloc((size_t)V * sizeof(int64_t));
+    int64_t* ed = (int64_t*)malloc((size_t)V * sizeof(int64_t));
+    int64_t Zt = 0, Zd = 0;
+    float mt, md;
+    const double uf = tmo_canonical(words[2 * k], words[2 * k + 1]);
+    int st = ROW_OK;
+    for (int i = 0; i < k; ++i) {
+        st = tmo_spec_weights(target + (int64_t)i * V, V, temperature, et, &Zt, &mt);
+        if (st) goto out;
+        st = tmo_spec_weights(draft + (int64_t)i * V, V, temperature, ed, &Zd, &md);
+        if (st) goto out;
+        const int x = draft_tokens[i];
+        if (x < 0 || x >= V) { st = ROW_BAD_PARAMS; goto out; }
+        double r;
+        if (ed[x] == 0) r = et[x] > 0 ? 1.0 : 0.0;
+        else r = ((double)et[x] * (double)Zd) / ((double)ed[x] * (double)Zt);
+        const double u = tmo_canonical(words[2 * i], words[2 * i + 1]);
+        if (u < r) continue;
+        /* First rejection: residual max(p_t - p_d, 0) on the 2^-44 grid. */
+        int64_t R = 0;
+        for (int v = 0; v < V; ++v) {
+            const double pt = (double)et[v] / (double)Zt;
+            const double pd = (double)ed[v] / (double)Zd;
+            const double d = pt - pd;
+            ed[v] = d > 0.0 ? tmo_q44(d) : 0;
+            R += ed[v];
+        }
+        *accepted = i;
+        *token = R > 0 ? inverse_cdf(ed, V, R, uf) : inverse_cdf(et, V, Zt, uf);
+        goto out;
+    }
+    st = tmo_spec_weights(target + (int64_t)k * V, V, temperature, et, &Zt, &mt);
+    if (st) goto out;
+    *accepted = k;
+    *token = inverse_cdf(et, V, Zt, uf);
+out:
+    free(et);
+    free(ed);
+    return st;
+}

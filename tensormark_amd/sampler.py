@@ -1,0 +1,303 @@
+"""Python host side of the MI355X sampler: ctypes over libtmsample_hip.so.
+
+Mirrors the reference sampler's interface (tensormark/tmsample.h:31-35 Opts,
+52-63 apply_repeat_penalty, 173-200 sample) for batched device tensors:
+``Opts`` carries the same three knobs, ``RowParams`` adds the per-row
+penalties, min-p and the Philox seed/offset, and ``Sampler.sample`` runs the
+composition of sample_token (tensormark/llama_chat.cpp:146-153) with the
+grammar restriction in front (llama_chat.cpp:184-209) in one HIP launch.
+
+PyTorch only supplies device memory and the stream.  There is no fallback:
+if the HIP library is missing or no GPU is present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import os
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtmsample_hip.so")
+
+TMS_OK = 0
+ROW_OK, ROW_BAD_PARAMS, ROW_ALL_MASKED, ROW_NONFINITE, ROW_UNSUPPORTED = 0, 1, 2, 3, 4
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+# Every symbol include/tmsample_hip.h declares.
+EXPORTS = (
+    "tms_abi_version",
+    "tms_status_string",
+    "tms_create",
+    "tms_destroy",
+    "tms_workspace_bytes",
+    "tms_sample_batch",
+    "tms_spec_verify",
+    "tms_debug_philox",
+    "tms_debug_exp",
+)
+
+
+class RowParams(C.Structure):
+    """tms_row_params: tmsample::Opts (tmsample.h:31-35) plus the extensions."""
+
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_k", C.c_int32),
+        ("top_p", C.c_float),
+        ("min_p", C.c_float),
+        ("repeat_penalty", C.c_float),
+        ("repeat_last_n", C.c_int32),
+        ("frequency_penalty", C.c_float),
+        ("presence_penalty", C.c_float),
+        ("greedy", C.c_int32),
+        ("flags", C.c_uint32),
+        ("seed", C.c_uint64),
+        ("offset", C.c_uint64),
+    ]
+
+
+ROW_DTYPE = np.dtype(
+    [
+        ("temperature", "<f4"), ("top_k", "<i4"), ("top_p", "<f4"), ("min_p", "<f4"),
+        ("repeat_penalty", "<f4"), ("repeat_last_n", "<i4"), ("frequency_penalty", "<f4"),
+        ("presence_penalty", "<f4"), ("greedy", "<i4"), ("flags", "<u4"), ("seed", "<u8"),
+        ("offset", "<u8"),
+    ]
+)
+assert ROW_DTYPE.itemsize == C.sizeof(RowParams) == 56
+
+
+@dataclasses.dataclass
+class Opts:
+    """tmsample::Opts (tensormark/tmsample.h:31-35), same defaults."""
+
+    temperature: float = 0.7
+    top_k: int = 40
+    top_p: float = 0.9
+
+
+def make_params(B: int, opts: Optional[Opts] = None, *, min_p=0.0, repeat_penalty=1.0,
+                repeat_last_n=64, frequency_penalty=0.0, presence_penalty=0.0, greedy=False,
+                seed=1234, offset=0) -> np.ndarray:
+    """A [B] ROW_DTYPE array; scalars broadcast, arrays give per-row values."""
+    o = opts or Opts()
+    p = np.zeros(B, ROW_DTYPE)
+    p["temperature"] = o.temperature
+    p["top_k"] = o.top_k
+    p["top_p"] = o.top_p
+    p["min_p"] = min_p
+    p["repeat_penalty"] = repeat_penalty
+    p["repeat_last_n"] = repeat_last_n
+    p["frequency_penalty"] = frequency_penalty
+    p["presence_penalty"] = presence_penalty
+    p["greedy"] = np.asarray(greedy).astype(np.int32)
+    p["seed"] = seed
+    p["offset"] = offset
+    return p
+
+
+class SampleArgs(C.Structure):
+    _fields_ = [
+        ("logits", C.c_void_p), ("dtype", C.c_int32), ("batch", C.c_int32),
+        ("vocab", C.c_int32), ("topk_cap", C.c_int32), ("row_stride", C.c_int64),
+        ("params", C.c_void_p), ("recent", C.c_void_p), ("n_recent", C.c_void_p),
+        ("recent_stride", C.c_int64), ("mask", C.c_void_p), ("mask_stride", C.c_int64),
+        ("draws", C.c_void_p), ("out_tokens", C.c_void_p), ("out_status", C.c_void_p),
+        ("out_keep", C.c_void_p), ("out_topk_ids", C.c_void_p), ("out_topk_probs", C.c_void_p),
+    ]
+
+
+class SpecArgs(C.Structure):
+    _fields_ = [
+        ("target_logits", C.c_void_p), ("draft_logits", C.c_void_p), ("dtype", C.c_int32),
+        ("batch", C.c_int32), ("k", C.c_int32), ("vocab", C.c_int32),
+        ("draft_tokens", C.c_void_p), ("params", C.c_void_p), ("draws", C.c_void_p),
+        ("out_accepted", C.c_void_p), ("out_token", C.c_void_p), ("out_status", C.c_void_p),
+    ]
+
+
+_LIB = None
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Load the HIP library; raises if it was not built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} not built: run python -m tensormark_amd.build")
+        lib = C.CDLL(path)
+        lib.tms_status_string.restype = C.c_char_p
+        lib.tms_workspace_bytes.restype = C.c_size_t
+        lib.tms_create.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+        lib.tms_destroy.argtypes = [C.c_void_p]
+        lib.tms_workspace_bytes.argtypes = [C.c_void_p]
+        lib.tms_sample_batch.argtypes = [C.c_void_p, C.POINTER(SampleArgs), C.c_void_p]
+        lib.tms_spec_verify.argtypes = [C.c_void_p, C.POINTER(SpecArgs), C.c_void_p]
+        lib.tms_debug_philox.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+        lib.tms_debug_exp.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+        _LIB = lib
+    return _LIB
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != TMS_OK:
+        msg = load_library().tms_status_string(rc).decode()
+        raise RuntimeError(f"{what} failed: {msg} ({rc})")
+
+
+def _torch():
+    import torch
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("tensormark_amd needs a HIP device; none is visible")
+    return torch
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_code(t) -> int:
+    import torch
+
+    return {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16,
+            torch.bfloat16: DTYPE_BF16}[t.dtype]
+
+
+class Sampler:
+    """A context (device workspace) for batches up to max_batch x max_vocab."""
+
+    def __init__(self, max_batch: int, max_vocab: int, device: int = 0):
+        torch = _torch()
+        self.torch = torch
+        self.lib = load_library()
+        self.device = device
+        h = C.c_void_p()
+        _check(self.lib.tms_create(device, max_batch, max_vocab, C.byref(h)), "tms_create")
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.tms_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(self.lib.tms_workspace_bytes(self.handle))
+
+    def params_tensor(self, params: np.ndarray):
+        raw = np.ascontiguousarray(params, ROW_DTYPE).view(np.uint8)
+        return self.torch.from_numpy(raw.copy()).to(f"cuda:{self.device}")
+
+    def sample(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
+               topk_cap: int = 0, out=None, stream=None):
+        """Sample one token per row of ``logits`` ([B, V] fp32/fp16/bf16, cuda).
+
+        ``params`` is a device uint8 tensor from params_tensor() (or a numpy
+        ROW_DTYPE array, uploaded here).  Returns a dict of device tensors:
+        tokens, status, keep, and topk_ids/topk_probs when topk_cap > 0.
+        """
+        torch = self.torch
+        if isinstance(params, np.ndarray):
+            params = self.params_tensor(params)
+        B, V = logits.shape
+        dev = logits.device
+        if out is None:
+            out = {
+                "tokens": torch.empty(B, dtype=torch.int32, device=dev),
+                "status": torch.empty(B, dtype=torch.int32, device=dev),
+                "keep": torch.empty(B, dtype=torch.int32, device=dev),
+            }
+            if topk_cap:
+                out["topk_ids"] = torch.empty((B, topk_cap), dtype=torch.int32, device=dev)
+                out["topk_probs"] = torch.empty((B, topk_cap), dtype=torch.float32, device=dev)
+        a = self.make_args(logits, params, recent=recent, n_recent=n_recent, mask=mask,
+                           draws=draws, topk_cap=topk_cap, out=out)
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        _check(self.lib.tms_sample_batch(self.handle, C.byref(a), C.c_void_p(s)),
+               "tms_sample_batch")
+        return out
+
+    def make_args(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
+                  topk_cap=0, out=None) -> SampleArgs:
+        B, V = logits.shape
+        a = SampleArgs()
+        a.logits = logits.data_ptr()
+        a.dtype = _dtype_code(logits)
+        a.batch = B
+        a.vocab = V
+        a.row_stride = logits.stride(0)
+        a.params = params.data_ptr()
+        a.recent = _ptr(recent)
+        a.recent_stride = recent.shape[1] if recent is not None else 0
+        a.n_recent = _ptr(n_recent)
+        a.mask = _ptr(mask)
+        a.mask_stride = mask.shape[1] if mask is not None else 0
+        a.draws = _ptr(draws)
+        a.out_tokens = out["tokens"].data_ptr()
+        a.out_status = out["status"].data_ptr()
+        a.out_keep = _ptr(out.get("keep"))
+        a.topk_cap = topk_cap
+        a.out_topk_ids = _ptr(out.get("topk_ids")) if topk_cap else None
+        a.out_topk_probs = _ptr(out.get("topk_probs")) if topk_cap else None
+        return a
+
+    def spec_verify(self, target, draft, draft_tokens, params, *, draws=None, stream=None):
+        """Speculative verify: target [B, k+1, V], draft [B, k, V], tokens [B, k]."""
+        torch = self.torch
+        if isinstance(params, np.ndarray):
+            params = self.params_tensor(params)
+        B, k1, V = target.shape
+        dev = target.device
+        out = {
+            "accepted": torch.empty(B, dtype=torch.int32, device=dev),
+            "token": torch.empty(B, dtype=torch.int32, device=dev),
+            "status": torch.empty(B, dtype=torch.int32, device=dev),
+        }
+        a = SpecArgs()
+        a.target_logits = target.data_ptr()
+        a.draft_logits = draft.data_ptr()
+        a.dtype = _dtype_code(target)
+        a.batch = B
+        a.k = k1 - 1
+        a.vocab = V
+        a.draft_tokens = draft_tokens.data_ptr()
+        a.params = params.data_ptr()
+        a.draws = _ptr(draws)
+        a.out_accepted = out["accepted"].data_ptr()
+        a.out_token = out["token"].data_ptr()
+        a.out_status = out["status"].data_ptr()
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        _check(self.lib.tms_spec_verify(self.handle, C.byref(a), C.c_void_p(s)),
+               "tms_spec_verify")
+        return out
+
+
+def debug_philox(in6, out4=None):
+    """Device Philox4x32-10 on a [n, 6] uint32 cuda tensor (as int32)."""
+    torch = _torch()
+    n = in6.shape[0]
+    if out4 is None:
+        out4 = torch.empty((n, 4), dtype=torch.int32, device=in6.device)
+    s = torch.cuda.current_stream(in6.device).cuda_stream
+    _check(load_library().tms_debug_philox(in6.data_ptr(), out4.data_ptr(), n, C.c_void_p(s)),
+           "tms_debug_philox")
+    return out4
+
+
+def debug_exp(x, which: int):
+    torch = _torch()
+    out = torch.empty_like(x)
+    s = torch.cuda.current_stream(x.device).cuda_stream
+    _check(load_library().tms_debug_exp(x.data_ptr(), out.data_ptr(), x.numel(), which,
+                                        C.c_void_p(s)), "tms_debug_exp")
+    return out

@@ -1,0 +1,259 @@
+"""GPU parity: the HIP sampler (through the C ABI) against the CPU oracle and
+the golden vectors of the compiled reference.  Token ids, keep counts and
+top-k id lists must be bit-exact; top-k probabilities within 1e-6 relative."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tensormark_amd import workloads
+from tests.helpers import golden_cases, params_array
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, torch, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.view(dtype)
+    return t.to("cuda:0")
+
+
+def run_gpu(sampler, logits, params, recent=None, n_recent=None, mask=None, draws=None,
+            topk_cap=0, dtype="f32"):
+    import torch
+
+    if dtype == "f32":
+        x = _dev(logits.astype(np.float32), torch)
+    elif dtype == "f16":
+        x = _dev(logits.astype(np.float16), torch)
+    else:
+        x = _dev(logits, torch, torch.bfloat16)   # uint16 bf16 bits
+    out = sampler.sample(
+        x, params,
+        recent=None if recent is None else _dev(recent.astype(np.int32), torch),
+        n_recent=None if n_recent is None else _dev(n_recent.astype(np.int32), torch),
+        mask=None if mask is None else _dev(mask.astype(np.uint32).view(np.int32), torch),
+        draws=None if draws is None else _dev(draws.astype(np.uint32).view(np.int32), torch),
+        topk_cap=topk_cap)
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in out.items()}
+
+
+def check(gpu, want, topk_cap=0, rows=None):
+    rows = np.arange(len(want["tokens"])) if rows is None else rows
+    for b in rows:
+        assert gpu["status"][b] == want["status"][b], (b, gpu["status"][b], want["status"][b])
+        assert gpu["tokens"][b] == want["tokens"][b], (b, gpu["tokens"][b], want["tokens"][b])
+        assert gpu["keep"][b] == want["keep"][b], (b, gpu["keep"][b], want["keep"][b])
+        if topk_cap:
+            gi, wi = gpu["topk_ids"][b], want["topk_ids"][b]
+            assert np.array_equal(gi, wi), (b, gi[:8], wi[:8])
+            gp, wp = gpu["topk_probs"][b], want["topk_probs"][b]
+            assert np.allclose(gp, wp, rtol=1e-6, atol=0), b
+
+
+def test_philox_device_matches_oracle(orc):
+    import torch
+
+    from tensormark_amd.sampler import debug_philox
+
+    rng = np.random.default_rng(0)
+    ins = [list(c) + list(k) for c, k, _ in [((0, 0, 0, 0), (0, 0), 0),
+                                               ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, 0)]]
+    ins += [list(int(v) for v in rng.integers(0, 2**32, 6)) for _ in range(4096)]
+    a = np.array(ins, np.uint32)
+    out = debug_philox(_dev(a.view(np.int32), torch)).cpu().numpy().view(np.uint32)
+    for i in range(len(a)):
+        assert list(out[i]) == orc.philox(a[i, :4], a[i, 4:]), i
+
+
+def test_exp64_device_bitwise_equals_oracle(orc):
+    import torch
+
+    from tensormark_amd.sampler import debug_exp
+
+    rng = np.random.default_rng(1)
+    xs = np.concatenate([-rng.random(50000) * 60, -rng.random(5000) * 745, [0.0, -746.5]])
+    y = debug_exp(torch.from_numpy(xs).to("cuda:0"), 1).cpu().numpy()
+    want = np.array([orc.exp64(float(v)) for v in xs])
+    assert np.array_equal(y.view(np.uint64), want.view(np.uint64))
+
+
+def test_device_libm_exp_vs_glibc_report():
+    """The sampler's fp64 softmax uses the HIP math library's exp where the
+    reference uses glibc's.  Report how often they differ (at most 1 ulp)."""
+    import math
+
+    import torch
+
+    from tensormark_amd.sampler import debug_exp
+
+    rng = np.random.default_rng(2)
+    xs = -rng.random(200000) * 40
+    y = debug_exp(torch.from_numpy(xs).to("cuda:0"), 0).cpu().numpy()
+    g = np.exp(xs)   # numpy uses the platform libm (glibc)
+    diff = y != g
+    ulps = np.abs(y[diff] - g[diff]) / np.array([math.ulp(v) for v in g[diff]])
+    print(f"\nlibm exp: {diff.sum()} of {len(xs)} differ from glibc; max {ulps.max() if len(ulps) else 0} ulp")
+    assert len(ulps) == 0 or ulps.max() <= 1.0
+
+
+def test_golden_vectors_gpu(sampler, golden):
+    for i, x, p, recent, mask, w0, w1, m in golden_cases(golden):
+        g = run_gpu(sampler, x[None], p, recent=None if recent is None else recent[None],
+                    mask=None if mask is None else mask[None],
+                    draws=np.array([[w0, w1]], np.uint32))
+        assert g["status"][0] == 0, i
+        assert g["tokens"][0] == m["tok"], (i, g["tokens"][0], m["tok"])
+        if not m["g"]:
+            assert (g["keep"][0] >= 2) == (m["used"] == 2), i
+
+
+def test_cfg1_vs_oracle(sampler, orc):
+    w = workloads.cfg1()
+    for off in range(20):
+        p = w["params"].copy()
+        p["offset"] = off
+        want = orc.sample_batch(w["logits"], p, recent=w["recent"], topk_cap=40)
+        g = run_gpu(sampler, w["logits"], p, recent=w["recent"], topk_cap=40)
+        check(g, want, 40)
+
+
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_cfg2_full_size_vs_oracle(sampler, orc, with_mask):
+    w = workloads.cfg2(with_mask=with_mask)
+    want = orc.sample_batch(w["logits"], w["params"], recent=w["recent"], mask=w["mask"],
+                            topk_cap=40)
+    g = run_gpu(sampler, w["logits"], w["params"], recent=w["recent"], mask=w["mask"],
+                topk_cap=40)
+    check(g, want, 40)
+
+
+def test_cfg3_full_size_fp16_vs_oracle(sampler, orc):
+    w = workloads.cfg3()
+    x32 = w["logits"].astype(np.float32)
+    want = orc.sample_batch(x32, w["params"], mask=w["mask"], topk_cap=64)
+    g = run_gpu(sampler, w["logits"], w["params"], mask=w["mask"], topk_cap=64, dtype="f16")
+    check(g, want, 64)
+
+
+def test_cfg5_rows_bf16_vs_oracle(sampler, orc):
+    w = workloads.cfg5(B=48)
+    bits = workloads.to_bf16_bits(w["logits"])
+    x32 = workloads.bf16_bits_to_f32(bits)
+    want = orc.sample_batch(x32, w["params"], recent=w["recent"], topk_cap=100)
+    g = run_gpu(sampler, bits, w["params"], recent=w["recent"], topk_cap=100, dtype="bf16")
+    check(g, want, 100)
+
+
+def test_many_draws_same_row(sampler, orc):
+    """One row, 256 batch copies with different uniforms: every draw matches."""
+    rng = np.random.default_rng(3)
+    V = 5000
+    x = np.repeat(rng.normal(0, 1.0, (1, V)).astype(np.float32), 256, axis=0)
+    p = params_array(256, temperature=1.3, top_k=100, top_p=0.97, seed=np.arange(256))
+    want = orc.sample_batch(x, p, topk_cap=100)
+    g = run_gpu(sampler, x, p, topk_cap=100)
+    check(g, want, 100)
+
+
+EDGE = {
+    "all_masked": dict(),
+    "nan": dict(),
+    "posinf": dict(),
+    "bad_temp": dict(),
+    "ties_all_equal": dict(),
+    "few_allowed": dict(),
+    "topk1": dict(),
+    "topk_gt_V": dict(),
+    "tiny_temp": dict(),
+    "big_window": dict(),
+    "unaligned_V": dict(),
+    "small_V": dict(),
+    "top_p_one": dict(),
+    "greedy_ties": dict(),
+    "quantized_ties": dict(),
+}
+
+
+def _edge_case(name, rng):
+    V = 20000
+    x = rng.normal(0, 2, (4, V)).astype(np.float32)
+    p = params_array(4, temperature=0.9, top_k=40, top_p=0.9, seed=np.arange(4))
+    recent = mask = None
+    if name == "all_masked":
+        mask = np.zeros((4, (V + 31) // 32), np.uint32)
+        mask[1:, :] = 0xFFFFFFFF
+    elif name == "nan":
+        x[0, 123] = np.nan
+        x[2, 19999] = np.nan
+    elif name == "posinf":
+        x[1, 7] = np.inf
+    elif name == "bad_temp":
+        p["temperature"] = [0.0, -1.0, np.inf, 0.5]
+    elif name == "ties_all_equal":
+        x[:] = 1.0
+        x[3, ::7] = 2.0
+    elif name == "few_allowed":
+        bits = np.zeros((4, ((V + 31) // 32) * 32), bool)
+        for b in range(4):
+            bits[b, rng.choice(V, size=[3, 10, 39, 45][b], replace=False)] = True
+        mask = workloads.pack_bits(bits)
+    elif name == "topk1":
+        p["top_k"] = 1
+    elif name == "topk_gt_V":
+        V = 300
+        x = x[:, :V].copy()
+        p["top_k"] = [V + 5, V, 0, -3]
+        p["top_p"] = 0.99
+    elif name == "tiny_temp":
+        p["temperature"] = [1e-3, 1e-6, 3.0, 100.0]
+    elif name == "big_window":
+        recent = rng.integers(0, 50, (4, 2000)).astype(np.int32)
+        recent[:, ::3] = 7
+        x[:, :50] += 8.0
+        p["repeat_penalty"] = 1.3
+        p["repeat_last_n"] = [2000, 1500, 10, 0]
+        p["frequency_penalty"] = 0.05
+        p["presence_penalty"] = 0.3
+    elif name == "unaligned_V":
+        V = 20001
+        x = rng.normal(0, 2, (4, V)).astype(np.float32)
+    elif name == "small_V":
+        V = 37
+        x = rng.normal(0, 2, (4, V)).astype(np.float32)
+        p["top_k"] = [40, 5, 37, 1]
+    elif name == "top_p_one":
+        p["top_p"] = [1.0, 1.0, 0.0, 2.0]
+        p["top_k"] = [40, 128, 40, 0]
+    elif name == "greedy_ties":
+        x[:] = 0.5
+        x[1, 5000] = 0.75
+        x[2, 19999] = 0.75
+        x[2, 15000] = 0.75
+        p["greedy"] = 1
+    elif name == "quantized_ties":
+        x = np.round(x * 2) / 2
+        p["top_k"] = [40, 100, 7, 128]
+    return x, p, recent, mask
+
+
+@pytest.mark.parametrize("name", list(EDGE))
+def test_edge_cases(sampler, orc, name):
+    rng = np.random.default_rng(abs(hash(name)) % 2**32)
+    x, p, recent, mask = _edge_case(name, rng)
+    cap = 40
+    want = orc.sample_batch(x, p, recent=recent, mask=mask, topk_cap=cap)
+    g = run_gpu(sampler, x, p, recent=recent, mask=mask, topk_cap=cap)
+    check(g, want, cap)
+
+
+def test_repeated_calls_reuse_workspace(sampler, orc):
+    """Back-to-back launches on one context: the arrival counters reset."""
+    w = workloads.cfg2(B=16, V=40000, seed=9)
+    want = orc.sample_batch(w["logits"], w["params"], recent=w["recent"], topk_cap=40)
+    for _ in range(5):
+        g = run_gpu(sampler, w["logits"], w["params"], recent=w["recent"], topk_cap=40)
+        check(g, want, 40)
