@@ -156,21 +156,22 @@ def main():
             for _ in range(args.steps):
                 launch()
         torch.cuda.synchronize()
-        graph.replay()   # one untimed replay: graph upload
+        with torch.cuda.stream(stream):
+            graph.replay()   # one untimed replay: graph upload
         torch.cuda.synchronize()
 
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    e0.record(stream)
-    if graph is not None:
-        graph.replay()
-    else:
-        with torch.cuda.stream(stream):
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
             for _ in range(args.steps):
                 launch()
-    e1.record(stream)
+        e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
