@@ -62,7 +62,8 @@ enum {
     TMS_ROW_BAD_PARAMS = 1,   /* temperature <= 0 or non-finite on a sampled row */
     TMS_ROW_ALL_MASKED = 2,   /* every id is -inf after mask and penalties */
     TMS_ROW_NONFINITE = 3,    /* NaN or +inf after masking, or lg overflowed */
-    TMS_ROW_UNSUPPORTED = 4   /* top-p-only row with too many candidates */
+    TMS_ROW_UNSUPPORTED = 4,  /* top-p-only row with too many candidates */
+    TMS_ROW_INTERNAL = 5      /* a chunk list never arrived (bounded wait expired) */
 };
 
 enum {

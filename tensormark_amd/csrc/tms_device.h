@@ -162,15 +162,63 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
     return v;
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
+// DPP lane moves (row_shr:n within 16-lane rows, row_bcast:15/31 across
+// rows).  `old` fills lanes whose source is outside the row or masked.
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xF, BOUND_ZERO);
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave (DPP, no LDS).
 __device__ __forceinline__ int wave_incl_scan_i32(int v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(v, d, 64);
-        if (lane >= d) v += o;
+    uint32_t u = (uint32_t)v;
+    u += dpp_u32<0x111, 0xF, true>(0u, u);   // row_shr:1
+    u += dpp_u32<0x112, 0xF, true>(0u, u);   // row_shr:2
+    u += dpp_u32<0x114, 0xF, true>(0u, u);   // row_shr:4
+    u += dpp_u32<0x118, 0xF, true>(0u, u);   // row_shr:8
+    u += dpp_u32<0x142, 0xA, false>(0u, u);  // row_bcast:15 into rows 1 and 3
+    u += dpp_u32<0x143, 0xC, false>(0u, u);  // row_bcast:31 into rows 2 and 3
+    return (int)u;
+}
+
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+    return __builtin_amdgcn_readlane(wave_incl_scan_i32(v), 63);
+}
+
+// Maximum over the wave of u64 keys, by DPP steps towards lane 63.
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+#define TMS_MAXSTEP(CTRL, RM, BZ)                                                   \
+    {                                                                             \
+        const uint32_t lo = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)v);               \
+        const uint32_t hi = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)(v >> 32));       \
+        const uint64_t o = ((uint64_t)hi << 32) | lo;                              \
+        v = o > v ? o : v;                                                        \
     }
-    return v;
+    TMS_MAXSTEP(0x111, 0xF, true)
+    TMS_MAXSTEP(0x112, 0xF, true)
+    TMS_MAXSTEP(0x114, 0xF, true)
+    TMS_MAXSTEP(0x118, 0xF, true)
+    TMS_MAXSTEP(0x142, 0xA, false)
+    TMS_MAXSTEP(0x143, 0xC, false)
+#undef TMS_MAXSTEP
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Maximum over the wave of floats (no NaN), by DPP steps towards lane 63.
+__device__ __forceinline__ float wave_max_f32_dpp(float v) {
+    const uint32_t ninf = 0xFF800000u;
+#define TMS_FMAXSTEP(CTRL, RM, BZ) \
+    v = fmaxf(v, __uint_as_float(dpp_u32<CTRL, RM, BZ>(ninf, __float_as_uint(v))));
+    TMS_FMAXSTEP(0x111, 0xF, false)
+    TMS_FMAXSTEP(0x112, 0xF, false)
+    TMS_FMAXSTEP(0x114, 0xF, false)
+    TMS_FMAXSTEP(0x118, 0xF, false)
+    TMS_FMAXSTEP(0x142, 0xA, false)
+    TMS_FMAXSTEP(0x143, 0xC, false)
+#undef TMS_FMAXSTEP
+    return __uint_as_float(__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
 }
 
 __device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t v) {
@@ -221,6 +269,59 @@ __device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v) {
         }
     }
     return v;
+}
+
+}  // namespace tms
+
+namespace tms {
+
+// Sort 128 u64 keys held two per lane (entry i = lane + 64 * slot) across a
+// wave, descending.
+__device__ __forceinline__ void wave_sort_desc_u64x2(uint64_t& a0, uint64_t& a1) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 2; k <= 128; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j >= 1; j >>= 1) {
+            if (j == 64) {
+                // Partners are the two slots of one lane; entry index bit 6
+                // is the slot, so the block direction comes from k alone.
+                const bool desc = true;   // k == 128: one descending block
+                const uint64_t mx = a0 > a1 ? a0 : a1;
+                const uint64_t mn = a0 > a1 ? a1 : a0;
+                a0 = desc ? mx : mn;
+                a1 = desc ? mn : mx;
+            } else {
+                const uint64_t o0 = shfl_xor_u64(a0, j);
+                const uint64_t o1 = shfl_xor_u64(a1, j);
+                const bool lower = (lane & j) == 0;
+                // entry index of slot s: lane + 64 s; block direction bit k.
+                const bool desc0 = (lane & k) == 0;
+                const bool desc1 = ((lane + 64) & k) == 0;
+                const bool tmax0 = (lower == desc0);
+                const bool tmax1 = (lower == desc1);
+                const uint64_t mx0 = o0 > a0 ? o0 : a0, mn0 = o0 > a0 ? a0 : o0;
+                const uint64_t mx1 = o1 > a1 ? o1 : a1, mn1 = o1 > a1 ? a1 : o1;
+                a0 = tmax0 ? mx0 : mn0;
+                a1 = tmax1 ? mx1 : mn1;
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// The largest float below x (x finite, not -FLT_MAX): one step down in the
+// order of IEEE values, by integer arithmetic on the bits.
+__device__ __forceinline__ float float_below(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) == 0) return __uint_as_float(0x80000001u);   // +-0 -> -min subnormal
+    return __uint_as_float((u & 0x80000000u) ? u + 1u : u - 1u);
 }
 
 }  // namespace tms

@@ -4,26 +4,34 @@
 // 16K ids; workgroup (b, c) streams its chunk from HBM once with 16-byte
 // loads into registers (64 values per thread), applies the grammar mask and
 // the history penalties there, and reduces the chunk to a short sorted
-// candidate list in the workspace.  The last workgroup of the row to arrive
-// (a per-row counter) merges the S lists and runs the sequential fp64 tail
-// of tmsample::sample (tensormark/tmsample.h:184-199): softmax over the
-// top-k, top-p and min-p cuts, and the inverse-CDF draw.
+// candidate list.  The last workgroup of the row to finish its stream merges
+// the S lists and runs the sequential fp64 tail of tmsample::sample
+// (tensormark/tmsample.h:184-199): softmax over the top-k, top-p and min-p
+// cuts, and the inverse-CDF draw.
 //
 // Row modes (uniform per workgroup):
 //   greedy  the chunk's best (value, lowest id); the merge takes the best.
 //   top-k   K <= kTopkFast: the chunk's exact top-K by (v / T desc, id asc).
-//           A threshold from the per-thread maxima bounds the candidates,
-//           so only they are divided by T.  An exact radix select over the
-//           chunk (re-read from L2) is the fallback when it admits too many.
+//           The K-th largest of the 256 thread maxima bounds the candidates
+//           (about K of them), so only they are divided by T.  An exact
+//           radix select over the chunk (re-read from L2) is the fallback
+//           when the bound admits too many.
 //   top-p   K > kTopkFast (top_k = 0 or large): every chunk entry whose
 //           probability can change the fp64 sums, i.e. v / T within 40 of
 //           the chunk maximum (exp(-40) < 2^-57); rows with more than the
 //           capacity report TMS_ROW_UNSUPPORTED.
 //
-// Cross-workgroup traffic (lists, counts, the arrival counter) uses relaxed
-// agent-scope atomics, which are coherent across the XCDs' L2 caches, with
-// the stores drained (s_waitcnt) before the arrival is counted; no L2
-// write-back or invalidate is needed.
+// Timeline of a workgroup: the stream's loads are the kernel's first
+// instructions and are issued unconditionally (clamped addresses, an all-ones
+// mask row when the caller gives none), so each slot is processed as it
+// lands; the history penalties are applied in a second pass once the window
+// counts are in LDS.  The workgroup then takes a ticket from the row's
+// arrival counter and selects its candidates while the ticket's atomic is in
+// flight.  The last ticket holder merges; the others publish their list and
+// set a ready bit in its header.  All cross-workgroup words are relaxed
+// agent-scope atomics, coherent across the XCDs' L2 caches, with stores
+// drained (s_waitcnt) before the header that announces them; the merger's
+// wait for the headers is bounded.
 
 #include <float.h>
 #include <hip/hip_runtime.h>
@@ -38,9 +46,13 @@ constexpr int kEpt = 64;                   // logits per thread held in register
 constexpr int kChunk = kBlock * kEpt;      // ids per workgroup
 constexpr int kTopkFast = 128;             // largest K on the threshold path
 constexpr int kCand = 512;                 // chunk candidates held in LDS
-constexpr int kMergeCap = 1024;            // candidates per merge round
+constexpr int kListStride = kCand + 2;     // u64 per published list: header + entries
+constexpr int kUni = 2048;                 // merge staging (u64)
+constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
+constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
+constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per list
 
 enum : int { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_TOPP = 2 };
 enum : int { FLAG_NONFINITE = 1, FLAG_OVERFLOW = 2 };
@@ -51,13 +63,12 @@ struct KArgs {
     int V;
     int S;            // chunks per row
     int CE;           // ids per chunk (multiple of the vector width)
-    int aligned;      // rows start on 16-byte boundaries
     const tms_row_params* params;
     const int32_t* recent;
     const int32_t* n_recent;
     int64_t recent_stride;
-    const uint32_t* mask;
-    int64_t mask_stride;
+    const uint32_t* mask;     // never null: an all-ones row when the caller has none
+    int64_t mask_stride;      // 0 with the all-ones row
     const uint32_t* draws;
     int32_t* out_tokens;
     int32_t* out_status;
@@ -66,10 +77,8 @@ struct KArgs {
     float* out_topk_probs;
     int topk_cap;
     // workspace
-    uint32_t* counters;    // [B] arrival counters, self-resetting
-    int32_t* chunk_n;      // [B][S] entries per chunk list
-    int32_t* chunk_flags;  // [B][S]
-    uint64_t* lists;       // [B][S][kCand]
+    uint32_t* counters;    // [B] arrival tickets, reset by the merger
+    uint64_t* lists;       // [B][S][kListStride]: header, entries; headers reset by the merger
 };
 
 struct Bf16 {
@@ -148,21 +157,24 @@ struct Smem {
     union {
         uint32_t cnt[kChunk / 2];
         struct {
-            uint64_t uni[kMergeCap];      // the round's lists; then pr[] of the tail
-            uint64_t sorted[kMergeCap];
-            double q[kMergeCap];
+            uint64_t uni[kUni];    // the lists of a merge round; pr[] of the top-p tail
+            uint64_t surv[kUni];   // the merged, sorted entries; q[] of the top-p tail
         } m;
     } big;
     uint64_t cand[kCand];
+    uint32_t tkey[kBlock];         // order keys of the thread maxima
     int wave_i[kWaves];
-    float wave_f[kWaves];
     uint64_t wave_k[kWaves];
+    float wave_f[kWaves];
     int list_off[kMaxChunks + 2];
     int list_src[kMaxChunks + 1];
-    int list_n[kMaxChunks];
+    int list_n[kMaxChunks];        // entries of each chunk list
+    int list_s[kMaxChunks];        // survivors of each chunk list
     int hist[256];
     int ncand;
+    int nvalid;
     int misc[8];
+    uint64_t theta;
 };
 
 __device__ __forceinline__ int block_excl_scan(int v, int& total, Smem& sm) {
@@ -182,49 +194,23 @@ __device__ __forceinline__ int block_excl_scan(int v, int& total, Smem& sm) {
     return base + inc - v;
 }
 
-__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Smem& sm) {
-    v = wave_max_u64(v);
-    if ((threadIdx.x & 63) == 0) sm.wave_k[threadIdx.x >> 6] = v;
-    __syncthreads();
-    uint64_t r = sm.wave_k[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; ++i) r = sm.wave_k[i] > r ? sm.wave_k[i] : r;
-    __syncthreads();
-    return r;
-}
-
-__device__ __forceinline__ float block_max_f32(float v, Smem& sm) {
-    v = wave_max_f32(v);
-    if ((threadIdx.x & 63) == 0) sm.wave_f[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = sm.wave_f[0];
-#pragma unroll
-    for (int i = 1; i < kWaves; ++i) r = fmaxf(r, sm.wave_f[i]);
-    __syncthreads();
-    return r;
-}
-
-__device__ __forceinline__ int block_or(int v, Smem& sm) {
-    const bool any = __any(v != 0);
-    if ((threadIdx.x & 63) == 0) sm.wave_i[threadIdx.x >> 6] = any ? 1 : 0;
-    __syncthreads();
-    int r = 0;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) r |= sm.wave_i[i];
-    __syncthreads();
-    return r;
-}
-
-// Sort sm.cand[0..n) descending in place (n <= kCand): one wave's bitonic
-// network for n <= 64, ranking by counting otherwise.
+// Sort sm.cand[0..n) descending in place (n <= kCand) by ranking: each key's
+// rank is the number of larger keys, counted with broadcast LDS reads.
 __device__ void sort_cand(int n, Smem& sm) {
     const int t = threadIdx.x;
     if (n <= 1) return;
     if (n <= 64) {
+        // One wave; its LDS operations complete in order, so the reads of
+        // the loop finish before the scatter.
         if (t < 64) {
-            uint64_t k = t < n ? sm.cand[t] : 0ull;
-            k = wave_sort_desc_u64(k);
-            if (t < n) sm.cand[t] = k;
+            const uint64_t mine = t < n ? sm.cand[t] : 0ull;
+            int rank = 0;
+#pragma unroll 8
+            for (int j = 0; j < n; ++j) rank += sm.cand[j] > mine ? 1 : 0;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (t < n) sm.cand[rank] = mine;
         }
         __syncthreads();
         return;
@@ -239,7 +225,7 @@ __device__ void sort_cand(int n, Smem& sm) {
         rank[r] = 0;
     }
     if (n <= kBlock) {
-#pragma unroll 4
+#pragma unroll 8
         for (int j = 0; j < n; ++j) rank[0] += sm.cand[j] > mine[0] ? 1 : 0;
     } else {
 #pragma unroll 4
@@ -262,7 +248,7 @@ template <typename T>
 __device__ float slow_value(const T* base, const uint32_t* mrow, int id, int e0, const Pen& pn,
                             const Smem& sm) {
     float v = Elt<T>::scalar(base + id);
-    if (mrow && !((mrow[id >> 5] >> (id & 31)) & 1u)) return -__builtin_huge_valf();
+    if (!((mrow[id >> 5] >> (id & 31)) & 1u)) return -__builtin_huge_valf();
     if (pn.on) {
         const int off = id - e0;
         const uint32_t c = (sm.big.cnt[off >> 1] >> ((off & 1) * 16)) & 0xFFFFu;
@@ -393,433 +379,138 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
-    constexpr int VEC = Elt<T>::kVec;
-    constexpr int NVT = kEpt / VEC;
-    __shared__ Smem sm;
-    const float NEG_INF = -__builtin_huge_valf();
-    const int t = threadIdx.x;
-    const int lane = t & 63, wv = t >> 6;
-    const int S = a.S;
-    const int row = blockIdx.x / S;
-    const int c = blockIdx.x - row * S;
-    const int V = a.V;
-    const tms_row_params P = a.params[row];
-
-    const bool greedy = P.greedy != 0;
-    const bool bad_params = !greedy && !(P.temperature > 0.0f && P.temperature <= FLT_MAX);
-    const int K = greedy ? 1 : ((P.top_k <= 0 || P.top_k > V) ? V : P.top_k);
-    const int mode = greedy ? MODE_GREEDY : (K <= kTopkFast ? MODE_TOPK : MODE_TOPP);
-    const float temp = P.temperature;
-    const bool divide = !greedy && temp != 1.0f;
-
-    // ---- history window: its ids are loaded before the logits so that the
-    //      wait for them does not also wait for the logits.
-    int nrec = 0;
-    if (a.recent) {
-        nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
-        if (nrec > (int)a.recent_stride) nrec = (int)a.recent_stride;
+__device__ __forceinline__ void row_uniform(const KArgs& a, int row, const tms_row_params& P,
+                                            uint32_t& w0, uint32_t& w1) {
+    if (a.draws) {
+        w0 = a.draws[2 * row];
+        w1 = a.draws[2 * row + 1];
+    } else {
+        row_words(P.seed, P.offset, 0u, w0, w1);
     }
-    Pen pn;
-    pn.rep_on = !(P.repeat_penalty <= 1.0f);
-    pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
-    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
-    pn.rep = P.repeat_penalty;
-    pn.freq = P.frequency_penalty;
-    pn.pres = P.presence_penalty;
-    const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
-    const int e0 = c * a.CE;
-    const int e1 = min(e0 + a.CE, V);
-    const int nvec = (e1 - e0 + VEC - 1) / VEC;
-    const int32_t* hist = pn.on ? a.recent + (int64_t)row * a.recent_stride : nullptr;
-    constexpr int kWin = 4;   // window ids per thread per pass
-    int wid[kWin];
-#pragma unroll
-    for (int i = 0; i < kWin; ++i) {
-        const int p = from + t + i * kBlock;
-        wid[i] = (pn.on && p < nrec) ? hist[p] : -1;
-    }
+}
 
-    // ---- stream the chunk: one mask word and one 16-byte vector per slot.
-    const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
-    const uint32_t* mrow = a.mask ? a.mask + (int64_t)row * a.mask_stride : nullptr;
-    uint4 raw[NVT];
-    uint32_t mw[NVT];
-#pragma unroll
-    for (int j = 0; j < NVT; ++j) {
-        const int v = t + j * kBlock;
-        const int eb = e0 + v * VEC;
-        mw[j] = 0xFFFFFFFFu;
-        raw[j] = make_uint4(0, 0, 0, 0);
-        if (v < nvec) {
-            if (mrow) mw[j] = mrow[eb >> 5];
-            if (a.aligned && eb + VEC <= e1) raw[j] = *(const uint4*)(base + eb);
+// Count of keys > k in the descending list L[0..n), n < P (P a power of
+// two): a fixed number of halving steps, so searches in several lists can
+// proceed in lock step.
+__device__ __forceinline__ int count_gt_fixed(const uint64_t* L, int n, uint64_t k, int P) {
+    int lo = 0;
+    for (int step = P >> 1; step >= 1; step >>= 1) {
+        const int nx = lo + step;
+        const bool in = nx <= n;
+        const uint64_t v = L[in ? nx - 1 : 0];
+        lo = (in && v > k) ? nx : lo;
+    }
+    return lo;
+}
+
+// The sequential fp64 tail for top-k rows: n = K <= 128 sorted entries in
+// `srt`, run by one wave.  pr, q and p live in LDS so every lane walks them
+// in order (broadcast reads) and forms each sum exactly as tmsample::sample
+// forms it, one dependent fp64 add per step; lane i & 63 keeps the partial
+// sum at step i in a register.  The partial sums only grow (the terms are
+// >= 0), so the top-p cut and the drawn index are counts of partial sums
+// below the threshold.
+__device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
+                          int n, int K, double* pr, double* q, double* /*unused*/) {
+    const int lane = threadIdx.x & 63;
+    uint32_t w0, w1;
+    row_uniform(a, row, P, w0, w1);   // independent of the sums: overlaps them
+    const double u = canonical(w0, w1);
+    const double mx = (double)ckey_val(srt[0]);
+    const bool h0 = lane < n, h1 = lane + 64 < n;
+    const double pr0 = h0 ? exp((double)ckey_val(srt[lane]) - mx) : 0.0;
+    const double pr1 = h1 ? exp((double)ckey_val(srt[lane + 64]) - mx) : 0.0;
+    if (h0) pr[lane] = pr0;
+    if (h1) pr[lane + 64] = pr1;
+    wave_lds_sync();
+    double z = 0, zc0 = 0, zc1 = 0;                 // tmsample.h:186-191
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) {
+        z += pr[i];
+        zc0 = lane == i ? z : zc0;
+        zc1 = lane + 64 == i ? z : zc1;
+    }
+    const double q0 = pr0 / z, q1 = pr1 / z;
+    if (h0) q[lane] = q0;
+    if (h1) q[lane + 64] = q1;
+    wave_lds_sync();
+    double cc0 = 0, cc1 = 0;
+    {
+        double cum = 0;                             // tmsample.h:192-197
+#pragma unroll 8
+        for (int i = 0; i < n; ++i) {
+            cum += q[i];
+            cc0 = lane == i ? cum : cc0;
+            cc1 = lane + 64 == i ? cum : cc1;
         }
     }
-
-    // ---- window counts: 16 bits per chunk id in LDS.
-    if (t == 0) sm.ncand = 0;
-    if (pn.on) {
-        uint4* c4 = (uint4*)sm.big.cnt;
-        for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
-        __syncthreads();
-        for (int p0 = from; p0 < nrec; p0 += kBlock * kWin) {
-#pragma unroll
-            for (int i = 0; i < kWin; ++i) {
-                int id;
-                if (p0 == from) {
-                    id = wid[i];
-                } else {
-                    const int p = p0 + t + i * kBlock;
-                    id = p < nrec ? hist[p] : -1;
-                }
-                if (id >= e0 && id < e1) {
-                    const int off = id - e0;
-                    atomicAdd(&sm.big.cnt[off >> 1], 1u << ((off & 1) * 16));
-                }
-            }
-        }
-        __syncthreads();
+    const double tp = (double)P.top_p;
+    const int below = __popcll(__ballot(h0 && cc0 < tp)) + __popcll(__ballot(h1 && cc1 < tp));
+    int kp = below + 1 < K ? below + 1 : K;   // keep = first index with cum >= top_p, + 1
+    if (!(P.top_p == P.top_p)) kp = K;        // NaN: cum >= top_p never holds
+    if (P.min_p > 0.0f) {
+        // min-p: the first entry below min_p ends the kept prefix.
+        const double mp = (double)P.min_p;
+        const uint64_t b0 = __ballot(lane >= 1 && h0 && pr0 < mp);
+        const uint64_t b1 = __ballot(h1 && pr1 < mp);
+        const int m = b0 ? __ffsll((unsigned long long)b0) - 1
+                         : (b1 ? 64 + __ffsll((unsigned long long)b1) - 1 : K);
+        if (m < kp) kp = m;
     }
-
-    // ---- per vector: widen, mask, penalties, checks, thread maximum.
-    float x[kEpt];
-    int nonfinite = 0;
-    float tmax = NEG_INF;
-#pragma unroll
-    for (int j = 0; j < NVT; ++j) {
-        const int v = t + j * kBlock;
-        const int eb = e0 + v * VEC;
-        float f[VEC];
-        if (a.aligned && eb + VEC <= e1) {
-            Elt<T>::widen(raw[j], f);
-        } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e)
-                f[e] = (v < nvec && eb + e < e1) ? Elt<T>::scalar(base + eb + e) : NEG_INF;
+    const int keep = kp;
+    int tokidx = 0;
+    if (keep >= 2) {
+        // std::discrete_distribution over pr[0..keep): sum = accumulate() =
+        // the z prefix at keep - 1, p = pr / sum, partial sums with the last
+        // forced to 1, lower_bound(u) = #(cp_j < u) over j < keep - 1.
+        const double sum = readlane_f64(keep - 1 < 64 ? zc0 : zc1, (keep - 1) & 63);
+        const double p0 = pr0 / sum, p1 = pr1 / sum;
+        wave_lds_sync();
+        if (h0) q[lane] = p0;
+        if (h1) q[lane + 64] = p1;
+        wave_lds_sync();
+        double c0 = 0, c1 = 0, cp = 0;
+#pragma unroll 8
+        for (int i = 0; i < keep - 1; ++i) {
+            cp += q[i];
+            c0 = lane == i ? cp : c0;
+            c1 = lane + 64 == i ? cp : c1;
         }
-        const uint32_t mb = mw[j] >> (eb & 31);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) f[e] = ((mb >> e) & 1u) ? f[e] : NEG_INF;
-        if (pn.on && v < nvec) {
-            uint32_t cw[VEC / 2];
-            uint32_t any = 0;
-#pragma unroll
-            for (int i = 0; i < VEC / 2; ++i) {
-                cw[i] = sm.big.cnt[((eb - e0) >> 1) + i];
-                any |= cw[i];
-            }
-            if (any) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const uint32_t cnt = (cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-                    if (cnt) f[e] = apply_pen(f[e], cnt, pn);
-                }
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            nonfinite |= (f[e] != f[e]) | (f[e] == __builtin_huge_valf());
-            tmax = fmaxf(tmax, f[e]);
-            x[j * VEC + e] = f[e];
+        tokidx = __popcll(__ballot(lane < keep - 1 && c0 < u)) +
+                 __popcll(__ballot(lane + 64 < keep - 1 && c1 < u));
+    }
+    if (lane == 0) {
+        a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
+        a.out_status[row] = TMS_ROW_OK;
+        if (a.out_keep) a.out_keep[row] = keep;
+    }
+    if (a.topk_cap) {
+        int32_t* ids = a.out_topk_ids ? a.out_topk_ids + (int64_t)row * a.topk_cap : nullptr;
+        float* probs = a.out_topk_probs ? a.out_topk_probs + (int64_t)row * a.topk_cap : nullptr;
+        for (int i = lane; i < a.topk_cap; i += 64) {
+            const bool have = i < n;
+            const double qq = i < 64 ? q0 : q1;
+            if (ids) ids[i] = have ? (int)ckey_id(srt[i]) : -1;
+            if (probs) probs[i] = have ? (float)qq : 0.0f;
         }
     }
-    const int flags_nf = block_or(nonfinite, sm) ? FLAG_NONFINITE : 0;
-    int flags = flags_nf;
-    int nout = 0;   // entries of sm.cand this chunk publishes
+}
 
-    if (!bad_params && !flags_nf) {
-        if (mode == MODE_GREEDY) {
-            uint64_t gb = 0;
-#pragma unroll
-            for (int j = 0; j < NVT; ++j) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float f = x[j * VEC + e];
-                    const uint64_t k =
-                        f != NEG_INF ? ckey(f, (uint32_t)(e0 + (t + j * kBlock) * VEC + e)) : 0ull;
-                    gb = k > gb ? k : gb;
-                }
-            }
-            const uint64_t b = block_max_u64(gb, sm);
-            if (t == 0 && b) sm.cand[0] = b;
-            nout = b ? 1 : 0;
-            __syncthreads();
-        } else if (mode == MODE_TOPK) {
-            // tau: at least K chunk entries are >= tau.  Each wave sorts its 64
-            // thread maxima; its ceil(K/4)-th is >= tau for 4 * ceil(K/4) >= K
-            // threads, each holding an entry >= tau.
-            const int kw = (K + kWaves - 1) / kWaves;
-            const float srt = wave_sort_desc_f32(tmax);
-            const float tw = __shfl(srt, kw - 1, 64);
-            if (lane == 0) sm.wave_f[wv] = tw;
-            __syncthreads();
-            float tau = sm.wave_f[0];
-#pragma unroll
-            for (int i = 1; i < kWaves; ++i) tau = fminf(tau, sm.wave_f[i]);
-            // Division can merge neighbouring values: lower tau to the smallest
-            // float with the same quotient, so every entry tying the K-th
-            // quotient is a candidate.
-            bool fallback = false;
-            if (divide && tau != NEG_INF) {
-                const float q = tau / temp;
-                int it = 0;
-                for (; it < 64; ++it) {
-                    const float p = nextafterf(tau, NEG_INF);
-                    if (p / temp == q) tau = p;
-                    else break;
-                }
-                fallback = it == 64;
-            }
-            if (!fallback) {
-#pragma unroll
-                for (int j = 0; j < NVT; ++j) {
-                    float vm = x[j * VEC];
-#pragma unroll
-                    for (int e = 1; e < VEC; ++e) vm = fmaxf(vm, x[j * VEC + e]);
-                    if (vm != NEG_INF && vm >= tau) {
-#pragma unroll
-                        for (int e = 0; e < VEC; ++e) {
-                            const float f = x[j * VEC + e];
-                            if (f != NEG_INF && f >= tau) {
-                                const int pos = atomicAdd(&sm.ncand, 1);
-                                if (pos < kCand)
-                                    sm.cand[pos] = ckey(divide ? f / temp : f,
-                                                        (uint32_t)(e0 + (t + j * kBlock) * VEC + e));
-                            }
-                        }
-                    }
-                }
-            }
-            __syncthreads();
-            const int n = sm.ncand;
-            __syncthreads();
-            if (fallback || n > kCand) {
-                nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn, sm);
-                sort_cand(nout, sm);
-            } else {
-                sort_cand(n, sm);
-                nout = n < K ? n : K;
-            }
-        } else {
-            // Top-p only: entries within kSigSpan of the chunk maximum (in v / T).
-            const float cmax = block_max_f32(tmax, sm);
-            if (cmax != NEG_INF) {
-                const float lmax = divide ? cmax / temp : cmax;
-                const double lthr = (double)lmax - (double)kSigSpan;
-                // Generous prefilter in v, exact test on the quotient.
-                const float vthr = __double2float_rd(
-                    ((double)lmax - (double)kSigSpan - 1.0 - fabs((double)lmax) * 0x1p-20) *
-                    (double)temp);
-#pragma unroll
-                for (int j = 0; j < NVT; ++j) {
-                    float vm = x[j * VEC];
-#pragma unroll
-                    for (int e = 1; e < VEC; ++e) vm = fmaxf(vm, x[j * VEC + e]);
-                    if (vm != NEG_INF && vm >= vthr) {
-#pragma unroll
-                        for (int e = 0; e < VEC; ++e) {
-                            const float f = x[j * VEC + e];
-                            if (f != NEG_INF && f >= vthr) {
-                                const float lg = divide ? f / temp : f;
-                                if ((double)lg >= lthr) {
-                                    const int pos = atomicAdd(&sm.ncand, 1);
-                                    if (pos < kCand)
-                                        sm.cand[pos] =
-                                            ckey(lg, (uint32_t)(e0 + (t + j * kBlock) * VEC + e));
-                                }
-                            }
-                        }
-                    }
-                }
-                __syncthreads();
-                const int n = sm.ncand;
-                __syncthreads();
-                if (n > kCand) {
-                    flags |= FLAG_OVERFLOW;
-                    nout = 0;
-                } else {
-                    sort_cand(n, sm);
-                    nout = n;
-                }
-            }
-        }
-    }
-
-    // ---- publish the chunk list (wave 0), then count the row's arrivals.
-    if (wv == 0) {
-        uint64_t* my_list = a.lists + ((int64_t)row * S + c) * kCand;
-        for (int i = lane; i < nout; i += 64) st_agent(&my_list[i], sm.cand[i]);
-        if (lane == 0) {
-            st_agent(&a.chunk_n[row * S + c], (int32_t)nout);
-            st_agent(&a.chunk_flags[row * S + c], (int32_t)flags);
-        }
-        __builtin_amdgcn_s_waitcnt(0);   // the stores above are complete
-        if (lane == 0) {
-            const uint32_t prev =
-                __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            sm.misc[0] = prev == (uint32_t)(S - 1) ? 1 : 0;
-        }
-    }
-    __syncthreads();
-    if (!sm.misc[0]) return;
-
-    // ================= merge: the last workgroup of the row =================
-    int any_flags = 0;
-    if (t < S) {
-        sm.list_n[t] = ld_agent(&a.chunk_n[row * S + t]);
-        any_flags = ld_agent(&a.chunk_flags[row * S + t]);
-    }
-    if (t == 0) st_agent(&a.counters[row], 0u);   // ready for the next launch
-    const int fl = block_or(any_flags & FLAG_NONFINITE, sm);
-    const int ov = block_or(any_flags & FLAG_OVERFLOW, sm);
-    if (t == 0) {
-        int tot = 0;
-        for (int i = 0; i < S; ++i) tot += sm.list_n[i];
-        sm.misc[5] = tot;
-    }
-    __syncthreads();
-    const int N = sm.misc[5];   // finite candidates over all chunk lists
-
-    int status = TMS_ROW_OK;
-    if (bad_params) status = TMS_ROW_BAD_PARAMS;
-    else if (fl) status = TMS_ROW_NONFINITE;
-    else if (ov || (mode == MODE_TOPP && N > kMergeCap)) status = TMS_ROW_UNSUPPORTED;
-    else if (N == 0) status = TMS_ROW_ALL_MASKED;
-    if (status != TMS_ROW_OK) {
-        write_row_error(a, row, status);
-        return;
-    }
-
-    // Merge in rounds: the running top list (sorted[0..n_acc)) plus as many
-    // chunk lists as fit in kMergeCap; every entry is ranked against the
-    // other lists of the round by binary search.  Top-k rows keep the best
-    // K after each round (K + one list always fits); top-p rows have
-    // N <= kMergeCap and finish in one round.
-    const uint64_t* row_lists = a.lists + (int64_t)row * S * kCand;
-    const int keep_cap = mode == MODE_TOPP ? kMergeCap : K;
-    int n_acc = 0;
-    int c_next = 0;
-    while (c_next < S) {
-        if (t == 0) {
-            int off = n_acc, g = 1, cc = c_next;
-            sm.list_off[0] = 0;
-            sm.list_off[1] = n_acc;
-            sm.list_src[0] = -1;
-            while (cc < S && off + sm.list_n[cc] <= kMergeCap) {
-                off += sm.list_n[cc];
-                sm.list_src[g] = cc;
-                sm.list_off[++g] = off;
-                ++cc;
-            }
-            sm.misc[6] = g;
-            sm.misc[7] = cc;
-        }
-        __syncthreads();
-        const int ng = sm.misc[6];
-        const int total = sm.list_off[ng];
-        for (int i = t; i < total; i += kBlock) {
-            int lc = 0;
-            while (sm.list_off[lc + 1] <= i) ++lc;
-            const int src = sm.list_src[lc];
-            sm.big.m.uni[i] =
-                src < 0 ? sm.big.m.sorted[i]
-                        : ld_agent(&row_lists[(int64_t)src * kCand + (i - sm.list_off[lc])]);
-        }
-        __syncthreads();
-        const int nkeep = total < keep_cap ? total : keep_cap;
-        for (int i = t; i < total; i += kBlock) {
-            int lc = 0;
-            while (sm.list_off[lc + 1] <= i) ++lc;
-            const uint64_t k = sm.big.m.uni[i];
-            int rank = i - sm.list_off[lc];
-            for (int o = 0; o < ng; ++o) {
-                if (o == lc) continue;
-                rank += count_greater(sm.big.m.uni + sm.list_off[o],
-                                      sm.list_off[o + 1] - sm.list_off[o], k);
-            }
-            if (rank < nkeep) sm.big.m.sorted[rank] = k;
-        }
-        c_next = sm.misc[7];
-        n_acc = nkeep;
-        __syncthreads();
-    }
-
-    int32_t* topk_ids = a.out_topk_ids ? a.out_topk_ids + (int64_t)row * a.topk_cap : nullptr;
-    float* topk_probs = a.out_topk_probs ? a.out_topk_probs + (int64_t)row * a.topk_cap : nullptr;
-    const uint64_t* srt = sm.big.m.sorted;
-
-    if (mode == MODE_GREEDY) {
-        const int tok = (int)ckey_id(srt[0]);
-        if (t == 0) {
-            a.out_tokens[row] = tok;
-            a.out_status[row] = TMS_ROW_OK;
-            if (a.out_keep) a.out_keep[row] = 0;
-        }
-        for (int i = t; i < a.topk_cap; i += kBlock) {
-            if (topk_ids) topk_ids[i] = i == 0 ? tok : -1;
-            if (topk_probs) topk_probs[i] = i == 0 ? 1.0f : 0.0f;
-        }
-        return;
-    }
-
-    // Entries the tail walks.  Top-k rows with fewer than K finite ids go on
-    // with -inf entries in ascending id order: the ids missing from the
-    // finite set, which is then complete.
-    int n = n_acc;
-    if (mode == MODE_TOPK && N < K) {
-        // ids in [0, K + N) absent from the N finite ones, lowest first
-        // (K + N < 2 * kTopkFast <= kBlock: one id per thread).
-        const int q = t;
-        int member = 0;
-        if (q < K + N)
-            for (int i = 0; i < N; ++i) member |= (int)ckey_id(srt[i]) == q;
-        const int gap = (q < K + N && !member && q < V) ? 1 : 0;
-        int tot;
-        const int p = block_excl_scan(gap, tot, sm);
-        if (gap && p < K - N) sm.big.m.sorted[N + p] = ckey(NEG_INF, (uint32_t)q);
-        __syncthreads();
-        n = K;
-    }
-    const float mx = ckey_val(srt[0]);
-    if (mx == __builtin_huge_valf()) {
-        write_row_error(a, row, TMS_ROW_NONFINITE);
-        return;
-    }
-    // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
-    if (mode == MODE_TOPP) {
-        int sig = 0;
-        for (int i = t; i < n; i += kBlock)
-            sig += ((double)ckey_val(srt[i]) - (double)mx >= -(double)kSigSpan) ? 1 : 0;
-        sig = wave_sum_i32(sig);
-        if (lane == 0) sm.wave_i[wv] = sig;
-        __syncthreads();
-        n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
-        __syncthreads();
-    }
-
-    // pr[i] = exp(lg_i - mx) in fp64 (tmsample.h:188-189).
-    double* pr = (double*)sm.big.m.uni;   // the round's lists are no longer needed
-    double* q = sm.big.m.q;
-    for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
-    __syncthreads();
-    if (wv != 0) return;
-
-    // The sequential fp64 tail runs in wave 0; every lane walks the same
-    // LDS entries (broadcast reads), so the sums are formed in the
-    // reference's order.
+// The same tail for top-p rows (n <= kToppCap entries in LDS, exact prefix
+// only), one wave reading the entries from LDS in order.
+__device__ void tail_topp(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
+                          int n, int K, double* pr, double* q) {
+    const int lane = threadIdx.x & 63;
     double z = 0;
 #pragma unroll 8
-    for (int i = 0; i < n; ++i) z += pr[i];               // tmsample.h:186-191
+    for (int i = 0; i < n; ++i) z += pr[i];
     for (int i = lane; i < n; i += 64) q[i] = pr[i] / z;
     wave_lds_sync();
     int kp = K;
     {
         double cum = 0;
         const double tp = (double)P.top_p;
-        for (int i = 0; i < n; ++i) {                       // tmsample.h:192-197
+        for (int i = 0; i < n; ++i) {
             cum += q[i];
             if (cum >= tp) {
                 kp = i + 1;
@@ -838,8 +529,6 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     const int lim = keep < n ? keep : n;
     int tokidx = 0;
     if (keep >= 2) {
-        // std::discrete_distribution over pr[0..keep): sum, normalise,
-        // partial sums with the last forced to 1, lower_bound(u).
         double sum = 0;
 #pragma unroll 8
         for (int i = 0; i < lim; ++i) sum += pr[i];
@@ -847,12 +536,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         for (int i = lane; i < lim; i += 64) q[i] = pr[i] / sum;
         wave_lds_sync();
         uint32_t w0, w1;
-        if (a.draws) {
-            w0 = a.draws[2 * row];
-            w1 = a.draws[2 * row + 1];
-        } else {
-            row_words(P.seed, P.offset, 0u, w0, w1);
-        }
+        row_uniform(a, row, P, w0, w1);
         const double u = canonical(w0, w1);
         double cp = 0;
         tokidx = keep - 1;
@@ -865,20 +549,662 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             }
         }
     }
-    // tokidx >= n only on top-p rows whose draw fell past the last entry that
-    // moves the sums: the reference then returns its K-th entry, which this
-    // row does not hold.
+    // tokidx >= n: the draw fell past the last entry that moves the sums, so
+    // the reference would return its K-th entry, which this row does not hold.
     const bool lost = tokidx >= n;
     if (lane == 0) {
         a.out_tokens[row] = lost ? -1 : (int)ckey_id(srt[tokidx]);
         a.out_status[row] = lost ? TMS_ROW_UNSUPPORTED : TMS_ROW_OK;
         if (a.out_keep) a.out_keep[row] = keep;
     }
+    int32_t* ids = a.out_topk_ids ? a.out_topk_ids + (int64_t)row * a.topk_cap : nullptr;
+    float* probs = a.out_topk_probs ? a.out_topk_probs + (int64_t)row * a.topk_cap : nullptr;
     for (int i = lane; i < a.topk_cap; i += 64) {
         const bool have = i < n;
-        if (topk_ids) topk_ids[i] = have ? (int)ckey_id(srt[i]) : -1;
-        if (topk_probs) topk_probs[i] = have ? (float)(pr[i] / z) : 0.0f;
+        if (ids) ids[i] = have ? (int)ckey_id(srt[i]) : -1;
+        if (probs) probs[i] = have ? (float)(pr[i] / z) : 0.0f;
     }
+}
+
+template <typename T, bool FAST>
+__global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
+    constexpr int VEC = Elt<T>::kVec;
+    constexpr int NVT = kEpt / VEC;
+    __shared__ Smem sm;
+    const float NEG_INF = -__builtin_huge_valf();
+    const int t = threadIdx.x;
+    const int lane = t & 63, wv = t >> 6;
+    const int S = a.S;
+    const int row = blockIdx.x / S;
+    const int c = blockIdx.x - row * S;
+    const int V = a.V;
+    const int e0 = c * a.CE;
+    const int e1 = min(e0 + a.CE, V);
+    const int nvec = (e1 - e0 + VEC - 1) / VEC;
+
+    // ---- history ids first (the row's first 4 * kBlock; positions are
+    //      checked against the window once the parameters are in), then the
+    //      stream: one mask word and one 16-byte vector per slot, every slot
+    //      loaded (clamped to the chunk's last vector), in slot order.
+    constexpr int kWin = 4;   // history ids per thread per pass
+    const int32_t* hist = a.recent + (int64_t)row * a.recent_stride;
+    int wid[kWin];
+    if (a.recent) {
+        const int rs = (int)a.recent_stride;
+#pragma unroll
+        for (int i = 0; i < kWin; ++i) wid[i] = hist[min(t + i * kBlock, rs - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
+    const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
+    uint4 raw[NVT];
+    uint32_t mw[NVT];
+    float sx[FAST ? 1 : kEpt];
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+        const int v = min(t + j * kBlock, nvec - 1);
+        const int eb = e0 + v * VEC;
+        mw[j] = mrow[eb >> 5];
+        if constexpr (FAST) {
+            raw[j] = *(const uint4*)(base + eb);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) sx[j * VEC + e] = Elt<T>::scalar(base + min(eb + e, V - 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    const tms_row_params P = a.params[row];
+
+    // ---- pass 1, as each slot lands: widen, mask, NaN/+inf check, slot max.
+    float x[kEpt];
+    float vmax[NVT];
+    int nonfinite = 0;
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+        const int v = t + j * kBlock;
+        const int eb = e0 + v * VEC;
+        float f[VEC];
+        if constexpr (FAST) {
+            Elt<T>::widen(raw[j], f);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) f[e] = sx[j * VEC + e];
+        }
+        const uint32_t mb = (v < nvec) ? (mw[j] >> (eb & 31)) : 0u;
+        float vm = NEG_INF;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            // bit e of mb, sign-extended, selects the value or -inf
+            const uint32_t sel = (uint32_t)((int)(mb << (31 - e)) >> 31);
+            uint32_t bits = (__float_as_uint(f[e]) & sel) | (0xFF800000u & ~sel);
+            if constexpr (!FAST) bits = (eb + e < e1) ? bits : 0xFF800000u;
+            const float g = __uint_as_float(bits);
+            nonfinite |= __builtin_amdgcn_class(g, 0x203);   // NaN or +inf
+            vm = fmaxf(vm, g);
+            x[j * VEC + e] = g;
+        }
+        vmax[j] = vm;
+    }
+
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- row parameters and history window (the parameters' load was issued
+    //      before pass 1 and is first waited for here).
+    const bool greedy = P.greedy != 0;
+    const bool bad_params = !greedy && !(P.temperature > 0.0f && P.temperature <= FLT_MAX);
+    const int K = greedy ? 1 : ((P.top_k <= 0 || P.top_k > V) ? V : P.top_k);
+    const int mode = greedy ? MODE_GREEDY : (K <= kTopkFast ? MODE_TOPK : MODE_TOPP);
+    const float temp = P.temperature;
+    const bool divide = !greedy && temp != 1.0f;
+    int nrec = 0;
+    if (a.recent) {
+        nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
+        if (nrec > (int)a.recent_stride) nrec = (int)a.recent_stride;
+    }
+    Pen pn;
+    pn.rep_on = !(P.repeat_penalty <= 1.0f);
+    pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
+    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
+    pn.rep = P.repeat_penalty;
+    pn.freq = P.frequency_penalty;
+    pn.pres = P.presence_penalty;
+    const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
+    if (pn.on) {
+        uint4* c4 = (uint4*)sm.big.cnt;
+        for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
+    }
+    if (t == 0) sm.ncand = 0;
+
+    // ---- pass 2: history penalties from the window counts.
+    if (pn.on) {
+        __syncthreads();   // counts cleared
+        // Positions [0, kWin * kBlock) came with the stream; later ones (long
+        // histories only) are read now.
+        for (int p0 = 0; p0 < nrec; p0 += kBlock * kWin) {
+#pragma unroll
+            for (int i = 0; i < kWin; ++i) {
+                const int p = p0 + t + i * kBlock;
+                const int id = (p < from || p >= nrec) ? -1 : (p0 == 0 ? wid[i] : hist[p]);
+                if (id >= e0 && id < e1) {
+                    const int off = id - e0;
+                    atomicAdd(&sm.big.cnt[off >> 1], 1u << ((off & 1) * 16));
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NVT; ++j) {
+            const int v = t + j * kBlock;
+            const int off = min(v * VEC, kChunk - VEC);
+            uint32_t cw[VEC / 2];
+            uint32_t any = 0;
+#pragma unroll
+            for (int i = 0; i < VEC / 2; ++i) {
+                cw[i] = sm.big.cnt[(off >> 1) + i];
+                any |= cw[i];
+            }
+            if (any && v < nvec) {
+                float vm = NEG_INF;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    const uint32_t cnt = (cw[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+                    float g = x[j * VEC + e];
+                    if (cnt) {
+                        g = apply_pen(g, cnt, pn);
+                        nonfinite |= __builtin_amdgcn_class(g, 0x203);
+                        x[j * VEC + e] = g;
+                    }
+                    vm = fmaxf(vm, g);
+                }
+                vmax[j] = vm;
+            }
+        }
+    }
+    float tmax = vmax[0];
+#pragma unroll
+    for (int j = 1; j < NVT; ++j) tmax = fmaxf(tmax, vmax[j]);
+
+    // ---- ticket: the row's last workgroup to get here merges.  The atomic's
+    //      result is first needed after the selection.
+    uint32_t ticket = 0;
+    if (t == 0)
+        ticket = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- selection: the chunk's candidates, sorted, into sm.cand[0..nout).
+    int flags = 0;
+    int nout = 0;
+    if (mode == MODE_GREEDY) {
+        uint64_t gb = 0;
+#pragma unroll
+        for (int j = 0; j < NVT; ++j) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                const float f = x[j * VEC + e];
+                const uint64_t k =
+                    f != NEG_INF ? ckey(f, (uint32_t)(e0 + (t + j * kBlock) * VEC + e)) : 0ull;
+                gb = k > gb ? k : gb;
+            }
+        }
+        gb = wave_max_u64_dpp(gb);
+        const bool nf = __any(nonfinite != 0);
+        if (lane == 0) {
+            sm.wave_k[wv] = gb;
+            sm.wave_i[wv] = nf;
+        }
+        __syncthreads();
+        uint64_t b = sm.wave_k[0];
+        int anynf = sm.wave_i[0];
+#pragma unroll
+        for (int i = 1; i < kWaves; ++i) {
+            b = sm.wave_k[i] > b ? sm.wave_k[i] : b;
+            anynf |= sm.wave_i[i];
+        }
+        if (anynf) flags |= FLAG_NONFINITE;
+        if (t == 0 && b) sm.cand[0] = b;
+        nout = (b && !anynf) ? 1 : 0;
+    } else {
+        // Threshold thr in v.  top-k: the K-th largest of the 256 thread
+        // maxima (K threads hold an entry >= it), found bit by bit on their
+        // order keys with ballots.  top-p: the chunk maximum less the
+        // significance span, generously, in v.
+        const bool nf = __any(nonfinite != 0);
+        sm.tkey[t] = okey(tmax);
+        if (lane == 0) sm.wave_i[wv] = nf;
+        __syncthreads();
+        int anynf = 0;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) anynf |= sm.wave_i[i];
+        if (anynf) flags |= FLAG_NONFINITE;
+        const uint4 k4 = ((const uint4*)sm.tkey)[lane];   // 4 keys per lane, all 256
+        float thr;
+        double lthr = 0.0;
+        bool fallback = false;
+        if (mode == MODE_TOPK) {
+            // Sixteen high bits suffice: `pre` stays a lower bound of the K-th
+            // key, and the few extra candidates it admits are ranked away.
+            uint32_t pre = 0;
+            for (int bit = 31; bit >= 16; --bit) {
+                const uint32_t cand = pre | (1u << bit);
+                const int cnt = __popcll(__ballot(k4.x >= cand)) + __popcll(__ballot(k4.y >= cand)) +
+                                __popcll(__ballot(k4.z >= cand)) + __popcll(__ballot(k4.w >= cand));
+                if (cnt >= K) pre = cand;
+            }
+            // Keys below okey(-FLT_MAX) decode to -inf or NaN: every finite entry.
+            thr = pre < 0x00800000u ? -FLT_MAX : okey_inv(pre);
+            // Division can merge neighbouring values: lower the threshold to
+            // the smallest float with the same quotient, so every entry tying
+            // the K-th quotient is a candidate.
+            if (divide && thr != NEG_INF) {
+                const float qt = thr / temp;
+                int it = 0;
+                for (; it < 64; ++it) {
+                    const float p = float_below(thr);
+                    if (p / temp == qt) thr = p;
+                    else break;
+                }
+                fallback = it == 64;
+            }
+            if (thr == NEG_INF) thr = -FLT_MAX;   // every finite entry
+        } else {
+            const uint32_t km = max(max(k4.x, k4.y), max(k4.z, k4.w));
+            uint32_t kmax = km;
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, m, 64));
+            const float cm = okey_inv(kmax);
+            const float lmax = divide ? cm / temp : cm;
+            lthr = (double)lmax - (double)kSigSpan;
+            thr = cm == NEG_INF ? __builtin_huge_valf()
+                                : __double2float_rd(((double)lmax - (double)kSigSpan - 1.0 -
+                                                     fabs((double)lmax) * 0x1p-20) *
+                                                    (double)temp);
+            if (thr == NEG_INF) thr = -FLT_MAX;
+        }
+        int n = 0;
+        if (!anynf && !bad_params && !fallback) {
+            // Each wave compacts its candidates with ballots into its own
+            // segment of cand (kCand / kWaves entries), as raw (value, id).
+            constexpr int kSeg = kCand / kWaves;
+            uint64_t* seg = sm.cand + wv * kSeg;
+            int wcnt = 0;
+#pragma unroll
+            for (int j = 0; j < NVT; ++j) {
+                if (__any(vmax[j] >= thr)) {
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) {
+                        const float f = x[j * VEC + e];
+                        const bool p = f >= thr;
+                        const uint64_t m = __ballot(p);
+                        if (m) {
+                            const int pos = wcnt + __builtin_amdgcn_mbcnt_hi(
+                                                       (uint32_t)(m >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                            if (p && pos < kSeg)
+                                seg[pos] = ((uint64_t)__float_as_uint(f) << 32) |
+                                           (uint32_t)(e0 + (t + j * kBlock) * VEC + e);
+                            wcnt += __popcll(m);
+                        }
+                    }
+                }
+            }
+            if (lane == 0) sm.wave_i[wv] = wcnt;
+            __syncthreads();
+            int cw[kWaves];
+            int over = 0;
+            n = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                cw[w] = sm.wave_i[w];
+                over |= cw[w] > kSeg;
+                n += cw[w];
+            }
+            if (over) {
+                // A wave's segment overflowed: compact again, contiguously.
+                if (t == 0) sm.ncand = 0;
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < NVT; ++j) {
+                    if (vmax[j] >= thr) {
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) {
+                            const float f = x[j * VEC + e];
+                            if (f >= thr) {
+                                const int pos = atomicAdd(&sm.ncand, 1);
+                                if (pos < kCand)
+                                    sm.cand[pos] = ((uint64_t)__float_as_uint(f) << 32) |
+                                                   (uint32_t)(e0 + (t + j * kBlock) * VEC + e);
+                            }
+                        }
+                    }
+                }
+                __syncthreads();
+                n = sm.ncand;
+                cw[0] = n;
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w) cw[w] = 0;
+            }
+            if (n <= kCand) {
+                // Dense pass (the window counts are dead now): divide the
+                // candidates, form their keys contiguously in uni; top-p drops
+                // those below the exact span (key 0 sorts last).  Then rank
+                // them by counting into cand.
+                uint64_t* keys = sm.big.m.uni;
+                int nv = 0;
+                for (int i = t; i < n; i += kBlock) {
+                    int w = 0, base_i = 0;
+#pragma unroll
+                    for (int u = 0; u < kWaves - 1; ++u)
+                        if (i >= base_i + cw[w]) { base_i += cw[w]; ++w; }
+                    const uint64_t rw = sm.cand[(over ? 0 : w * kSeg) + (i - base_i)];
+                    const float f = __uint_as_float((uint32_t)(rw >> 32));
+                    const uint32_t id = (uint32_t)rw;
+                    const float lg = divide ? f / temp : f;
+                    const bool keepit = mode == MODE_TOPK || (double)lg >= lthr;
+                    keys[i] = keepit ? ckey(lg, id) : 0ull;
+                    nv += keepit;
+                }
+                if (mode == MODE_TOPP) {
+                    nv = wave_sum_dpp(nv);
+                    if (lane == 0) sm.wave_i[wv] = nv;
+                }
+                __syncthreads();
+                if (mode == MODE_TOPP) nout = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
+                else nout = n < K ? n : K;
+                for (int i = t; i < n; i += kBlock) {
+                    const uint64_t k = keys[i];
+                    int r0 = 0, r1 = 0;
+                    int jj = 0;
+                    for (; jj + 1 < n; jj += 2) {
+                        r0 += keys[jj] > k ? 1 : 0;
+                        r1 += keys[jj + 1] > k ? 1 : 0;
+                    }
+                    if (jj < n) r0 += keys[jj] > k ? 1 : 0;
+                    sm.cand[r0 + r1] = k;
+                }
+                __syncthreads();
+            }
+        }
+        if (!anynf && !bad_params && (fallback || n > kCand)) {
+            if (mode == MODE_TOPK) {
+                nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn, sm);
+                sort_cand(nout, sm);
+            } else {
+                flags |= FLAG_OVERFLOW;
+                nout = 0;
+            }
+        }
+    }
+
+    // ---- publish, or merge.
+    if (t == 0) sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
+    __syncthreads();
+    uint64_t* row_lists = a.lists + (int64_t)row * S * kListStride;
+    if (!sm.misc[0]) {
+        if (wv == 0) {
+            uint64_t* my_list = row_lists + (int64_t)c * kListStride;
+            for (int i = lane; i < nout; i += 64) st_agent(&my_list[1 + i], sm.cand[i]);
+            __builtin_amdgcn_s_waitcnt(0);   // entries complete before the header
+            if (lane == 0)
+                st_agent(&my_list[0], kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout);
+        }
+        return;
+    }
+
+    // ================= merge: the last workgroup of the row =================
+    // Top-k rows read a sample, each list's header and first r entries
+    // (r ~ 2K/S), in one speculative round: a list whose header is not yet
+    // ready, or whose entries still read 0 (the merger of the previous call
+    // zeroed every word it consumed; keys are never 0), is polled again,
+    // boundedly.  The K best of the sample are the row's K best unless some
+    // list's last sampled entry is among them while the list holds more;
+    // only then, and for top-p rows, are whole lists merged.
+    if (t == 0) st_agent(&a.counters[row], 0u);   // ready for the next launch
+    const int r = mode == MODE_TOPP ? 0 : min(K, max(4, (2 * K + S - 1) / S));
+    const int R1 = r + 1;   // words per list in uni: header, r entries
+    const bool spec = mode != MODE_TOPP && S * R1 <= kUni;
+    uint64_t* uni = sm.big.m.uni;
+    if (t == 0) sm.theta = 0;   // lists to poll again (bit per list)
+    if (spec) {
+        for (int idx = t; idx < S * R1; idx += kBlock) {
+            const int cc = idx / R1, jj = idx - cc * R1;
+            uint64_t v;
+            if (cc == c)
+                v = jj == 0 ? (kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout)
+                            : (jj <= nout ? sm.cand[jj - 1] : 0ull);
+            else
+                v = ld_agent(&row_lists[(int64_t)cc * kListStride + jj]);
+            uni[idx] = v;
+        }
+        __syncthreads();
+        for (int idx = t; idx < S * R1; idx += kBlock) {
+            const int cc = idx / R1, jj = idx - cc * R1;
+            const uint64_t h = uni[cc * R1];
+            const int m = min((int)(uint32_t)h, r);
+            if (!(h & kReady) || (jj >= 1 && jj <= m && uni[idx] == 0))
+                atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
+        }
+        __syncthreads();
+    } else {
+        // Headers only; whole lists are read below.
+        if (t < S) {
+            const uint64_t h = t == c ? (kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout)
+                                      : ld_agent(&row_lists[(int64_t)t * kListStride]);
+            uni[t] = h;
+            if (!(h & kReady)) atomicOr((unsigned long long*)&sm.theta, 1ull << t);
+        }
+        __syncthreads();
+    }
+    const int HW = spec ? R1 : 1;   // stride of the headers in uni
+    if (wv == 0) {
+        // Poll the lists that were not complete, then read their sample.
+        int timed_out = 0;
+        const uint64_t redo = sm.theta;
+        if (lane < S && ((redo >> lane) & 1)) {
+            uint64_t h = 0;
+            for (int it = 0; it < kPollCap; ++it) {
+                h = ld_agent(&row_lists[(int64_t)lane * kListStride]);
+                if (h & kReady) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (h & kReady) {
+                uni[lane * HW] = h;
+                if (spec) {
+                    const int m = min((int)(uint32_t)h, r);
+                    for (int jj = 1; jj <= m; ++jj)
+                        uni[lane * R1 + jj] = ld_agent(&row_lists[(int64_t)lane * kListStride + jj]);
+                }
+            } else {
+                timed_out = 1;
+            }
+        }
+        int n_c = 0, f_c = 0, m_c = 0;
+        if (lane < S) {
+            const uint64_t h = uni[lane * HW];
+            n_c = (int)(uint32_t)h;
+            f_c = (int)((h >> 32) & 0xFF);
+            m_c = min(n_c, r);
+            sm.list_n[lane] = n_c;
+            sm.list_s[lane] = m_c;
+        }
+        const int N = wave_sum_dpp(n_c);
+        int fo = f_c;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) fo |= __shfl_xor(fo, m, 64);
+        const int to = __any(timed_out);
+        if (lane == 0) {
+            sm.misc[5] = N;
+            sm.misc[4] = fo;
+            sm.misc[3] = to;
+            sm.misc[1] = 0;   // "a list ran out"
+        }
+    }
+    __syncthreads();
+    const int N = sm.misc[5];
+    const int fo = sm.misc[4];
+    int status = TMS_ROW_OK;
+    if (sm.misc[3]) status = TMS_ROW_INTERNAL;
+    else if (bad_params) status = TMS_ROW_BAD_PARAMS;
+    else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
+    else if ((fo & FLAG_OVERFLOW) || (mode == MODE_TOPP && N > kToppCap)) status = TMS_ROW_UNSUPPORTED;
+    else if (N == 0) status = TMS_ROW_ALL_MASKED;
+
+    uint64_t* srt = sm.big.m.surv;
+    int n_acc = 0;
+    bool full = !spec;
+    if (status == TMS_ROW_OK && spec) {
+        // Rank the sample by counting (headers and padding count as 0).
+        for (int idx = t; idx < S * R1; idx += kBlock) {
+            const int cc = idx / R1, jj = idx - cc * R1;
+            if (jj == 0 || jj > sm.list_s[cc]) uni[idx] = 0;
+        }
+        __syncthreads();
+        const int M = S * R1;
+        n_acc = min(N, K);
+        for (int idx = t; idx < M; idx += kBlock) {
+            const uint64_t k = uni[idx];
+            if (k == 0) continue;
+            int r0 = 0, r1 = 0, jx = 0;
+            for (; jx + 1 < M; jx += 2) {
+                r0 += uni[jx] > k ? 1 : 0;
+                r1 += uni[jx + 1] > k ? 1 : 0;
+            }
+            if (jx < M) r0 += uni[jx] > k ? 1 : 0;
+            const int rank = r0 + r1;
+            if (rank < n_acc) srt[rank] = k;
+            const int cc = idx / R1, jj = idx - cc * R1;
+            // The run's last sampled entry is among the K best, and the list
+            // holds more: its next entries might be too.
+            if (jj == sm.list_s[cc] && rank < K && sm.list_n[cc] > sm.list_s[cc]) sm.misc[1] = 1;
+        }
+        __syncthreads();
+        full = sm.misc[1] != 0;
+    }
+    if (status == TMS_ROW_OK && full) {
+        // Whole lists, in rounds: the running top list (surv[0..n_acc)) plus
+        // as many chunk lists as fit in kUni, ranked by binary search against
+        // each other.  Top-k rows read at most K entries a list.
+        const int keep_cap = mode == MODE_TOPP ? kToppCap : K;
+        if (t < S) sm.list_s[t] = mode == MODE_TOPP ? sm.list_n[t] : min(sm.list_n[t], K);
+        n_acc = 0;
+        int c_next = 0;
+        __syncthreads();
+        while (c_next < S) {
+            if (t == 0) {
+                int off = n_acc, g = 1, cc = c_next;
+                sm.hist[0] = 0;   // this round's list offsets
+                sm.hist[1] = n_acc;
+                sm.list_src[0] = -1;
+                while (cc < S && off + sm.list_s[cc] <= kUni) {
+                    off += sm.list_s[cc];
+                    sm.list_src[g] = cc;
+                    sm.hist[++g] = off;
+                    ++cc;
+                }
+                sm.misc[6] = g;
+                sm.misc[7] = cc;
+            }
+            __syncthreads();
+            const int ng = sm.misc[6];
+            const int total = sm.hist[ng];
+            for (int i = t; i < total; i += kBlock) {
+                int lc = 0;
+                while (sm.hist[lc + 1] <= i) ++lc;
+                const int src = sm.list_src[lc];
+                const int jj = i - sm.hist[lc];
+                uni[i] = src < 0 ? srt[i]
+                         : (src == c ? sm.cand[jj]
+                                     : ld_agent(&row_lists[(int64_t)src * kListStride + 1 + jj]));
+            }
+            __syncthreads();
+            const int nkeep = total < keep_cap ? total : keep_cap;
+            for (int i = t; i < total; i += kBlock) {
+                int lc = 0;
+                while (sm.hist[lc + 1] <= i) ++lc;
+                const uint64_t k = uni[i];
+                int rank = i - sm.hist[lc];
+                for (int o = 0; o < ng; ++o) {
+                    if (o == lc) continue;
+                    rank += count_greater(uni + sm.hist[o], sm.hist[o + 1] - sm.hist[o], k);
+                }
+                if (rank < nkeep) srt[rank] = k;
+            }
+            c_next = sm.misc[7];
+            n_acc = nkeep;
+            __syncthreads();
+        }
+    }
+    // Zero every word the other chunks wrote this call (headers, entries), so
+    // the next call starts from zeros.
+    if (!sm.misc[3]) {
+        for (int cc = 0; cc < S; ++cc) {
+            if (cc == c) continue;
+            const int nw = 1 + sm.list_n[cc];
+            for (int jj = t; jj < nw; jj += kBlock)
+                st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
+        }
+    }
+    if (status != TMS_ROW_OK) {
+        write_row_error(a, row, status);
+        return;
+    }
+
+    if (mode == MODE_GREEDY) {
+        const int tok = (int)ckey_id(srt[0]);
+        if (t == 0) {
+            a.out_tokens[row] = tok;
+            a.out_status[row] = TMS_ROW_OK;
+            if (a.out_keep) a.out_keep[row] = 0;
+        }
+        for (int i = t; i < a.topk_cap; i += kBlock) {
+            if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
+            if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
+        }
+        return;
+    }
+
+    int n = n_acc;
+    if (mode == MODE_TOPK && N < K) {
+        // Fewer than K finite ids: the tail goes on with -inf entries in
+        // ascending id order, i.e. the ids in [0, K + N) missing from the
+        // (then complete) finite set; K + N < 2 * kTopkFast <= kBlock.
+        const int q = t;
+        int member = 0;
+        if (q < K + N)
+            for (int i = 0; i < N; ++i) member |= (int)ckey_id(srt[i]) == q;
+        const int gap = (q < K + N && !member && q < V) ? 1 : 0;
+        int tot;
+        const int p = block_excl_scan(gap, tot, sm);
+        if (gap && p < K - N) srt[N + p] = ckey(NEG_INF, (uint32_t)q);
+        __syncthreads();
+        n = K;
+    }
+    const float mx = ckey_val(srt[0]);
+    if (mx == __builtin_huge_valf()) {
+        write_row_error(a, row, TMS_ROW_NONFINITE);
+        return;
+    }
+    if (mode == MODE_TOPK) {
+        if (wv == 0)
+            tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand,
+                      (double*)sm.cand + kTopkFast);
+        return;
+    }
+    // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
+    {
+        int sig = 0;
+        for (int i = t; i < n; i += kBlock)
+            sig += ((double)ckey_val(srt[i]) - (double)mx >= -(double)kSigSpan) ? 1 : 0;
+        sig = wave_sum_dpp(sig);
+        if (lane == 0) sm.wave_i[wv] = sig;
+        __syncthreads();
+        n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
+        __syncthreads();
+    }
+    double* pr = (double*)sm.big.m.uni;               // staging no longer needed
+    double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
+    for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
+    __syncthreads();
+    if (wv == 0) tail_topp(a, row, P, srt, n, K, pr, q);
 }
 
 }  // namespace tms
@@ -892,10 +1218,9 @@ struct tms_context {
     int max_chunks;
     size_t bytes;
     void* ws;
-    uint32_t* counters;
-    int32_t* chunk_n;
-    int32_t* chunk_flags;
-    uint64_t* lists;
+    uint32_t* counters;   // [max_batch] arrival counters
+    uint32_t* ones;       // all-ones mask row, for calls without a grammar mask
+    uint64_t* lists;      // [max_batch][max_chunks][kListStride]
 };
 
 extern "C" int tms_abi_version(void) { return TMS_ABI_VERSION; }
@@ -931,13 +1256,14 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->max_chunks = chunks_for(max_vocab);
     const size_t nb = (size_t)max_batch;
     const size_t nc = nb * (size_t)ctx->max_chunks;
-    const size_t off_n = 256 * ((nb * 4 + 255) / 256);
-    const size_t off_f = off_n + 256 * ((nc * 4 + 255) / 256);
-    const size_t off_l = off_f + 256 * ((nc * 4 + 255) / 256);
-    ctx->bytes = off_l + nc * tms::kCand * sizeof(uint64_t);
+    const size_t ones_words = ((size_t)max_vocab + 31) / 32;
+    const size_t off_ones = 256 * ((nb * 4 + 255) / 256);
+    const size_t off_l = off_ones + 256 * ((ones_words * 4 + 255) / 256);
+    ctx->bytes = off_l + nc * tms::kListStride * sizeof(uint64_t);
     int rc = TMS_OK;
     if (hipMalloc(&ctx->ws, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;
-    else if (hipMemset(ctx->ws, 0, off_l) != hipSuccess) rc = TMS_ERR_HIP;
+    else if (hipMemset(ctx->ws, 0, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;   // lists start zeroed
+    else if (hipMemset((char*)ctx->ws + off_ones, 0xFF, ones_words * 4) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipDeviceSynchronize() != hipSuccess) rc = TMS_ERR_HIP;
     if (rc != TMS_OK) {
         if (ctx->ws) (void)hipFree(ctx->ws);
@@ -947,8 +1273,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     }
     char* p = (char*)ctx->ws;
     ctx->counters = (uint32_t*)p;
-    ctx->chunk_n = (int32_t*)(p + off_n);
-    ctx->chunk_flags = (int32_t*)(p + off_f);
+    ctx->ones = (uint32_t*)(p + off_ones);
     ctx->lists = (uint64_t*)(p + off_l);
     (void)hipSetDevice(prev);
     *out = ctx;
@@ -992,13 +1317,14 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     k.S = chunks_for(a->vocab);
     const int per = (a->vocab + k.S - 1) / k.S;
     k.CE = (per + vec - 1) / vec * vec;
-    k.aligned = ((uintptr_t)a->logits % 16 == 0) && ((a->row_stride * esz) % 16 == 0);
+    const bool fast = ((uintptr_t)a->logits % 16 == 0) && ((a->row_stride * esz) % 16 == 0) &&
+                      (a->vocab % vec == 0);
     k.params = a->params;
     k.recent = a->recent;
     k.n_recent = a->n_recent;
     k.recent_stride = a->recent_stride;
-    k.mask = a->mask;
-    k.mask_stride = a->mask_stride;
+    k.mask = a->mask ? a->mask : ctx->ones;
+    k.mask_stride = a->mask ? a->mask_stride : 0;
     k.draws = a->draws;
     k.out_tokens = a->out_tokens;
     k.out_status = a->out_status;
@@ -1007,20 +1333,23 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     k.out_topk_probs = a->out_topk_probs;
     k.topk_cap = (a->out_topk_ids || a->out_topk_probs) ? a->topk_cap : 0;
     k.counters = ctx->counters;
-    k.chunk_n = ctx->chunk_n;
-    k.chunk_flags = ctx->chunk_flags;
     k.lists = ctx->lists;
     const dim3 grid((unsigned)(a->batch * k.S)), block(tms::kBlock);
+#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F>), grid, block, 0, stream, k)
     switch (a->dtype) {
         case TMS_DTYPE_F32:
-            hipLaunchKernelGGL(tms::sample_kernel<float>, grid, block, 0, stream, k);
+            if (fast) TMS_LAUNCH(float, true);
+            else TMS_LAUNCH(float, false);
             break;
         case TMS_DTYPE_F16:
-            hipLaunchKernelGGL(tms::sample_kernel<_Float16>, grid, block, 0, stream, k);
+            if (fast) TMS_LAUNCH(_Float16, true);
+            else TMS_LAUNCH(_Float16, false);
             break;
         default:
-            hipLaunchKernelGGL(tms::sample_kernel<tms::Bf16>, grid, block, 0, stream, k);
+            if (fast) TMS_LAUNCH(tms::Bf16, true);
+            else TMS_LAUNCH(tms::Bf16, false);
             break;
     }
+#undef TMS_LAUNCH
     return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;
 }
