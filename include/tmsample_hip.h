@@ -135,7 +135,10 @@ typedef struct tms_spec_args {
     const int32_t* draft_tokens;  /* device, [batch][k] */
     const tms_row_params* params; /* device, [batch]: temperature, seed, offset */
     const uint32_t* draws;        /* device, [batch][k + 1][2], nullable: words for
-                                     the k accept tests and the final draw */
+                                     the k accept tests and the final draw; when
+                                     null, pair i is Philox4x32-10 outputs 0 and 1
+                                     for key = seed and counter = (offset lo,
+                                     offset hi, i, 0) */
     int32_t* out_accepted;        /* device, [batch]: accepted draft count */
     int32_t* out_token;           /* device, [batch]: residual or bonus token */
     int32_t* out_status;          /* device, [batch], TMS_ROW_* */

@@ -301,40 +301,60 @@ void tmo_sample_batch(const float* logits, int B, int V, int64_t row_stride,
 
 /* ---------------------------------------------------- speculative verify */
 
-/* exp(x) from range reduction and a polynomial (Cody & Waite, "Software
- * Manual for the Elementary Functions", 1980): x = k ln2 + r with
- * |r| <= ln2/2, ln2 split into a double and its residual, e^r by its Taylor
- * series to degree 13 in Horner form, then scaling by 2^k.  Used by the
- * build-defined speculative verify so that the device and this oracle
- * evaluate bit-identical weights; every step is one IEEE operation. */
+/* 2^(j/64), j = 0..63, each the double nearest the exact value (computed
+ * with 60-digit decimal arithmetic). */
+static const double kExp2_64ths[64] = {
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
+};
+
+/* exp(x) by table-driven range reduction (Tang, ACM TOMS 15(2), 1989):
+ * x = (64m + j) ln2/64 + r with |r| <= ln2/128, ln2/64 split into a double
+ * and its residual, e^r by its Taylor series to degree 5 in Horner form,
+ * times 2^(j/64), times 2^m.  Used by the build-defined speculative verify so
+ * that the device and this oracle evaluate bit-identical weights; every step
+ * is one IEEE operation. */
 double tmo_exp64(double x) {
     if (isnan(x)) return x;
-    if (x == -INFINITY || x < -746.0) return 0.0;
+    if (x < -746.0) return 0.0;
     if (x > 709.782712893384) return INFINITY;
-    const double inv_ln2 = 1.4426950408889634;
-    const double ln2_hi = 0x1.62e42fefa39efp-1;
-    const double ln2_lo = 0x1.abc9e3b39803fp-56;
-    const double kd = floor(x * inv_ln2 + 0.5);
-    double r = fma(-kd, ln2_hi, x);
-    r = fma(-kd, ln2_lo, r);
-    static const double c[14] = {
-        1.0, 1.0, 1.0 / 2, 1.0 / 6, 1.0 / 24, 1.0 / 120, 1.0 / 720, 1.0 / 5040,
-        1.0 / 40320, 1.0 / 362880, 1.0 / 3628800, 1.0 / 39916800, 1.0 / 479001600,
-        1.0 / 6227020800.0};
-    double q = c[13];
-    for (int i = 12; i >= 0; --i) q = fma(q, r, c[i]);
-    int k = (int)kd;
-    if (k > 1023) {
-        q = q * 2.0;
-        k -= 1;
+    const double kd = floor(x * 0x1.71547652b82fep+6 + 0.5);
+    double r = fma(-kd, 0x1.62e42fefa39efp-7, x);
+    r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
+    double p = 1.0 / 120;
+    p = fma(p, r, 1.0 / 24);
+    p = fma(p, r, 1.0 / 6);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    const int ki = (int)kd;
+    int m = ki >> 6;   /* floor division: arithmetic shift */
+    double y = kExp2_64ths[ki & 63] * p;
+    if (m > 1023) {
+        y = y * 2.0;
+        m -= 1;
     }
-    if (k < -1020) {
-        q = q * 0x1p-200;
-        k += 200;
+    if (m < -1020) {
+        y = y * 0x1p-200;
+        m += 200;
     }
     union { double d; uint64_t u; } s;
-    s.u = (uint64_t)(k + 1023) << 52;
-    return q * s.d;
+    s.u = (uint64_t)(int64_t)(m + 1023) << 52;
+    return y * s.d;
 }
 
 /* Weights on a 2^-44 grid: round(y * 2^44), half up. */

@@ -1,0 +1,43 @@
+// tms_context.h -- the library's per-device context (internal).
+//
+// One hipMalloc at creation holds every workspace region; the sampling and
+// verify calls allocate nothing.  Every region a kernel reads before writing
+// starts zeroed, and the kernels return it to zero (counters, list headers,
+// published partial sums) before they exit, so back-to-back calls need no
+// clearing launch.
+#ifndef TMS_CONTEXT_H
+#define TMS_CONTEXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tms {
+constexpr int kSpecMaxK = 16;      // draft tokens per sequence
+constexpr int kSpecParts = 64;     // vocabulary parts of the residual draw
+}  // namespace tms
+
+// Statistics of one speculative-verify row (target or draft).
+struct tms_spec_stat {
+    float m;        // max of v / T
+    int32_t status; // TMS_ROW_*
+    int64_t Z;      // sum of the row's 2^-44 weights
+    int64_t ex;     // weight of the draft token (rows with one), else 0
+    int64_t pad;
+};
+
+struct tms_context {
+    int device;
+    int max_batch;
+    int max_vocab;
+    int max_chunks;
+    size_t bytes;
+    void* ws;
+    uint32_t* counters;        // [max_batch] sampler arrival counters
+    uint32_t* ones;            // all-ones mask row, for calls without a grammar mask
+    uint64_t* lists;           // [max_batch][max_chunks][kListStride] chunk candidate lists
+    uint32_t* spec_tickets;    // [max_batch] verify arrival counters
+    uint64_t* spec_parts;      // [max_batch][kSpecParts][2] published partial sums
+    tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]
+};
+
+#endif  // TMS_CONTEXT_H

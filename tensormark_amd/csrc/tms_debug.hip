@@ -17,10 +17,15 @@ __global__ void philox_kernel(const uint32_t* in6, uint32_t* out4, int n) {
     for (int j = 0; j < 4; ++j) out4[4 * i + j] = c[j];
 }
 
+__constant__ double kExpTab[64] = {TMS_EXP2_64THS};
+
 __global__ void exp_kernel(const double* in, double* out, int n, int which) {
+    __shared__ double tab[64];
+    if (threadIdx.x < 64) tab[threadIdx.x] = kExpTab[threadIdx.x];
+    __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    out[i] = which ? exp64(in[i]) : exp(in[i]);
+    out[i] = which ? exp64(in[i], tab) : exp(in[i]);
 }
 
 }  // namespace tms

@@ -78,43 +78,57 @@ __device__ __forceinline__ double canonical(uint32_t w0, uint32_t w1) {
 
 // ------------------------------------------------------------------- exp
 
-// exp(x) by Cody-Waite reduction and a degree-13 Taylor polynomial, one IEEE
-// operation per step, so the host checker evaluates the same bits.  Used by
-// the speculative verify, whose weights are build-defined.
-__device__ __forceinline__ double exp64(double x) {
+// 2^(j/64), j = 0..63, each the double nearest the exact value.
+#define TMS_EXP2_64THS \
+    0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0, \
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0, \
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0, \
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0, \
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0, \
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0, \
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0, \
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0, \
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0, \
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0, \
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0, \
+    0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0, \
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0, \
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0, \
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0, \
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
+
+// exp(x) by table-driven range reduction (Tang, "Table-driven implementation
+// of the exponential function in IEEE floating-point arithmetic", ACM TOMS
+// 15(2), 1989): x = (64m + j) ln2/64 + r with |r| <= ln2/128, ln2/64 split
+// into a double and its residual, e^r by its Taylor series to degree 5 in
+// Horner form, times 2^(j/64) from the table `tab` (64 doubles, in LDS), times
+// 2^m.  Every step is one IEEE operation, so the host checker evaluates the
+// identical function.  Used for the speculative verify's weights.
+__device__ __forceinline__ double exp64(double x, const double* tab) {
     if (x != x) return x;
     if (x < -746.0) return 0.0;
     if (x > 709.782712893384) return __builtin_huge_val();
-    const double inv_ln2 = 1.4426950408889634;
-    const double ln2_hi = 0x1.62e42fefa39efp-1;
-    const double ln2_lo = 0x1.abc9e3b39803fp-56;
-    const double kd = floor(x * inv_ln2 + 0.5);
-    double r = fma(-kd, ln2_hi, x);
-    r = fma(-kd, ln2_lo, r);
-    double q = 1.0 / 6227020800.0;
-    q = fma(q, r, 1.0 / 479001600);
-    q = fma(q, r, 1.0 / 39916800);
-    q = fma(q, r, 1.0 / 3628800);
-    q = fma(q, r, 1.0 / 362880);
-    q = fma(q, r, 1.0 / 40320);
-    q = fma(q, r, 1.0 / 5040);
-    q = fma(q, r, 1.0 / 720);
-    q = fma(q, r, 1.0 / 120);
-    q = fma(q, r, 1.0 / 24);
-    q = fma(q, r, 1.0 / 6);
-    q = fma(q, r, 1.0 / 2);
-    q = fma(q, r, 1.0);
-    q = fma(q, r, 1.0);
-    int k = (int)kd;
-    if (k > 1023) {
-        q = q * 2.0;
-        k -= 1;
+    const double kd = floor(x * 0x1.71547652b82fep+6 + 0.5);
+    double r = fma(-kd, 0x1.62e42fefa39efp-7, x);
+    r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
+    double p = 1.0 / 120;
+    p = fma(p, r, 1.0 / 24);
+    p = fma(p, r, 1.0 / 6);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    const int ki = (int)kd;
+    int m = ki >> 6;
+    double y = tab[ki & 63] * p;
+    if (m > 1023) {
+        y = y * 2.0;
+        m -= 1;
     }
-    if (k < -1020) {
-        q = q * 0x1p-200;
-        k += 200;
+    if (m < -1020) {
+        y = y * 0x1p-200;
+        m += 200;
     }
-    return q * __longlong_as_double((long long)(k + 1023) << 52);
+    return y * __longlong_as_double((long long)(m + 1023) << 52);
 }
 
 __device__ __forceinline__ int64_t q44(double y) {
@@ -322,6 +336,68 @@ __device__ __forceinline__ float float_below(float x) {
     const uint32_t u = __float_as_uint(x);
     if ((u & 0x7FFFFFFFu) == 0) return __uint_as_float(0x80000001u);   // +-0 -> -min subnormal
     return __uint_as_float((u & 0x80000000u) ? u + 1u : u - 1u);
+}
+
+// bf16 storage: the high half of an fp32.
+struct Bf16 {
+    uint16_t bits;
+};
+
+// Element types: vector width of a 16-byte load, exact widening to fp32.
+template <typename T>
+struct Elt;
+template <>
+struct Elt<float> {
+    static constexpr int kVec = 4;
+    __device__ static void widen(const uint4& q, float (&f)[4]) {
+        f[0] = __uint_as_float(q.x);
+        f[1] = __uint_as_float(q.y);
+        f[2] = __uint_as_float(q.z);
+        f[3] = __uint_as_float(q.w);
+    }
+    __device__ static float scalar(const float* p) { return *p; }
+};
+template <>
+struct Elt<_Float16> {
+    static constexpr int kVec = 8;
+    __device__ static float h2f(uint32_t h) {
+        _Float16 v;
+        const uint16_t b = (uint16_t)h;
+        __builtin_memcpy(&v, &b, 2);
+        return (float)v;
+    }
+    __device__ static void widen(const uint4& q, float (&f)[8]) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = h2f(w[i] & 0xFFFFu);
+            f[2 * i + 1] = h2f(w[i] >> 16);
+        }
+    }
+    __device__ static float scalar(const _Float16* p) { return (float)*p; }
+};
+template <>
+struct Elt<Bf16> {
+    static constexpr int kVec = 8;
+    __device__ static void widen(const uint4& q, float (&f)[8]) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        }
+    }
+    __device__ static float scalar(const Bf16* p) { return __uint_as_float((uint32_t)p->bits << 16); }
+};
+
+// Relaxed agent-scope accesses: coherent across the XCDs' L2 caches.
+template <typename U>
+__device__ __forceinline__ void st_agent(U* p, U v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename U>
+__device__ __forceinline__ U ld_agent(const U* p) {
+    return __hip_atomic_load(const_cast<U*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace tms

@@ -39,6 +39,7 @@
 
 #include "../../include/tmsample_hip.h"
 #include "tms_device.h"
+#include "tms_context.h"
 
 namespace tms {
 
@@ -79,57 +80,6 @@ struct KArgs {
     // workspace
     uint32_t* counters;    // [B] arrival tickets, reset by the merger
     uint64_t* lists;       // [B][S][kListStride]: header, entries; headers reset by the merger
-};
-
-struct Bf16 {
-    uint16_t bits;
-};
-
-// Element types: vector width of a 16-byte load, exact widening to fp32.
-template <typename T>
-struct Elt;
-template <>
-struct Elt<float> {
-    static constexpr int kVec = 4;
-    __device__ static void widen(const uint4& q, float (&f)[4]) {
-        f[0] = __uint_as_float(q.x);
-        f[1] = __uint_as_float(q.y);
-        f[2] = __uint_as_float(q.z);
-        f[3] = __uint_as_float(q.w);
-    }
-    __device__ static float scalar(const float* p) { return *p; }
-};
-template <>
-struct Elt<_Float16> {
-    static constexpr int kVec = 8;
-    __device__ static float h2f(uint32_t h) {
-        _Float16 v;
-        const uint16_t b = (uint16_t)h;
-        __builtin_memcpy(&v, &b, 2);
-        return (float)v;
-    }
-    __device__ static void widen(const uint4& q, float (&f)[8]) {
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = h2f(w[i] & 0xFFFFu);
-            f[2 * i + 1] = h2f(w[i] >> 16);
-        }
-    }
-    __device__ static float scalar(const _Float16* p) { return (float)*p; }
-};
-template <>
-struct Elt<Bf16> {
-    static constexpr int kVec = 8;
-    __device__ static void widen(const uint4& q, float (&f)[8]) {
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f[2 * i] = __uint_as_float(w[i] << 16);
-            f[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-        }
-    }
-    __device__ static float scalar(const Bf16* p) { return __uint_as_float((uint32_t)p->bits << 16); }
 };
 
 // History penalties of one row.
@@ -349,14 +299,6 @@ __device__ __forceinline__ int count_greater(const uint64_t* L, int n, uint64_t 
     return lo;
 }
 
-template <typename U>
-__device__ __forceinline__ void st_agent(U* p, U v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename U>
-__device__ __forceinline__ U ld_agent(const U* p) {
-    return __hip_atomic_load(const_cast<U*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 __device__ __forceinline__ void write_row_error(const KArgs& a, int row, int status) {
     const int t = threadIdx.x;
@@ -1211,17 +1153,6 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 
 // ============================================================== C ABI
 
-struct tms_context {
-    int device;
-    int max_batch;
-    int max_vocab;
-    int max_chunks;
-    size_t bytes;
-    void* ws;
-    uint32_t* counters;   // [max_batch] arrival counters
-    uint32_t* ones;       // all-ones mask row, for calls without a grammar mask
-    uint64_t* lists;      // [max_batch][max_chunks][kListStride]
-};
 
 extern "C" int tms_abi_version(void) { return TMS_ABI_VERSION; }
 
@@ -1259,7 +1190,10 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t ones_words = ((size_t)max_vocab + 31) / 32;
     const size_t off_ones = 256 * ((nb * 4 + 255) / 256);
     const size_t off_l = off_ones + 256 * ((ones_words * 4 + 255) / 256);
-    ctx->bytes = off_l + nc * tms::kListStride * sizeof(uint64_t);
+    const size_t off_st = off_l + nc * tms::kListStride * sizeof(uint64_t);
+    const size_t off_sp = off_st + 256 * ((nb * 4 + 255) / 256);
+    const size_t off_ss = off_sp + nb * tms::kSpecParts * 2 * sizeof(uint64_t);
+    ctx->bytes = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
     int rc = TMS_OK;
     if (hipMalloc(&ctx->ws, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipMemset(ctx->ws, 0, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;   // lists start zeroed
@@ -1275,6 +1209,9 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->counters = (uint32_t*)p;
     ctx->ones = (uint32_t*)(p + off_ones);
     ctx->lists = (uint64_t*)(p + off_l);
+    ctx->spec_tickets = (uint32_t*)(p + off_st);
+    ctx->spec_parts = (uint64_t*)(p + off_sp);
+    ctx->spec_stats = (tms_spec_stat*)(p + off_ss);
     (void)hipSetDevice(prev);
     *out = ctx;
     return TMS_OK;
