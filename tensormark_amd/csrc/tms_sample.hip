@@ -51,6 +51,7 @@ constexpr int kListStride = kCand + 2;     // u64 per published list: header + e
 constexpr int kUni = 2048;                 // merge staging (u64)
 constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
+constexpr int kRankLists = 16;             // chunk lists ranked in registers by the merge
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
 constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per list
@@ -352,8 +353,91 @@ __device__ __forceinline__ int count_gt_fixed(const uint64_t* L, int n, uint64_t
 // sum at step i in a register.  The partial sums only grow (the terms are
 // >= 0), so the top-p cut and the drawn index are counts of partial sums
 // below the threshold.
+// Number of keys larger than k in the sorted (descending) lists 0..S-1 other
+// than `skip`; list o holds n[o] keys at L[o * stride + 1 ...].  Binary
+// searches over all lists in lockstep: each step issues every list's read
+// before any compare, and the updates are selects, so the reads overlap.
+template <int NL>
+__device__ __forceinline__ int larger_in_lists(const uint64_t* L, int stride, int S, int skip,
+                                               int steps, uint64_t k, const int* n) {
+    int lo[NL], hi[NL];
+#pragma unroll
+    for (int o = 0; o < NL; ++o) {
+        lo[o] = 0;
+        hi[o] = (o < S && o != skip) ? n[o] : 0;
+    }
+    for (int st = 0; st < steps; ++st) {
+        uint64_t v[NL];
+#pragma unroll
+        for (int o = 0; o < NL; ++o) v[o] = L[o * stride + 1 + ((lo[o] + hi[o]) >> 1)];
+#pragma unroll
+        for (int o = 0; o < NL; ++o) {
+            const int mid = (lo[o] + hi[o]) >> 1;
+            const bool live = lo[o] < hi[o];
+            const bool gt = v[o] > k;
+            lo[o] = (live && gt) ? mid + 1 : lo[o];
+            hi[o] = (live && !gt) ? mid : hi[o];
+        }
+    }
+    int c = 0;
+#pragma unroll
+    for (int o = 0; o < NL; ++o) c += lo[o];
+    return c;
+}
+
+// Zero the published lists of a row (header and entries of every chunk but
+// `own`), threads tid0 .. nthr-1 of the workgroup.
+__device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, int own, const int* list_n,
+                                           int tid0, int nthr) {
+    for (int cc = 0; cc < S; ++cc) {
+        if (cc == own) continue;
+        const int nw = 1 + list_n[cc];
+        for (int jj = tid0; jj < nw; jj += nthr)
+            st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
+    }
+}
+
+// Left-to-right sum of v[0..n), as a scalar loop computes it.
+__device__ __forceinline__ double seq_sum(const double* v, int n) {
+    double s = 0.0;
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) s += v[i];
+    return s;
+}
+
+// First i in [0, n) whose left-to-right prefix sum v[0] + ... + v[i] is >=
+// thr, or n (v >= 0, so the prefixes never decrease).  Eight prefixes at a
+// time stay in registers; the chain stops at the block that crosses.
+__device__ __forceinline__ int first_prefix_ge(const double* v, int n, double thr) {
+    double s = 0.0;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+        double c[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            s += v[i + e];
+            c[e] = s;
+        }
+        if (s >= thr) {
+            int below = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) below += c[e] < thr ? 1 : 0;
+            return i + below;
+        }
+    }
+    for (; i < n; ++i) {
+        s += v[i];
+        if (s >= thr) return i;
+    }
+    return n;
+}
+
+// fp64 tail of tmsample::sample (tensormark/tmsample.h:185-199) for top-k
+// rows, one wave, n = K <= 2 * 64 sorted entries in srt: pr = exp(lg - mx),
+// z, the top-p and min-p cuts and the std::discrete_distribution draw, with
+// every sum in the reference's order (uniform chains over LDS).
 __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
-                          int n, int K, double* pr, double* q, double* /*unused*/) {
+                          int n, int K, double* pr, double* q) {
     const int lane = threadIdx.x & 63;
     uint32_t w0, w1;
     row_uniform(a, row, P, w0, w1);   // independent of the sums: overlaps them
@@ -365,31 +449,15 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
     if (h0) pr[lane] = pr0;
     if (h1) pr[lane + 64] = pr1;
     wave_lds_sync();
-    double z = 0, zc0 = 0, zc1 = 0;                 // tmsample.h:186-191
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) {
-        z += pr[i];
-        zc0 = lane == i ? z : zc0;
-        zc1 = lane + 64 == i ? z : zc1;
-    }
+    const double z = seq_sum(pr, n);                // tmsample.h:186-191
     const double q0 = pr0 / z, q1 = pr1 / z;
     if (h0) q[lane] = q0;
     if (h1) q[lane + 64] = q1;
     wave_lds_sync();
-    double cc0 = 0, cc1 = 0;
-    {
-        double cum = 0;                             // tmsample.h:192-197
-#pragma unroll 8
-        for (int i = 0; i < n; ++i) {
-            cum += q[i];
-            cc0 = lane == i ? cum : cc0;
-            cc1 = lane + 64 == i ? cum : cc1;
-        }
-    }
-    const double tp = (double)P.top_p;
-    const int below = __popcll(__ballot(h0 && cc0 < tp)) + __popcll(__ballot(h1 && cc1 < tp));
-    int kp = below + 1 < K ? below + 1 : K;   // keep = first index with cum >= top_p, + 1
-    if (!(P.top_p == P.top_p)) kp = K;        // NaN: cum >= top_p never holds
+    // keep = first index with cum >= top_p, + 1, else K (tmsample.h:192-197;
+    // a NaN top_p never compares true).
+    const int fi = first_prefix_ge(q, n, (double)P.top_p);
+    int kp = fi < n ? fi + 1 : K;
     if (P.min_p > 0.0f) {
         // min-p: the first entry below min_p ends the kept prefix.
         const double mp = (double)P.min_p;
@@ -402,24 +470,16 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
     const int keep = kp;
     int tokidx = 0;
     if (keep >= 2) {
-        // std::discrete_distribution over pr[0..keep): sum = accumulate() =
-        // the z prefix at keep - 1, p = pr / sum, partial sums with the last
-        // forced to 1, lower_bound(u) = #(cp_j < u) over j < keep - 1.
-        const double sum = readlane_f64(keep - 1 < 64 ? zc0 : zc1, (keep - 1) & 63);
+        // std::discrete_distribution over pr[0..keep): sum = accumulate(),
+        // p = pr / sum, partial sums with the last forced to 1, then
+        // lower_bound(u) = the first j < keep - 1 with cp_j >= u, else keep - 1.
+        const double sum = seq_sum(pr, keep);
         const double p0 = pr0 / sum, p1 = pr1 / sum;
         wave_lds_sync();
-        if (h0) q[lane] = p0;
-        if (h1) q[lane + 64] = p1;
+        if (h0) pr[lane] = p0;
+        if (h1) pr[lane + 64] = p1;
         wave_lds_sync();
-        double c0 = 0, c1 = 0, cp = 0;
-#pragma unroll 8
-        for (int i = 0; i < keep - 1; ++i) {
-            cp += q[i];
-            c0 = lane == i ? cp : c0;
-            c1 = lane + 64 == i ? cp : c1;
-        }
-        tokidx = __popcll(__ballot(lane < keep - 1 && c0 < u)) +
-                 __popcll(__ballot(lane + 64 < keep - 1 && c1 < u));
+        tokidx = first_prefix_ge(pr, keep - 1, u);
     }
     if (lane == 0) {
         a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
@@ -901,9 +961,9 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     // list's last sampled entry is among them while the list holds more;
     // only then, and for top-p rows, are whole lists merged.
     if (t == 0) st_agent(&a.counters[row], 0u);   // ready for the next launch
-    const int r = mode == MODE_TOPP ? 0 : min(K, max(4, (2 * K + S - 1) / S));
+    const int r = (mode == MODE_TOPP || S > kRankLists) ? 0 : min(K, kUni / S - 1);
     const int R1 = r + 1;   // words per list in uni: header, r entries
-    const bool spec = mode != MODE_TOPP && S * R1 <= kUni;
+    const bool spec = r > 0;
     uint64_t* uni = sm.big.m.uni;
     if (t == 0) sm.theta = 0;   // lists to poll again (bit per list)
     if (spec) {
@@ -994,29 +1054,72 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     int n_acc = 0;
     bool full = !spec;
     if (status == TMS_ROW_OK && spec) {
-        // Rank the sample by counting (headers and padding count as 0).
-        for (int idx = t; idx < S * R1; idx += kBlock) {
-            const int cc = idx / R1, jj = idx - cc * R1;
-            if (jj == 0 || jj > sm.list_s[cc]) uni[idx] = 0;
+        // Prune with a lower bound tau on the row's K-th key: the largest
+        // K-th entry of any list (that list alone holds K keys >= it), or
+        // the smallest m-th entry over all lists, m = ceil(K / S) (the S
+        // lists hold S * m >= K keys >= it).  Only keys >= tau can rank
+        // below K, and every key larger than one of them is >= tau too, so
+        // counting within that set ranks it exactly.
+        n_acc = min(N, K);
+        if (wv == 0) {
+            const int m = (K + S - 1) / S;
+            const int ls = lane < S ? sm.list_s[lane] : 0;
+            const uint64_t kth = (lane < S && ls >= K) ? uni[lane * R1 + K] : 0ull;
+            const uint64_t mth = lane >= S ? ~0ull : (ls >= m ? uni[lane * R1 + m] : 0ull);
+            const uint64_t tau = max(wave_max_u64_dpp(kth), ~wave_max_u64_dpp(~mth));
+            if (lane == 0) {
+                sm.theta = tau;
+                sm.ncand = 0;
+            }
         }
         __syncthreads();
-        const int M = S * R1;
-        n_acc = min(N, K);
-        for (int idx = t; idx < M; idx += kBlock) {
-            const uint64_t k = uni[idx];
-            if (k == 0) continue;
-            int r0 = 0, r1 = 0, jx = 0;
-            for (; jx + 1 < M; jx += 2) {
-                r0 += uni[jx] > k ? 1 : 0;
-                r1 += uni[jx + 1] > k ? 1 : 0;
-            }
-            if (jx < M) r0 += uni[jx] > k ? 1 : 0;
-            const int rank = r0 + r1;
-            if (rank < n_acc) srt[rank] = k;
+        const uint64_t tau = sm.theta;
+        for (int idx = t; idx < S * R1; idx += kBlock) {
             const int cc = idx / R1, jj = idx - cc * R1;
-            // The run's last sampled entry is among the K best, and the list
-            // holds more: its next entries might be too.
-            if (jj == sm.list_s[cc] && rank < K && sm.list_n[cc] > sm.list_s[cc]) sm.misc[1] = 1;
+            const uint64_t k = uni[idx];
+            const bool in = jj >= 1 && jj <= sm.list_s[cc] && k >= tau;
+            const uint64_t bal = __ballot(in);
+            int base = 0;
+            if (lane == 0 && bal) base = atomicAdd(&sm.ncand, __popcll(bal));
+            base = __shfl(base, 0, 64);
+            if (in) {
+                const int pos = base + (int)__builtin_amdgcn_mbcnt_hi(
+                    (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                // cand keeps the key; list and position ride in surv's tail.
+                sm.cand[pos < kCand ? pos : 0] = k;
+                if (pos < kCand) sm.big.m.surv[kUni - 1 - pos] = ((uint64_t)cc << 32) | (uint32_t)jj;
+            }
+        }
+        __syncthreads();
+        const int nc = sm.ncand;
+        if (nc <= kCand) {
+            for (int i = t; i < nc; i += kBlock) {
+                const uint64_t k = sm.cand[i];
+                int r0 = 0, r1 = 0, j = 0;
+                for (; j + 1 < nc; j += 2) {
+                    r0 += sm.cand[j] > k ? 1 : 0;
+                    r1 += sm.cand[j + 1] > k ? 1 : 0;
+                }
+                if (j < nc) r0 += sm.cand[j] > k ? 1 : 0;
+                const int rank = r0 + r1;
+                const uint64_t where = sm.big.m.surv[kUni - 1 - i];
+                const int cc = (int)(where >> 32), jj = (int)(uint32_t)where;
+                if (rank < n_acc) srt[rank] = k;
+                if (jj == sm.list_s[cc] && rank < K - 1 && sm.list_n[cc] > sm.list_s[cc]) sm.misc[1] = 1;
+            }
+        } else {
+            // Rare: tau admits most entries (lists shorter than K).
+            const int steps = 32 - __builtin_clz((unsigned)r);   // halvings of [0, r]
+            for (int idx = t; idx < S * R1; idx += kBlock) {
+                const int cc = idx / R1, jj = idx - cc * R1;
+                if (jj == 0 || jj > sm.list_s[cc]) continue;
+                const uint64_t k = uni[idx];
+                const int rank = jj - 1 + (S <= 8 ? larger_in_lists<8>(uni, R1, S, cc, steps, k, sm.list_s)
+                                                  : larger_in_lists<kRankLists>(uni, R1, S, cc, steps, k,
+                                                                                sm.list_s));
+                if (rank < n_acc) srt[rank] = k;
+                if (jj == sm.list_s[cc] && rank < K - 1 && sm.list_n[cc] > sm.list_s[cc]) sm.misc[1] = 1;
+            }
         }
         __syncthreads();
         full = sm.misc[1] != 0;
@@ -1075,16 +1178,11 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             __syncthreads();
         }
     }
-    // Zero every word the other chunks wrote this call (headers, entries), so
-    // the next call starts from zeros.
-    if (!sm.misc[3]) {
-        for (int cc = 0; cc < S; ++cc) {
-            if (cc == c) continue;
-            const int nw = 1 + sm.list_n[cc];
-            for (int jj = t; jj < nw; jj += kBlock)
-                st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
-        }
-    }
+    // Every word the other chunks wrote this call (headers, entries) goes
+    // back to zero for the next call; on a top-k row's success path waves
+    // 1-3 do it while wave 0 runs the tail.
+    const bool defer_zero = status == TMS_ROW_OK && mode == MODE_TOPK && !sm.misc[3];
+    if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, c, sm.list_n, t, kBlock);
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
         return;
@@ -1122,13 +1220,15 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     }
     const float mx = ckey_val(srt[0]);
     if (mx == __builtin_huge_valf()) {
+        if (defer_zero) zero_lists(row_lists, S, c, sm.list_n, t, kBlock);
         write_row_error(a, row, TMS_ROW_NONFINITE);
         return;
     }
     if (mode == MODE_TOPK) {
         if (wv == 0)
-            tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand,
-                      (double*)sm.cand + kTopkFast);
+            tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand);
+        else
+            zero_lists(row_lists, S, c, sm.list_n, t - 64, kBlock - 64);
         return;
     }
     // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
