@@ -42,6 +42,9 @@ def parse():
                     help="reuse one input batch (cache-resident after the first launch)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--eager", action="store_true", help="time eager launches, no graph")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="first run 3 plain device copies of MIB MiB (a known-size kernel that "
+                         "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -125,6 +128,15 @@ def main():
     dev = torch.device("cuda:0")
     w, dt_name, algo_bytes, name = workload(args.config)
     import ctypes
+
+    if args.calib_copy > 0:
+        n = args.calib_copy * 2**20 // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     stream = torch.cuda.Stream(device=dev)
     sp = ctypes.c_void_p(stream.cuda_stream)

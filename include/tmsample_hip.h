@@ -187,6 +187,24 @@ int tms_sample_batch(tms_context* ctx, const tms_sample_args* args, hipStream_t 
 int tms_spec_verify(tms_context* ctx, const tms_spec_args* args, hipStream_t stream);
 
 /*
+ * The history transforms on a host row of V fp32 logits, in place, for
+ * callers that run them before upload (rows with the n-gram ban or DRY on;
+ * the device applies the repetition penalty itself from the window).
+ *   tms_host_repeat_penalty   tmsample::apply_repeat_penalty  (tensormark/tmsample.h:52-63)
+ *   tms_host_no_repeat_ngram  tmsample::apply_no_repeat_ngram (tensormark/tmsample.h:81-114)
+ *   tms_host_dry              tmsample::apply_dry             (tensormark/tmsample.h:148-170),
+ *                             the DryOpts fields (tensormark/tmsample.h:141-146) passed
+ *                             one by one; is_breaker is nullable, indexed by id.
+ */
+void tms_host_repeat_penalty(float* logits, int V, const int32_t* recent, int n_recent,
+                             int window, float penalty);
+void tms_host_no_repeat_ngram(float* logits, int V, const int32_t* recent, int n_recent,
+                              int ngram);
+void tms_host_dry(float* logits, int V, const int32_t* recent, int n_recent, float multiplier,
+                  float base, int allowed_length, int penalty_last_n,
+                  const unsigned char* is_breaker);
+
+/*
  * Test hooks.  Run the device Philox4x32-10 on n (counter[4], key[2])
  * tuples packed as 6 words each and write 4 words each; evaluate the device
  * double exp on n inputs (which = 0: the HIP math library, 1: the

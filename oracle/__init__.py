@@ -220,6 +220,22 @@ class Ref:
     def canonical(self, w0, w1):
         return self.lib.ref_canonical(w0, w1)
 
+    def no_repeat_ngram(self, row, recent, ngram):
+        row = np.ascontiguousarray(row, np.float32).copy()
+        r = np.ascontiguousarray(recent, np.int32)
+        self.lib.ref_no_repeat_ngram(_p(row, C.c_float), C.c_int(row.size), _p(r, C.c_int32),
+                                     C.c_int(r.size), C.c_int(ngram))
+        return row
+
+    def dry(self, row, recent, multiplier, base, allowed_length, penalty_last_n, is_breaker=None):
+        row = np.ascontiguousarray(row, np.float32).copy()
+        r = np.ascontiguousarray(recent, np.int32)
+        brk = None if is_breaker is None else np.ascontiguousarray(is_breaker, np.uint8)
+        self.lib.ref_dry(_p(row, C.c_float), C.c_int(row.size), _p(r, C.c_int32), C.c_int(r.size),
+                         C.c_float(multiplier), C.c_float(base), C.c_int(allowed_length),
+                         C.c_int(penalty_last_n), None if brk is None else _p(brk, C.c_uint8))
+        return row
+
     def discrete(self, pr, w0, w1):
         pr = np.ascontiguousarray(pr, np.float64)
         used = C.c_int()

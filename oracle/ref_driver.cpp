@@ -129,4 +129,24 @@ double ref_bench(const float* logits, int B, int V, float T, int top_k, float to
     return best;
 }
 
+// The reference's no-repeat n-gram ban and DRY on a row, in place
+// (tensormark/tmsample.h:81-114, 148-170).
+void ref_no_repeat_ngram(float* logits, int V, const std::int32_t* recent, int n_recent, int ngram) {
+    std::vector<float> row(logits, logits + V);
+    tmsample::apply_no_repeat_ngram(row, recent, n_recent, ngram);
+    std::memcpy(logits, row.data(), sizeof(float) * static_cast<std::size_t>(V));
+}
+
+void ref_dry(float* logits, int V, const std::int32_t* recent, int n_recent, float multiplier,
+             float base, int allowed_length, int penalty_last_n, const unsigned char* is_breaker) {
+    std::vector<float> row(logits, logits + V);
+    tmsample::DryOpts o;
+    o.multiplier = multiplier;
+    o.base = base;
+    o.allowed_length = allowed_length;
+    o.penalty_last_n = penalty_last_n;
+    tmsample::apply_dry(row, recent, n_recent, o, is_breaker);
+    std::memcpy(logits, row.data(), sizeof(float) * static_cast<std::size_t>(V));
+}
+
 }  // extern "C"

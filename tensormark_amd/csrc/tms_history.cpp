@@ -1,0 +1,78 @@
+// tms_history.cpp -- the deterministic history transforms of TensorMark's
+// sampler on a host row: repetition penalty, no-repeat n-gram ban and DRY.
+//
+// They run on the host, before a row is uploaded, for callers that enable
+// the n-gram ban or DRY (the device sampler applies the repetition penalty
+// itself from the window, but DRY's logit shift must follow it, so a row
+// with DRY or a ban goes through all three here in the reference's order:
+// tensormark/llama_chat.cpp:146-153).
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <utility>
+#include <vector>
+
+#include "../../include/tmsample_hip.h"
+
+// tensormark/tmsample.h:52-63: v > 0 ? v / p : v * p, once per occurrence.
+extern "C" void tms_host_repeat_penalty(float* logits, int V, const int32_t* recent, int n_recent,
+                                        int window, float penalty) {
+    if (!logits || !recent || penalty <= 1.0f || window <= 0 || n_recent <= 0) return;
+    for (int i = n_recent > window ? n_recent - window : 0; i < n_recent; ++i) {
+        const int id = recent[i];
+        if (id < 0 || id >= V) continue;
+        const float v = logits[id];
+        logits[id] = v > 0.f ? v / penalty : v * penalty;
+    }
+}
+
+// tensormark/tmsample.h:81-114: every id that followed an earlier occurrence
+// of the current (ngram - 1)-id context becomes -inf; if that leaves no
+// finite logit the banned ids get their values back.
+extern "C" void tms_host_no_repeat_ngram(float* logits, int V, const int32_t* recent, int n_recent,
+                                         int ngram) {
+    if (!logits || !recent || ngram < 2 || n_recent < ngram) return;
+    const float ninf = -INFINITY;
+    const int ctx = ngram - 1;
+    const int tail = n_recent - ctx;
+    std::vector<std::pair<int, float>> undo;
+    for (int i = 0; i < tail; ++i) {
+        if (memcmp(recent + i, recent + tail, sizeof(int32_t) * (size_t)ctx) != 0) continue;
+        const int next = recent[i + ctx];
+        if (next < 0 || next >= V) continue;
+        if (logits[next] == ninf) continue;   // banned already: keep the first saved value
+        undo.emplace_back(next, logits[next]);
+        logits[next] = ninf;
+    }
+    if (undo.empty()) return;
+    for (int i = 0; i < V; ++i)
+        if (logits[i] > ninf || logits[i] != logits[i]) return;   // something is left
+    for (const auto& u : undo) logits[u.first] = u.second;
+}
+
+// tensormark/tmsample.h:148-170: for each earlier position whose run agrees
+// with the window's tail for L >= allowed_length ids (never across a breaker
+// id), subtract multiplier * base^(L - allowed_length) from the id that
+// followed the earlier run.
+extern "C" void tms_host_dry(float* logits, int V, const int32_t* recent, int n_recent,
+                             float multiplier, float base, int allowed_length, int penalty_last_n,
+                             const unsigned char* is_breaker) {
+    if (!logits || !recent || multiplier <= 0.0f || allowed_length < 1) return;
+    const int n = n_recent < penalty_last_n ? n_recent : penalty_last_n;
+    if (n_recent < allowed_length + 1 || n < allowed_length + 1) return;
+    const int32_t* w = recent + (n_recent - n);
+    const int last = n - 1;
+    for (int i = 0; i < last; ++i) {
+        int L = 0;
+        while (L <= i && w[i - L] == w[last - L] &&
+               !(is_breaker && (is_breaker[w[i - L]] || is_breaker[w[last - L]])))
+            ++L;
+        if (L < allowed_length) continue;
+        const int next = w[i + 1];
+        if (next < 0 || next >= V) continue;
+        if (is_breaker && is_breaker[next]) continue;
+        logits[next] -= multiplier * powf(base, (float)(L - allowed_length));
+    }
+}

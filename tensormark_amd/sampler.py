@@ -37,6 +37,9 @@ EXPORTS = (
     "tms_spec_verify",
     "tms_debug_philox",
     "tms_debug_exp",
+    "tms_host_repeat_penalty",
+    "tms_host_no_repeat_ngram",
+    "tms_host_dry",
 )
 
 
@@ -138,6 +141,13 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         lib.tms_spec_verify.argtypes = [C.c_void_p, C.POINTER(SpecArgs), C.c_void_p]
         lib.tms_debug_philox.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
         lib.tms_debug_exp.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
+        fp, ip = C.POINTER(C.c_float), C.POINTER(C.c_int32)
+        lib.tms_host_repeat_penalty.argtypes = [fp, C.c_int, ip, C.c_int, C.c_int, C.c_float]
+        lib.tms_host_no_repeat_ngram.argtypes = [fp, C.c_int, ip, C.c_int, C.c_int]
+        lib.tms_host_dry.argtypes = [fp, C.c_int, ip, C.c_int, C.c_float, C.c_float, C.c_int,
+                                     C.c_int, C.c_void_p]
+        for f in (lib.tms_host_repeat_penalty, lib.tms_host_no_repeat_ngram, lib.tms_host_dry):
+            f.restype = None
         _LIB = lib
     return _LIB
 
@@ -280,6 +290,40 @@ class Sampler:
         _check(self.lib.tms_spec_verify(self.handle, C.byref(a), C.c_void_p(s)),
                "tms_spec_verify")
         return out
+
+
+def _f32_row(row):
+    assert isinstance(row, np.ndarray) and row.dtype == np.float32 and row.flags.c_contiguous
+    return row.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _ids(recent):
+    r = np.ascontiguousarray(recent, np.int32)
+    return r, r.ctypes.data_as(C.POINTER(C.c_int32))
+
+
+def apply_repeat_penalty(row, recent, window, penalty):
+    """tmsample::apply_repeat_penalty (tmsample.h:52-63) on a host fp32 row, in place."""
+    r, rp = _ids(recent)
+    load_library().tms_host_repeat_penalty(_f32_row(row), row.size, rp, r.size, window, penalty)
+
+
+def apply_no_repeat_ngram(row, recent, ngram):
+    """tmsample::apply_no_repeat_ngram (tmsample.h:81-114) on a host fp32 row, in place."""
+    r, rp = _ids(recent)
+    load_library().tms_host_no_repeat_ngram(_f32_row(row), row.size, rp, r.size, ngram)
+
+
+def apply_dry(row, recent, multiplier=0.0, base=1.75, allowed_length=2, penalty_last_n=256,
+              is_breaker=None):
+    """tmsample::apply_dry (tmsample.h:148-170) on a host fp32 row, in place."""
+    r, rp = _ids(recent)
+    brk = None
+    if is_breaker is not None:
+        brk = np.ascontiguousarray(is_breaker, np.uint8)
+    load_library().tms_host_dry(_f32_row(row), row.size, rp, r.size, multiplier, base,
+                                allowed_length, penalty_last_n,
+                                None if brk is None else brk.ctypes.data_as(C.c_void_p))
 
 
 def debug_philox(in6, out4=None):
