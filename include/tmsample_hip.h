@@ -205,6 +205,52 @@ void tms_host_dry(float* logits, int V, const int32_t* recent, int n_recent, flo
                   const unsigned char* is_breaker);
 
 /*
+ * Host GBNF engine: the producer of the grammar bitmask.  Replaces
+ * tmgbnf::Grammar and tmgbnf::TokenMask (tensormark/gbnf.h:345-851) with the
+ * same language semantics; the allowed set comes out as the sampler's mask
+ * words directly.  Host-only, single-threaded per grammar.
+ *
+ *   tms_grammar_parse     Grammar::parse (gbnf.h:347-385); NULL on a parse
+ *                         error, with the message in err (gbnf: ...)
+ *   tms_grammar_start     Grammar::start (gbnf.h:435-440)
+ *   tms_grammar_advance   Grammar::advance, one byte (gbnf.h:455-480); 0 =
+ *                         rejected (the state is then dead)
+ *   tms_grammar_can_end   Grammar::can_end (gbnf.h:443-448)
+ *   tms_grammar_accepts   Grammar::accepts (gbnf.h:484-489)
+ *   tms_gstate_copy/free/equal   State value semantics (gbnf.h:409-416)
+ *   tms_vocab_create      TokenMask(g, token_text, eos, skip) (gbnf.h:729-755);
+ *                         text[i]/len[i] = bytes of token i; skip nullable
+ *   tms_vocab_allowed     TokenMask::allowed (gbnf.h:759-769): ascending ids,
+ *                         returns the count (ids may be NULL to size)
+ *   tms_vocab_mask        the same set as bits: words[id >> 5] bit id & 31,
+ *                         n_words words cleared first; returns ids written
+ *   tms_vocab_consume     TokenMask::consume (gbnf.h:772-778)
+ *   tms_vocab_clear_cache TokenMask::clear_cache (gbnf.h:850)
+ */
+typedef struct tms_grammar tms_grammar;
+typedef struct tms_gstate tms_gstate;
+typedef struct tms_vocab tms_vocab;
+
+tms_grammar* tms_grammar_parse(const char* text, size_t len, char* err, size_t err_cap);
+void tms_grammar_free(tms_grammar* g);
+int tms_grammar_rule_count(const tms_grammar* g);
+tms_gstate* tms_grammar_start(tms_grammar* g);
+int tms_grammar_advance(tms_grammar* g, tms_gstate* s, unsigned char byte);
+int tms_grammar_can_end(const tms_grammar* g, const tms_gstate* s);
+int tms_grammar_accepts(tms_grammar* g, const char* text, size_t len);
+tms_gstate* tms_gstate_copy(const tms_gstate* s);
+void tms_gstate_free(tms_gstate* s);
+int tms_gstate_equal(const tms_gstate* a, const tms_gstate* b);
+tms_vocab* tms_vocab_create(tms_grammar* g, const char* const* text, const size_t* len,
+                            int n_tokens, int eos, const unsigned char* skip);
+void tms_vocab_free(tms_vocab* v);
+int tms_vocab_node_count(const tms_vocab* v);
+int tms_vocab_allowed(tms_vocab* v, const tms_gstate* s, int32_t* ids, int cap);
+int tms_vocab_mask(tms_vocab* v, const tms_gstate* s, uint32_t* words, int n_words);
+int tms_vocab_consume(tms_vocab* v, tms_grammar* g, tms_gstate* s, int id);
+void tms_vocab_clear_cache(tms_vocab* v);
+
+/*
  * Test hooks.  Run the device Philox4x32-10 on n (counter[4], key[2])
  * tuples packed as 6 words each and write 4 words each; evaluate the device
  * double exp on n inputs (which = 0: the HIP math library, 1: the

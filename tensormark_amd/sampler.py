@@ -40,6 +40,23 @@ EXPORTS = (
     "tms_host_repeat_penalty",
     "tms_host_no_repeat_ngram",
     "tms_host_dry",
+    "tms_grammar_parse",
+    "tms_grammar_free",
+    "tms_grammar_rule_count",
+    "tms_grammar_start",
+    "tms_grammar_advance",
+    "tms_grammar_can_end",
+    "tms_grammar_accepts",
+    "tms_gstate_copy",
+    "tms_gstate_free",
+    "tms_gstate_equal",
+    "tms_vocab_create",
+    "tms_vocab_free",
+    "tms_vocab_node_count",
+    "tms_vocab_allowed",
+    "tms_vocab_mask",
+    "tms_vocab_consume",
+    "tms_vocab_clear_cache",
 )
 
 
@@ -148,6 +165,33 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
                                      C.c_int, C.c_void_p]
         for f in (lib.tms_host_repeat_penalty, lib.tms_host_no_repeat_ngram, lib.tms_host_dry):
             f.restype = None
+        vp = C.c_void_p
+        lib.tms_grammar_parse.restype = vp
+        lib.tms_grammar_parse.argtypes = [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t]
+        lib.tms_grammar_free.argtypes = [vp]
+        lib.tms_grammar_free.restype = None
+        lib.tms_grammar_rule_count.argtypes = [vp]
+        lib.tms_grammar_start.restype = vp
+        lib.tms_grammar_start.argtypes = [vp]
+        lib.tms_grammar_advance.argtypes = [vp, vp, C.c_ubyte]
+        lib.tms_grammar_can_end.argtypes = [vp, vp]
+        lib.tms_grammar_accepts.argtypes = [vp, C.c_char_p, C.c_size_t]
+        lib.tms_gstate_copy.restype = vp
+        lib.tms_gstate_copy.argtypes = [vp]
+        lib.tms_gstate_free.argtypes = [vp]
+        lib.tms_gstate_free.restype = None
+        lib.tms_gstate_equal.argtypes = [vp, vp]
+        lib.tms_vocab_create.restype = vp
+        lib.tms_vocab_create.argtypes = [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t), C.c_int,
+                                         C.c_int, vp]
+        lib.tms_vocab_free.argtypes = [vp]
+        lib.tms_vocab_free.restype = None
+        lib.tms_vocab_node_count.argtypes = [vp]
+        lib.tms_vocab_allowed.argtypes = [vp, vp, vp, C.c_int]
+        lib.tms_vocab_mask.argtypes = [vp, vp, vp, C.c_int]
+        lib.tms_vocab_consume.argtypes = [vp, vp, vp, C.c_int]
+        lib.tms_vocab_clear_cache.argtypes = [vp]
+        lib.tms_vocab_clear_cache.restype = None
         _LIB = lib
     return _LIB
 

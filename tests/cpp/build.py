@@ -18,7 +18,7 @@ OUT = os.path.join(HERE, "_build", "host_api_check")
 def build(verbose: bool = False) -> str:
     os.makedirs(os.path.dirname(OUT), exist_ok=True)
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
-    cmd = [os.path.join(rocm, "bin", "hipcc"), "-std=c++17", "-O2", "-Wall",
+    cmd = [os.path.join(rocm, "bin", "hipcc"), "--offload-arch=gfx950", "-std=c++17", "-O2", "-Wall",
            "-I", os.path.join(ROOT, "include"),
            "-o", OUT + ".tmp", os.path.join(HERE, "host_api_check.cpp"),
            "-L", os.path.join(ROOT, "tensormark_amd"), "-ltmsample_hip",

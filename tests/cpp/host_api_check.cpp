@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../oracle/tms_oracle.h"
+#include "tmgbnf_amd.hpp"
 #include "tmsample_amd.hpp"
 
 namespace {
@@ -28,12 +29,16 @@ void expect(bool ok, const char* what, int c) {
     }
 }
 
+std::mt19937_64 g64(int a, int b) { return std::mt19937_64(static_cast<uint64_t>(a) * 1000003u + b); }
+
 std::vector<float> make_row(std::mt19937_64& g, int V, float sd) {
     std::normal_distribution<float> n(0.0f, sd);
     std::vector<float> x(static_cast<size_t>(V));
     for (float& v : x) v = n(g);
     return x;
 }
+
+std::vector<float> make_row(std::mt19937_64&& g, int V, float sd) { return make_row(g, V, sd); }
 
 tmo_row_params oracle_params(const tmsample_amd::Opts& o, bool greedy) {
     tmo_row_params p{};
@@ -136,6 +141,55 @@ int main() {
         const int got = s.sample_token(mine, V, o, false, r2, hist.data(), n);
         expect(got == want, "sample_token (DRY): token", c);
         expect(r1 == r2, "sample_token (DRY): generator state", c);
+    }
+
+    // Constrained decoding: the grammar engine's mask restricts each GPU draw;
+    // every sampled id must be allowed, and a sequence ending in EOS must be a
+    // sentence of the grammar.
+    {
+        const char* gtext = R"(root ::= "{" ws pair ("," ws pair)* "}"
+pair ::= "\"" [a-z]+ "\"" ":" ws num
+num  ::= "-"? [0-9]+
+ws   ::= " "?)";
+        const auto g = tmgbnf_amd::Grammar::parse(gtext);
+        std::vector<std::string> vocab = {"{", "}", ",", ":", " ", "\"", "-", "\"a\"", "\"key\":",
+                                          "0", "1", "12", "345", "x", "ab", "z", "{\"", "\":",
+                                          "}}", ", ", "9"};
+        const int eos = static_cast<int>(vocab.size());
+        const int V = eos + 1;
+        tmgbnf_amd::TokenMask tm(g, vocab, eos);
+        int finished = 0;
+        for (int seq = 0; seq < 12; ++seq, ++c) {
+            auto st = g.start();
+            std::string text;
+            std::mt19937 rng(static_cast<unsigned>(900 + seq));
+            bool ok = true, ended = false;
+            for (int step = 0; step < 40 && ok; ++step) {
+                std::vector<uint32_t> words(static_cast<size_t>((V + 31) / 32));
+                const int n_allowed = tm.mask(st, words.data(), static_cast<int>(words.size()));
+                std::vector<float> row = make_row(g64(seq, step), V, 1.5f);
+                tmsample_amd::ChatOpts o;
+                o.temperature = 1.0f;
+                o.top_k = 40;
+                o.top_p = 1.0f;
+                const int tok = s.sample_token(row, V, o, false, rng, nullptr, 0, words.data());
+                const bool allowed = n_allowed > 0 && ((words[tok >> 5] >> (tok & 31)) & 1u);
+                ok = allowed;
+                if (!allowed) break;
+                if (tok == eos) {
+                    ended = true;
+                    break;
+                }
+                text += vocab[static_cast<size_t>(tok)];
+                ok = tm.consume(st, tok);
+            }
+            expect(ok, "constrained decode: every sampled id allowed and consumed", c);
+            if (ended) {
+                ++finished;
+                expect(g.accepts(text), "constrained decode: EOS ends a sentence of the grammar", c);
+            }
+        }
+        expect(finished > 0, "constrained decode: some sequence reached EOS", c++);
     }
 
     // Errors surface as exceptions with the row status.
