@@ -55,6 +55,7 @@ constexpr int kRankLists = 16;             // chunk lists ranked in registers by
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
 constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per list
+constexpr int kReadRounds = 64;            // bound on the merger's re-reads of a sample
 
 enum : int { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_TOPP = 2 };
 enum : int { FLAG_NONFINITE = 1, FLAG_OVERFLOW = 2 };
@@ -965,7 +966,10 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     const int R1 = r + 1;   // words per list in uni: header, r entries
     const bool spec = r > 0;
     uint64_t* uni = sm.big.m.uni;
-    if (t == 0) sm.theta = 0;   // lists to poll again (bit per list)
+    if (t == 0) {
+        sm.theta = 0;     // lists to read again (bit per list)
+        sm.misc[3] = 0;   // a list never arrived
+    }
     if (spec) {
         for (int idx = t; idx < S * R1; idx += kBlock) {
             const int cc = idx / R1, jj = idx - cc * R1;
@@ -978,14 +982,46 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             uni[idx] = v;
         }
         __syncthreads();
-        for (int idx = t; idx < S * R1; idx += kBlock) {
-            const int cc = idx / R1, jj = idx - cc * R1;
-            const uint64_t h = uni[cc * R1];
-            const int m = min((int)(uint32_t)h, r);
-            if (!(h & kReady) || (jj >= 1 && jj <= m && uni[idx] == 0))
-                atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
+        // Validate; lists read before they were complete are read again in
+        // rounds: wave 0 waits (bounded) for their ready headers, then every
+        // thread re-reads their sampled entries at once.
+        for (int round = 0;; ++round) {
+            for (int idx = t; idx < S * R1; idx += kBlock) {
+                const int cc = idx / R1, jj = idx - cc * R1;
+                const uint64_t h = uni[cc * R1];
+                const int m = min((int)(uint32_t)h, r);
+                if (!(h & kReady) || (jj >= 1 && jj <= m && uni[idx] == 0))
+                    atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
+            }
+            __syncthreads();
+            const uint64_t redo = sm.theta;
+            if (redo == 0 || sm.misc[3]) break;
+            if (round == kReadRounds) {
+                if (t == 0) sm.misc[3] = 1;
+                __syncthreads();
+                break;
+            }
+            __syncthreads();   // every thread has read theta
+            if (t == 0) sm.theta = 0;
+            if (wv == 0 && lane < S && ((redo >> lane) & 1)) {
+                uint64_t h = 0;
+                for (int it = 0; it < kPollCap; ++it) {
+                    h = ld_agent(&row_lists[(int64_t)lane * kListStride]);
+                    if (h & kReady) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                uni[lane * R1] = h;
+                if (!(h & kReady)) sm.misc[3] = 1;
+            }
+            __syncthreads();
+            for (int idx = t; idx < S * R1; idx += kBlock) {
+                const int cc = idx / R1, jj = idx - cc * R1;
+                if (jj == 0 || !((redo >> cc) & 1)) continue;
+                if (jj <= min((int)(uint32_t)uni[cc * R1], r))
+                    uni[idx] = ld_agent(&row_lists[(int64_t)cc * kListStride + jj]);
+            }
+            __syncthreads();
         }
-        __syncthreads();
     } else {
         // Headers only; whole lists are read below.
         if (t < S) {
@@ -998,9 +1034,8 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     }
     const int HW = spec ? R1 : 1;   // stride of the headers in uni
     if (wv == 0) {
-        // Poll the lists that were not complete, then read their sample.
-        int timed_out = 0;
-        const uint64_t redo = sm.theta;
+        // Headers-only mode: wait (bounded) for the lists not yet complete.
+        const uint64_t redo = spec ? 0ull : sm.theta;
         if (lane < S && ((redo >> lane) & 1)) {
             uint64_t h = 0;
             for (int it = 0; it < kPollCap; ++it) {
@@ -1008,16 +1043,8 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 if (h & kReady) break;
                 __builtin_amdgcn_s_sleep(1);
             }
-            if (h & kReady) {
-                uni[lane * HW] = h;
-                if (spec) {
-                    const int m = min((int)(uint32_t)h, r);
-                    for (int jj = 1; jj <= m; ++jj)
-                        uni[lane * R1 + jj] = ld_agent(&row_lists[(int64_t)lane * kListStride + jj]);
-                }
-            } else {
-                timed_out = 1;
-            }
+            uni[lane * HW] = h;
+            if (!(h & kReady)) sm.misc[3] = 1;
         }
         int n_c = 0, f_c = 0, m_c = 0;
         if (lane < S) {
@@ -1032,11 +1059,9 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         int fo = f_c;
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) fo |= __shfl_xor(fo, m, 64);
-        const int to = __any(timed_out);
         if (lane == 0) {
             sm.misc[5] = N;
             sm.misc[4] = fo;
-            sm.misc[3] = to;
             sm.misc[1] = 0;   // "a list ran out"
         }
     }
