@@ -25,10 +25,10 @@
 // instructions and are issued unconditionally (clamped addresses, an all-ones
 // mask row when the caller gives none), so each slot is processed as it
 // lands; the history penalties are applied in a second pass once the window
-// counts are in LDS.  The workgroup then takes a ticket from the row's
-// arrival counter and selects its candidates while the ticket's atomic is in
-// flight.  The last ticket holder merges; the others publish their list and
-// set a ready bit in its header.  All cross-workgroup words are relaxed
+// counts are in LDS.  The workgroup then selects its candidates and takes a
+// ticket from the row's arrival counter.  The last ticket holder merges; the
+// others publish their list and set a ready bit in its header.  All
+// cross-workgroup words are relaxed
 // agent-scope atomics, coherent across the XCDs' L2 caches, with stores
 // drained (s_waitcnt) before the header that announces them; the merger's
 // wait for the headers is bounded.
@@ -386,12 +386,11 @@ __device__ __forceinline__ int larger_in_lists(const uint64_t* L, int stride, in
     return c;
 }
 
-// Zero the published lists of a row (header and entries of every chunk but
-// `own`), threads tid0 .. nthr-1 of the workgroup.
-__device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, int own, const int* list_n,
+// Zero the published lists of a row (header and entries of every chunk),
+// threads tid0 .. nthr-1 of the workgroup.
+__device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, const int* list_n,
                                            int tid0, int nthr) {
     for (int cc = 0; cc < S; ++cc) {
-        if (cc == own) continue;
         const int nw = 1 + list_n[cc];
         for (int jj = tid0; jj < nw; jj += nthr)
             st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
@@ -727,13 +726,6 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 #pragma unroll
     for (int j = 1; j < NVT; ++j) tmax = fmaxf(tmax, vmax[j]);
 
-    // ---- ticket: the row's last workgroup to get here merges.  The atomic's
-    //      result is first needed after the selection.
-    uint32_t ticket = 0;
-    if (t == 0)
-        ticket = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-
     // ---- selection: the chunk's candidates, sorted, into sm.cand[0..nout).
     int flags = 0;
     int nout = 0;
@@ -938,29 +930,33 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         }
     }
 
-    // ---- publish, or merge.
-    if (t == 0) sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
-    __syncthreads();
+    // ---- publish, then take a ticket: the row's last workgroup to publish
+    //      merges, and every other list is complete by then.
     uint64_t* row_lists = a.lists + (int64_t)row * S * kListStride;
-    if (!sm.misc[0]) {
-        if (wv == 0) {
-            uint64_t* my_list = row_lists + (int64_t)c * kListStride;
-            for (int i = lane; i < nout; i += 64) st_agent(&my_list[1 + i], sm.cand[i]);
-            __builtin_amdgcn_s_waitcnt(0);   // entries complete before the header
-            if (lane == 0)
-                st_agent(&my_list[0], kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout);
+    if (wv == 0) {
+        uint64_t* my_list = row_lists + (int64_t)c * kListStride;
+        for (int i = lane; i < nout; i += 64) st_agent(&my_list[1 + i], sm.cand[i]);
+        __builtin_amdgcn_s_waitcnt(0);   // entries complete before the header
+        if (lane == 0) {
+            st_agent(&my_list[0], kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout);
+            __builtin_amdgcn_s_waitcnt(0);   // the header before the ticket
+            const uint32_t ticket = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+            sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
         }
-        return;
     }
+    __syncthreads();
+    if (!sm.misc[0]) return;
 
     // ================= merge: the last workgroup of the row =================
-    // Top-k rows read a sample, each list's header and first r entries
-    // (r ~ 2K/S), in one speculative round: a list whose header is not yet
-    // ready, or whose entries still read 0 (the merger of the previous call
-    // zeroed every word it consumed; keys are never 0), is polled again,
-    // boundedly.  The K best of the sample are the row's K best unless some
-    // list's last sampled entry is among them while the list holds more;
-    // only then, and for top-p rows, are whole lists merged.
+    // Top-k rows read each list's header and first r entries (r = K where
+    // it fits) in one round.  Every list was published before its ticket,
+    // so that round normally finds them complete; a header not yet ready or
+    // an entry still 0 (the merger of the previous call zeroed every word it
+    // consumed; keys are never 0) is read again, boundedly.  The K best of
+    // the sample are the row's K best unless some list's last sampled entry
+    // is among them while the list holds more; only then, and for top-p
+    // rows, are whole lists merged.
     if (t == 0) st_agent(&a.counters[row], 0u);   // ready for the next launch
     const int r = (mode == MODE_TOPP || S > kRankLists) ? 0 : min(K, kUni / S - 1);
     const int R1 = r + 1;   // words per list in uni: header, r entries
@@ -1207,7 +1203,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     // back to zero for the next call; on a top-k row's success path waves
     // 1-3 do it while wave 0 runs the tail.
     const bool defer_zero = status == TMS_ROW_OK && mode == MODE_TOPK && !sm.misc[3];
-    if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, c, sm.list_n, t, kBlock);
+    if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, sm.list_n, t, kBlock);
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
         return;
@@ -1245,7 +1241,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     }
     const float mx = ckey_val(srt[0]);
     if (mx == __builtin_huge_valf()) {
-        if (defer_zero) zero_lists(row_lists, S, c, sm.list_n, t, kBlock);
+        if (defer_zero) zero_lists(row_lists, S, sm.list_n, t, kBlock);
         write_row_error(a, row, TMS_ROW_NONFINITE);
         return;
     }
@@ -1253,7 +1249,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         if (wv == 0)
             tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand);
         else
-            zero_lists(row_lists, S, c, sm.list_n, t - 64, kBlock - 64);
+            zero_lists(row_lists, S, sm.list_n, t - 64, kBlock - 64);
         return;
     }
     // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
