@@ -24,8 +24,11 @@
 // Timeline of a workgroup: the stream's loads are the kernel's first
 // instructions and are issued unconditionally (clamped addresses, an all-ones
 // mask row when the caller gives none), so each slot is processed as it
-// lands; the history penalties are applied in a second pass once the window
-// counts are in LDS.  The workgroup then selects its candidates and takes a
+// lands.  The history window is counted in LDS before the stream lands: each
+// penalised entry is masked out of the stream like a grammar-masked one and
+// comes back as an extra candidate from the thread that counted its id first
+// (that thread read the logit separately and applies the compounding penalty
+// once).  The workgroup then selects its candidates and takes a
 // ticket from the row's arrival counter.  The last ticket holder merges; the
 // others publish their list and set a ready bit in its header.  All
 // cross-workgroup words are relaxed
@@ -115,6 +118,7 @@ struct Smem {
     } big;
     uint64_t cand[kCand];
     uint32_t tkey[kBlock];         // order keys of the thread maxima
+    uint32_t pbits[2 * kBlock];    // per thread: its penalised entries (bit = slot * VEC + e)
     int wave_i[kWaves];
     uint64_t wave_k[kWaves];
     float wave_f[kWaves];
@@ -596,6 +600,13 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 #pragma unroll
         for (int i = 0; i < kWin; ++i) wid[i] = hist[min(t + i * kBlock, rs - 1)];
     }
+    // Row parameters: scalar loads, independent of the vector stream.
+    const tms_row_params P = a.params[row];
+    int nrec = 0;
+    if (a.recent) {
+        nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
+        if (nrec > (int)a.recent_stride) nrec = (int)a.recent_stride;
+    }
     __builtin_amdgcn_sched_barrier(0);
     const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
     const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
@@ -616,7 +627,59 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    const tms_row_params P = a.params[row];
+    // ---- history penalties, before the stream lands.  Every window id in
+    //      this chunk is counted in LDS; the thread that counts an id first
+    //      owns it: it marks the entry in its holder's bit set (pass 1 then
+    //      masks it like a grammar-masked entry) and, after pass 1, applies
+    //      the penalty to the logit it read for it and carries the result as
+    //      an extra candidate.  Windows past kWin * kBlock positions take the
+    //      register pass below instead.
+    Pen pn;
+    pn.rep_on = !(P.repeat_penalty <= 1.0f);
+    pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
+    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
+    pn.rep = P.repeat_penalty;
+    pn.freq = P.frequency_penalty;
+    pn.pres = P.presence_penalty;
+    const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
+    const bool pen_own = pn.on && nrec <= kWin * kBlock;
+    if (pn.on) {
+        uint4* c4 = (uint4*)sm.big.cnt;
+        for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
+        sm.pbits[2 * t] = 0;
+        sm.pbits[2 * t + 1] = 0;
+        __syncthreads();
+    }
+    int own_off[kWin];
+    float own_v[kWin];
+    uint32_t own_m[kWin];
+    uint64_t penbits = 0;
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) own_off[i] = -1;
+    if (pen_own) {
+#pragma unroll
+        for (int i = 0; i < kWin; ++i) {
+            const int p = t + i * kBlock;
+            const int id = (p >= from && p < nrec) ? wid[i] : -1;
+            const bool in = id >= e0 && id < e1;
+            const int off = in ? id - e0 : 0;
+            // read for every slot (clamped): the logit and its mask word
+            own_v[i] = Elt<T>::scalar(base + e0 + off);
+            own_m[i] = mrow[(e0 + off) >> 5];
+            if (in) {
+                const uint32_t sh = (off & 1) * 16;
+                const uint32_t old = atomicAdd(&sm.big.cnt[off >> 1], 1u << sh);
+                if (((old >> sh) & 0xFFFFu) == 0) {
+                    own_off[i] = off;
+                    const int vv = off / VEC;
+                    const int bit = (vv / kBlock) * VEC + off % VEC;
+                    atomicOr(&sm.pbits[2 * (vv % kBlock) + (bit >> 5)], 1u << (bit & 31));
+                }
+            }
+        }
+        __syncthreads();
+        penbits = ((uint64_t)sm.pbits[2 * t + 1] << 32) | sm.pbits[2 * t];
+    }
 
     // ---- pass 1, as each slot lands: widen, mask, NaN/+inf check, slot max.
     float x[kEpt];
@@ -633,7 +696,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) f[e] = sx[j * VEC + e];
         }
-        const uint32_t mb = (v < nvec) ? (mw[j] >> (eb & 31)) : 0u;
+        const uint32_t mb = (v < nvec) ? ((mw[j] >> (eb & 31)) & ~(uint32_t)(penbits >> (j * VEC))) : 0u;
         float vm = NEG_INF;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
@@ -658,30 +721,34 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     const int mode = greedy ? MODE_GREEDY : (K <= kTopkFast ? MODE_TOPK : MODE_TOPP);
     const float temp = P.temperature;
     const bool divide = !greedy && temp != 1.0f;
-    int nrec = 0;
-    if (a.recent) {
-        nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
-        if (nrec > (int)a.recent_stride) nrec = (int)a.recent_stride;
-    }
-    Pen pn;
-    pn.rep_on = !(P.repeat_penalty <= 1.0f);
-    pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
-    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
-    pn.rep = P.repeat_penalty;
-    pn.freq = P.frequency_penalty;
-    pn.pres = P.presence_penalty;
-    const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
-    if (pn.on) {
-        uint4* c4 = (uint4*)sm.big.cnt;
-        for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
-    }
     if (t == 0) sm.ncand = 0;
 
-    // ---- pass 2: history penalties from the window counts.
-    if (pn.on) {
-        __syncthreads();   // counts cleared
-        // Positions [0, kWin * kBlock) came with the stream; later ones (long
-        // histories only) are read now.
+    // ---- the owned penalised entries: count, mask bit, penalty.
+    float xo[kWin];
+    uint32_t io[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) {
+        xo[i] = NEG_INF;
+        io[i] = 0;
+        if (own_off[i] >= 0) {
+            const int off = own_off[i];
+            const uint32_t cnt = (sm.big.cnt[off >> 1] >> ((off & 1) * 16)) & 0xFFFFu;
+            const bool allowed = (own_m[i] >> ((e0 + off) & 31)) & 1u;
+            float g = allowed ? own_v[i] : NEG_INF;
+            nonfinite |= __builtin_amdgcn_class(g, 0x203);
+            if (allowed) {
+                g = apply_pen(g, cnt, pn);
+                nonfinite |= __builtin_amdgcn_class(g, 0x203);
+            }
+            xo[i] = g;
+            io[i] = (uint32_t)(e0 + off);
+        }
+    }
+
+    // ---- pass 2 (long windows only): history penalties from the counts.
+    if (pn.on && !pen_own) {
+        // Positions [0, kWin * kBlock) came with the stream; later ones are
+        // read now.
         for (int p0 = 0; p0 < nrec; p0 += kBlock * kWin) {
 #pragma unroll
             for (int i = 0; i < kWin; ++i) {
@@ -725,6 +792,8 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     float tmax = vmax[0];
 #pragma unroll
     for (int j = 1; j < NVT; ++j) tmax = fmaxf(tmax, vmax[j]);
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) tmax = fmaxf(tmax, xo[i]);
 
     // ---- selection: the chunk's candidates, sorted, into sm.cand[0..nout).
     int flags = 0;
@@ -740,6 +809,11 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                     f != NEG_INF ? ckey(f, (uint32_t)(e0 + (t + j * kBlock) * VEC + e)) : 0ull;
                 gb = k > gb ? k : gb;
             }
+        }
+#pragma unroll
+        for (int i = 0; i < kWin; ++i) {
+            const uint64_t k = xo[i] != NEG_INF ? ckey(xo[i], io[i]) : 0ull;
+            gb = k > gb ? k : gb;
         }
         gb = wave_max_u64_dpp(gb);
         const bool nf = __any(nonfinite != 0);
@@ -842,6 +916,18 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                     }
                 }
             }
+#pragma unroll
+            for (int i = 0; i < kWin; ++i) {
+                const bool p = xo[i] >= thr;
+                const uint64_t m = __ballot(p);
+                if (m) {
+                    const int pos = wcnt + __builtin_amdgcn_mbcnt_hi(
+                                               (uint32_t)(m >> 32),
+                                               __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                    if (p && pos < kSeg) seg[pos] = ((uint64_t)__float_as_uint(xo[i]) << 32) | io[i];
+                    wcnt += __popcll(m);
+                }
+            }
             if (lane == 0) sm.wave_i[wv] = wcnt;
             __syncthreads();
             int cw[kWaves];
@@ -870,6 +956,13 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                                                    (uint32_t)(e0 + (t + j * kBlock) * VEC + e);
                             }
                         }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < kWin; ++i) {
+                    if (xo[i] >= thr) {
+                        const int pos = atomicAdd(&sm.ncand, 1);
+                        if (pos < kCand) sm.cand[pos] = ((uint64_t)__float_as_uint(xo[i]) << 32) | io[i];
                     }
                 }
                 __syncthreads();
