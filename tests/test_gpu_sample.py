@@ -170,6 +170,7 @@ EDGE = {
     "topk_gt_V": dict(),
     "tiny_temp": dict(),
     "big_window": dict(),
+    "owned_window": dict(),
     "unaligned_V": dict(),
     "small_V": dict(),
     "top_p_one": dict(),
@@ -218,6 +219,21 @@ def _edge_case(name, rng):
         p["repeat_last_n"] = [2000, 1500, 10, 0]
         p["frequency_penalty"] = 0.05
         p["presence_penalty"] = 0.3
+    elif name == "owned_window":
+        # <= 1024 history ids: penalties through the id owners; heavy
+        # repeats, penalised ids the mask hides, ids past V
+        recent = rng.integers(0, 60, (4, 1000)).astype(np.int32)
+        recent[:, ::5] = 19999
+        recent[:, 1::97] = V + 3
+        x[:, :60] += 7.0
+        bits = np.ones((4, ((V + 31) // 32) * 32), bool)
+        bits[:, 10:20] = False
+        mask = workloads.pack_bits(bits)
+        p["repeat_penalty"] = [1.3, 1.05, 2.0, 1.0]
+        p["repeat_last_n"] = [1000, 400, 1, 64]
+        p["frequency_penalty"] = [0.05, 0.0, -0.5, 0.2]
+        p["presence_penalty"] = [0.3, 0.0, 0.1, 0.1]
+        p["greedy"] = [0, 0, 1, 0]
     elif name == "unaligned_V":
         V = 20001
         x = rng.normal(0, 2, (4, V)).astype(np.float32)
