@@ -54,7 +54,7 @@ constexpr int kListStride = kCand + 2;     // u64 per published list: header + e
 constexpr int kUni = 2048;                 // merge staging (u64)
 constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
-constexpr int kRankLists = 16;             // chunk lists ranked in registers by the merge
+constexpr int kRankLists = 16;             // most chunk lists the sampled merge reads in one round
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
 constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per list
@@ -358,38 +358,6 @@ __device__ __forceinline__ int count_gt_fixed(const uint64_t* L, int n, uint64_t
 // sum at step i in a register.  The partial sums only grow (the terms are
 // >= 0), so the top-p cut and the drawn index are counts of partial sums
 // below the threshold.
-// Number of keys larger than k in the sorted (descending) lists 0..S-1 other
-// than `skip`; list o holds n[o] keys at L[o * stride + 1 ...].  Binary
-// searches over all lists in lockstep: each step issues every list's read
-// before any compare, and the updates are selects, so the reads overlap.
-template <int NL>
-__device__ __forceinline__ int larger_in_lists(const uint64_t* L, int stride, int S, int skip,
-                                               int steps, uint64_t k, const int* n) {
-    int lo[NL], hi[NL];
-#pragma unroll
-    for (int o = 0; o < NL; ++o) {
-        lo[o] = 0;
-        hi[o] = (o < S && o != skip) ? n[o] : 0;
-    }
-    for (int st = 0; st < steps; ++st) {
-        uint64_t v[NL];
-#pragma unroll
-        for (int o = 0; o < NL; ++o) v[o] = L[o * stride + 1 + ((lo[o] + hi[o]) >> 1)];
-#pragma unroll
-        for (int o = 0; o < NL; ++o) {
-            const int mid = (lo[o] + hi[o]) >> 1;
-            const bool live = lo[o] < hi[o];
-            const bool gt = v[o] > k;
-            lo[o] = (live && gt) ? mid + 1 : lo[o];
-            hi[o] = (live && !gt) ? mid : hi[o];
-        }
-    }
-    int c = 0;
-#pragma unroll
-    for (int o = 0; o < NL; ++o) c += lo[o];
-    return c;
-}
-
 // Zero the published lists of a row (header and entries of every chunk),
 // threads tid0 .. nthr-1 of the workgroup.
 __device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, const int* list_n,
@@ -401,37 +369,60 @@ __device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, const int
     }
 }
 
-// Left-to-right sum of v[0..n), as a scalar loop computes it.
-__device__ __forceinline__ double seq_sum(const double* v, int n) {
+// Sixteen doubles from LDS (16-byte reads; v + i 16-byte aligned).
+__device__ __forceinline__ void ld16(const double* v, int i, double (&c)[16]) {
+    const double2* v2 = (const double2*)(v + i);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const double2 d = v2[u];
+        c[2 * u] = d.x;
+        c[2 * u + 1] = d.y;
+    }
+}
+
+// Left-to-right prefix sums of v[0..n) as a scalar loop computes them; v
+// holds zeros from n up to the next multiple of 16 (x + 0.0 == x for
+// x >= 0).  Lane 0 stores every prefix to pre[] (off the dependent chain);
+// returns the total.
+__device__ __forceinline__ double seq_prefix_sums(const double* v, int n, double* pre) {
     double s = 0.0;
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) s += v[i];
+    for (int i = 0; i < n; i += 16) {
+        double c[16];
+        ld16(v, i, c);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            s += c[e];
+            c[e] = s;
+        }
+        if ((threadIdx.x & 63) == 0) {
+            double2* p2 = (double2*)(pre + i);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) p2[u] = make_double2(c[2 * u], c[2 * u + 1]);
+        }
+    }
     return s;
 }
 
 // First i in [0, n) whose left-to-right prefix sum v[0] + ... + v[i] is >=
-// thr, or n (v >= 0, so the prefixes never decrease).  Eight prefixes at a
-// time stay in registers; the chain stops at the block that crosses.
+// thr, or n (v >= 0 and zero-padded as above, so the prefixes never
+// decrease).  Sixteen prefixes at a time stay in registers; the chain stops
+// at the block that crosses.
 __device__ __forceinline__ int first_prefix_ge(const double* v, int n, double thr) {
     double s = 0.0;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-        double c[8];
+    for (int i = 0; i < n; i += 16) {
+        double c[16];
+        ld16(v, i, c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            s += v[i + e];
+        for (int e = 0; e < 16; ++e) {
+            s += c[e];
             c[e] = s;
         }
         if (s >= thr) {
             int below = 0;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) below += c[e] < thr ? 1 : 0;
+            for (int e = 0; e < 16; ++e) below += c[e] < thr ? 1 : 0;
             return i + below;
         }
-    }
-    for (; i < n; ++i) {
-        s += v[i];
-        if (s >= thr) return i;
     }
     return n;
 }
@@ -450,13 +441,15 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
     const bool h0 = lane < n, h1 = lane + 64 < n;
     const double pr0 = h0 ? exp((double)ckey_val(srt[lane]) - mx) : 0.0;
     const double pr1 = h1 ? exp((double)ckey_val(srt[lane + 64]) - mx) : 0.0;
-    if (h0) pr[lane] = pr0;
-    if (h1) pr[lane + 64] = pr1;
+    // pr, q and p in LDS, each zero from n up to a multiple of 16
+    double* zpre = pr + 256;   // the prefixes of z
+    pr[lane] = pr0;
+    pr[lane + 64] = pr1;
     wave_lds_sync();
-    const double z = seq_sum(pr, n);                // tmsample.h:186-191
+    const double z = seq_prefix_sums(pr, n, zpre);   // tmsample.h:186-191
     const double q0 = pr0 / z, q1 = pr1 / z;
-    if (h0) q[lane] = q0;
-    if (h1) q[lane + 64] = q1;
+    q[lane] = q0;
+    q[lane + 64] = q1;
     wave_lds_sync();
     // keep = first index with cum >= top_p, + 1, else K (tmsample.h:192-197;
     // a NaN top_p never compares true).
@@ -477,11 +470,10 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
         // std::discrete_distribution over pr[0..keep): sum = accumulate(),
         // p = pr / sum, partial sums with the last forced to 1, then
         // lower_bound(u) = the first j < keep - 1 with cp_j >= u, else keep - 1.
-        const double sum = seq_sum(pr, keep);
+        const double sum = zpre[keep - 1];
         const double p0 = pr0 / sum, p1 = pr1 / sum;
-        wave_lds_sync();
-        if (h0) pr[lane] = p0;
-        if (h1) pr[lane + 64] = p1;
+        pr[lane] = lane < keep - 1 ? p0 : 0.0;
+        pr[lane + 64] = lane + 64 < keep - 1 ? p1 : 0.0;
         wave_lds_sync();
         tokidx = first_prefix_ge(pr, keep - 1, u);
     }
@@ -1181,58 +1173,54 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             const uint64_t kth = (lane < S && ls >= K) ? uni[lane * R1 + K] : 0ull;
             const uint64_t mth = lane >= S ? ~0ull : (ls >= m ? uni[lane * R1 + m] : 0ull);
             const uint64_t tau = max(wave_max_u64_dpp(kth), ~wave_max_u64_dpp(~mth));
-            if (lane == 0) {
-                sm.theta = tau;
-                sm.ncand = 0;
+            // Each sorted list's keys >= tau are a prefix: its length by
+            // binary search, its place among the candidates by a scan.
+            int p = 0;
+            if (lane < S) {
+                int hi = ls;
+                while (p < hi) {
+                    const int mid = (p + hi) >> 1;
+                    if (uni[lane * R1 + 1 + mid] >= tau) p = mid + 1;
+                    else hi = mid;
+                }
             }
-        }
-        __syncthreads();
-        const uint64_t tau = sm.theta;
-        for (int idx = t; idx < S * R1; idx += kBlock) {
-            const int cc = idx / R1, jj = idx - cc * R1;
-            const uint64_t k = uni[idx];
-            const bool in = jj >= 1 && jj <= sm.list_s[cc] && k >= tau;
-            const uint64_t bal = __ballot(in);
-            int base = 0;
-            if (lane == 0 && bal) base = atomicAdd(&sm.ncand, __popcll(bal));
-            base = __shfl(base, 0, 64);
-            if (in) {
-                const int pos = base + (int)__builtin_amdgcn_mbcnt_hi(
-                    (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-                // cand keeps the key; list and position ride in surv's tail.
-                sm.cand[pos < kCand ? pos : 0] = k;
-                if (pos < kCand) sm.big.m.surv[kUni - 1 - pos] = ((uint64_t)cc << 32) | (uint32_t)jj;
+            const int incl = wave_incl_scan_i32(p);
+            const int tot = __shfl(incl, 63, 64);
+            if (lane < S && tot <= kCand) {
+                // Copy the prefix into cand.  A list whose whole sample is
+                // in (only possible when fewer than K entries were sampled)
+                // while it holds more sends the row to the whole-list merge.
+#pragma unroll 4
+                for (int j = 0; j < p; ++j) sm.cand[incl - p + j] = uni[lane * R1 + 1 + j];
+                if (r < K && p == ls && sm.list_n[lane] > ls) sm.misc[1] = 1;
+            }
+            if (lane == 0) {
+                sm.ncand = tot;
+                if (tot > kCand) sm.misc[1] = 1;   // rare (a weak tau): whole lists below
             }
         }
         __syncthreads();
         const int nc = sm.ncand;
         if (nc <= kCand) {
+            // Zero-pad to a multiple of 8 (keys are never 0), then count in
+            // blocks of eight keys read 16 bytes at a time.
+            if (t < 8 && nc + t < kCand) sm.cand[nc + t] = 0ull;
+            __syncthreads();
+            const uint4* c4 = (const uint4*)sm.cand;
             for (int i = t; i < nc; i += kBlock) {
                 const uint64_t k = sm.cand[i];
-                int r0 = 0, r1 = 0, j = 0;
-                for (; j + 1 < nc; j += 2) {
-                    r0 += sm.cand[j] > k ? 1 : 0;
-                    r1 += sm.cand[j + 1] > k ? 1 : 0;
+                int r0 = 0, r1 = 0;
+                for (int j = 0; j < nc; j += 8) {
+                    uint4 q[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) q[u] = c4[(j >> 1) + u];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        r0 += (((uint64_t)q[u].y << 32) | q[u].x) > k ? 1 : 0;
+                        r1 += (((uint64_t)q[u].w << 32) | q[u].z) > k ? 1 : 0;
+                    }
                 }
-                if (j < nc) r0 += sm.cand[j] > k ? 1 : 0;
-                const int rank = r0 + r1;
-                const uint64_t where = sm.big.m.surv[kUni - 1 - i];
-                const int cc = (int)(where >> 32), jj = (int)(uint32_t)where;
-                if (rank < n_acc) srt[rank] = k;
-                if (jj == sm.list_s[cc] && rank < K - 1 && sm.list_n[cc] > sm.list_s[cc]) sm.misc[1] = 1;
-            }
-        } else {
-            // Rare: tau admits most entries (lists shorter than K).
-            const int steps = 32 - __builtin_clz((unsigned)r);   // halvings of [0, r]
-            for (int idx = t; idx < S * R1; idx += kBlock) {
-                const int cc = idx / R1, jj = idx - cc * R1;
-                if (jj == 0 || jj > sm.list_s[cc]) continue;
-                const uint64_t k = uni[idx];
-                const int rank = jj - 1 + (S <= 8 ? larger_in_lists<8>(uni, R1, S, cc, steps, k, sm.list_s)
-                                                  : larger_in_lists<kRankLists>(uni, R1, S, cc, steps, k,
-                                                                                sm.list_s));
-                if (rank < n_acc) srt[rank] = k;
-                if (jj == sm.list_s[cc] && rank < K - 1 && sm.list_n[cc] > sm.list_s[cc]) sm.misc[1] = 1;
+                if (r0 + r1 < n_acc) srt[r0 + r1] = k;
             }
         }
         __syncthreads();
