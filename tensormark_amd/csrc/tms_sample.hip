@@ -227,7 +227,10 @@ __device__ int radix_slow(const T* base, const uint32_t* mrow, int e0, int e1, i
     int remaining = K;
     for (int shift = 24; shift >= 0; shift -= 8) {
         sm.hist[t] = 0;
-        if (t == 0) sm.ncand = 0;
+        if (t == 0) {
+        sm.ncand = 0;
+        sm.misc[2] = 0;   // the merger's read found an incomplete list
+    }
         __syncthreads();
         for (int id = e0 + t; id < e1; id += kBlock) {
             const float v = slow_value(base, mrow, id, e0, pn, sm);
@@ -358,12 +361,12 @@ __device__ __forceinline__ int count_gt_fixed(const uint64_t* L, int n, uint64_t
 // sum at step i in a register.  The partial sums only grow (the terms are
 // >= 0), so the top-p cut and the drawn index are counts of partial sums
 // below the threshold.
-// Zero the published lists of a row (header and entries of every chunk),
-// threads tid0 .. nthr-1 of the workgroup.
-__device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, const int* list_n,
+// Zero the published lists of a row (header, entries and padding up to r of
+// every chunk), threads tid0 .. nthr-1 of the workgroup.
+__device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, int r, const int* list_n,
                                            int tid0, int nthr) {
     for (int cc = 0; cc < S; ++cc) {
-        const int nw = 1 + list_n[cc];
+        const int nw = 1 + max(list_n[cc], r);
         for (int jj = tid0; jj < nw; jj += nthr)
             st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
     }
@@ -713,7 +716,10 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     const int mode = greedy ? MODE_GREEDY : (K <= kTopkFast ? MODE_TOPK : MODE_TOPP);
     const float temp = P.temperature;
     const bool divide = !greedy && temp != 1.0f;
-    if (t == 0) sm.ncand = 0;
+    if (t == 0) {
+        sm.ncand = 0;
+        sm.misc[2] = 0;   // the merger's read found an incomplete list
+    }
 
     // ---- the owned penalised entries: count, mask bit, penalty.
     float xo[kWin];
@@ -933,7 +939,10 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             }
             if (over) {
                 // A wave's segment overflowed: compact again, contiguously.
-                if (t == 0) sm.ncand = 0;
+                if (t == 0) {
+        sm.ncand = 0;
+        sm.misc[2] = 0;   // the merger's read found an incomplete list
+    }
                 __syncthreads();
 #pragma unroll
                 for (int j = 0; j < NVT; ++j) {
@@ -1017,10 +1026,15 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 
     // ---- publish, then take a ticket: the row's last workgroup to publish
     //      merges, and every other list is complete by then.
+    // The merger reads the first r entries of every list at once (top-k and
+    // greedy rows); slots past nout hold key 1, below every real key, so
+    // every word it reads is non-zero once written.
+    const int r = (mode == MODE_TOPP || S > kRankLists) ? 0 : min(K, kUni / S - 1);
     uint64_t* row_lists = a.lists + (int64_t)row * S * kListStride;
     if (wv == 0) {
         uint64_t* my_list = row_lists + (int64_t)c * kListStride;
-        for (int i = lane; i < nout; i += 64) st_agent(&my_list[1 + i], sm.cand[i]);
+        for (int i = lane; i < max(nout, r); i += 64)
+            st_agent(&my_list[1 + i], i < nout ? sm.cand[i] : (uint64_t)1);
         __builtin_amdgcn_s_waitcnt(0);   // entries complete before the header
         if (lane == 0) {
             st_agent(&my_list[0], kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout);
@@ -1043,7 +1057,6 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     // is among them while the list holds more; only then, and for top-p
     // rows, are whole lists merged.
     if (t == 0) st_agent(&a.counters[row], 0u);   // ready for the next launch
-    const int r = (mode == MODE_TOPP || S > kRankLists) ? 0 : min(K, kUni / S - 1);
     const int R1 = r + 1;   // words per list in uni: header, r entries
     const bool spec = r > 0;
     uint64_t* uni = sm.big.m.uni;
@@ -1052,21 +1065,27 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         sm.misc[3] = 0;   // a list never arrived
     }
     if (spec) {
+        // Every word read must be set: a ready header, non-zero entries (the
+        // writer padded its r slots).  Each thread checks its own words.
+        int bad = 0;
         for (int idx = t; idx < S * R1; idx += kBlock) {
             const int cc = idx / R1, jj = idx - cc * R1;
             uint64_t v;
-            if (cc == c)
+            if (cc == c) {
                 v = jj == 0 ? (kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout)
-                            : (jj <= nout ? sm.cand[jj - 1] : 0ull);
-            else
+                            : (jj <= nout ? sm.cand[jj - 1] : 1ull);
+            } else {
                 v = ld_agent(&row_lists[(int64_t)cc * kListStride + jj]);
+                bad |= (jj == 0 ? !(v & kReady) : v == 0) ? 1 : 0;
+            }
             uni[idx] = v;
         }
+        if (__ballot(bad) && lane == 0) atomicOr(&sm.misc[2], 1);
         __syncthreads();
-        // Validate; lists read before they were complete are read again in
-        // rounds: wave 0 waits (bounded) for their ready headers, then every
-        // thread re-reads their sampled entries at once.
-        for (int round = 0;; ++round) {
+        // Lists read before they were complete are read again in rounds:
+        // wave 0 waits (bounded) for their ready headers, then every thread
+        // re-reads their sampled entries at once.
+        for (int round = 0; sm.misc[2]; ++round) {
             for (int idx = t; idx < S * R1; idx += kBlock) {
                 const int cc = idx / R1, jj = idx - cc * R1;
                 const uint64_t h = uni[cc * R1];
@@ -1284,7 +1303,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     // back to zero for the next call; on a top-k row's success path waves
     // 1-3 do it while wave 0 runs the tail.
     const bool defer_zero = status == TMS_ROW_OK && mode == MODE_TOPK && !sm.misc[3];
-    if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, sm.list_n, t, kBlock);
+    if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
         return;
@@ -1322,7 +1341,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     }
     const float mx = ckey_val(srt[0]);
     if (mx == __builtin_huge_valf()) {
-        if (defer_zero) zero_lists(row_lists, S, sm.list_n, t, kBlock);
+        if (defer_zero) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
         write_row_error(a, row, TMS_ROW_NONFINITE);
         return;
     }
@@ -1330,7 +1349,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         if (wv == 0)
             tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand);
         else
-            zero_lists(row_lists, S, sm.list_n, t - 64, kBlock - 64);
+            zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
         return;
     }
     // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
