@@ -85,7 +85,7 @@ def cpu_baseline(w, cfg):
     t0 = time.perf_counter()
     dt, _ = ref.bench(x, 0.7, 40, 0.95, recent=w["recent"], window=256, penalty=1.1,
                       mask=w["mask"], threads=threads, reps=1)
-    reps = max(1, min(200, int(2.0 / max(dt, 1e-4))))
+    reps = max(1, min(5000, int(10.0 / max(dt, 1e-4))))   # about 10 s of host work
     dt, _ = ref.bench(x, 0.7, 40, 0.95, recent=w["recent"], window=256, penalty=1.1,
                       mask=w["mask"], threads=threads, reps=reps)
     wall = time.perf_counter() - t0

@@ -195,6 +195,26 @@ __device__ __forceinline__ int wave_incl_scan_i32(int v) {
     return (int)u;
 }
 
+// Inclusive prefix sums of non-negative doubles across the wave (DPP, a
+// tree of depth 6; lanes without a source add +0.0, which is exact).
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+#define TMS_FSCAN(CTRL, RM, BZ)                                                            \
+    {                                                                                      \
+        const uint64_t b = (uint64_t)__double_as_longlong(v);                              \
+        const uint32_t lo = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)b);                        \
+        const uint32_t hi = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)(b >> 32));                \
+        v += __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));                 \
+    }
+    TMS_FSCAN(0x111, 0xF, true)
+    TMS_FSCAN(0x112, 0xF, true)
+    TMS_FSCAN(0x114, 0xF, true)
+    TMS_FSCAN(0x118, 0xF, true)
+    TMS_FSCAN(0x142, 0xA, false)
+    TMS_FSCAN(0x143, 0xC, false)
+#undef TMS_FSCAN
+    return v;
+}
+
 __device__ __forceinline__ int wave_sum_dpp(int v) {
     return __builtin_amdgcn_readlane(wave_incl_scan_i32(v), 63);
 }
@@ -398,6 +418,16 @@ __device__ __forceinline__ void st_agent(U* p, U v) {
 template <typename U>
 __device__ __forceinline__ U ld_agent(const U* p) {
     return __hip_atomic_load(const_cast<U*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup barrier for LDS traffic only.  __syncthreads() also waits for
+// this wave's global stores still in flight (a device round trip after a
+// store); every exchange between the threads of a workgroup here goes
+// through LDS, so only LDS is ordered.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 }  // namespace tms

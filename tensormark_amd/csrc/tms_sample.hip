@@ -137,7 +137,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int& total, Smem& sm) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int inc = wave_incl_scan_i32(v);
     if (lane == 63) sm.wave_i[w] = inc;
-    __syncthreads();
+    lds_sync();
     int base = 0;
     total = 0;
 #pragma unroll
@@ -146,7 +146,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int& total, Smem& sm) {
         base += i < w ? t : 0;
         total += t;
     }
-    __syncthreads();
+    lds_sync();
     return base + inc - v;
 }
 
@@ -163,12 +163,12 @@ __device__ void sort_cand(int n, Smem& sm) {
             int rank = 0;
 #pragma unroll 8
             for (int j = 0; j < n; ++j) rank += sm.cand[j] > mine ? 1 : 0;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
             __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
             if (t < n) sm.cand[rank] = mine;
         }
-        __syncthreads();
+        lds_sync();
         return;
     }
     constexpr int R = kCand / kBlock;
@@ -191,11 +191,11 @@ __device__ void sort_cand(int n, Smem& sm) {
             for (int r = 0; r < R; ++r) rank[r] += o > mine[r] ? 1 : 0;
         }
     }
-    __syncthreads();
+    lds_sync();
 #pragma unroll
     for (int r = 0; r < R; ++r)
         if (t + r * kBlock < n) sm.cand[rank[r]] = mine[r];
-    __syncthreads();
+    lds_sync();
 }
 
 // The final value of chunk id `id` (mask, then penalties from the LDS
@@ -231,14 +231,14 @@ __device__ int radix_slow(const T* base, const uint32_t* mrow, int e0, int e1, i
         sm.ncand = 0;
         sm.misc[2] = 0;   // the merger's read found an incomplete list
     }
-        __syncthreads();
+        lds_sync();
         for (int id = e0 + t; id < e1; id += kBlock) {
             const float v = slow_value(base, mrow, id, e0, pn, sm);
             if (v == NEG_INF) continue;
             const uint32_t k = okey(divide ? v / temp : v);
             if ((k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 0xFF], 1);
         }
-        __syncthreads();
+        lds_sync();
         const int h = sm.hist[255 - t];   // thread t holds digit 255 - t
         int total;
         const int above = block_excl_scan(h, total, sm);
@@ -250,18 +250,18 @@ __device__ int radix_slow(const T* base, const uint32_t* mrow, int e0, int e1, i
                 const int pos = atomicAdd(&sm.ncand, 1);
                 sm.cand[pos] = ckey(divide ? v / temp : v, (uint32_t)id);
             }
-            __syncthreads();
+            lds_sync();
             return sm.ncand;
         }
         if (above < remaining && above + h >= remaining) {
             sm.misc[0] = 255 - t;
             sm.misc[1] = above;
         }
-        __syncthreads();
+        lds_sync();
         remaining -= sm.misc[1];
         prefix |= (uint32_t)sm.misc[0] << shift;
         pmask |= 0xFFu << shift;
-        __syncthreads();
+        lds_sync();
     }
     // prefix is the K-th largest key; K - remaining keys are strictly greater.
     for (int id = e0 + t; id < e1; id += kBlock) {
@@ -273,7 +273,7 @@ __device__ int radix_slow(const T* base, const uint32_t* mrow, int e0, int e1, i
             sm.cand[pos] = ckey(lg, (uint32_t)id);
         }
     }
-    __syncthreads();
+    lds_sync();
     const int g = sm.ncand;
     // Ties in id order, 256 consecutive ids per step.
     int taken = 0;
@@ -293,7 +293,7 @@ __device__ int radix_slow(const T* base, const uint32_t* mrow, int e0, int e1, i
         if (tie && taken + p < remaining) sm.cand[g + taken + p] = ckey(lg, (uint32_t)id);
         taken += tot;
     }
-    __syncthreads();
+    lds_sync();
     return g + (taken < remaining ? taken : remaining);
 }
 
@@ -325,9 +325,9 @@ __device__ __forceinline__ void write_row_error(const KArgs& a, int row, int sta
 }
 
 __device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
 __device__ __forceinline__ void row_uniform(const KArgs& a, int row, const tms_row_params& P,
@@ -434,8 +434,8 @@ __device__ __forceinline__ int first_prefix_ge(const double* v, int n, double th
 // rows, one wave, n = K <= 2 * 64 sorted entries in srt: pr = exp(lg - mx),
 // z, the top-p and min-p cuts and the std::discrete_distribution draw, with
 // every sum in the reference's order (uniform chains over LDS).
-__device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
-                          int n, int K, double* pr, double* q) {
+__device__ void tail_topk_exact(const KArgs& a, int row, const tms_row_params& P,
+                                const uint64_t* srt, int n, int K, double* pr, double* q) {
     const int lane = threadIdx.x & 63;
     uint32_t w0, w1;
     row_uniform(a, row, P, w0, w1);   // independent of the sums: overlaps them
@@ -495,6 +495,92 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
             if (probs) probs[i] = have ? (float)qq : 0.0f;
         }
     }
+}
+
+// Whether the left-to-right prefix sums of the entries decide "first index
+// k < m whose prefix is >= thr" the same way as the prefixes c (lane k in
+// c0, lane k - 64 in c1) computed by a tree.  For n <= 128 non-negative
+// terms over a total >= 1, the reference's sequential prefixes (and the
+// quotients they sum) and the tree's differ by at most (2n + 24) * 2^-53
+// relative, plus a few subnormal units; the margin below is more than twice
+// that.  Returns false when some prefix up to the decision lies within the
+// margin of thr (or thr is NaN): only the sequential sums decide it.
+__device__ __forceinline__ bool decide_first_ge(double c0, double c1, double thr, int m, int& idx) {
+    const int lane = threadIdx.x & 63;
+    constexpr double kRel = (4.0 * 2 * 64 + 64.0) * 0x1p-53;
+    constexpr double kAbs = 1e-300;
+    const double m0 = (c0 + fabs(thr)) * kRel + kAbs, m1 = (c1 + fabs(thr)) * kRel + kAbs;
+    const bool v0 = lane < m, v1 = lane + 64 < m;
+    const uint64_t g0 = __ballot(v0 && c0 > thr + m0), g1 = __ballot(v1 && c1 > thr + m1);
+    const uint64_t l0 = __ballot(!v0 || c0 < thr - m0), l1 = __ballot(!v1 || c1 < thr - m1);
+    const int first = g0 ? __ffsll((unsigned long long)g0) - 1
+                         : (g1 ? 64 + __ffsll((unsigned long long)g1) - 1 : m);
+    idx = first;
+    const auto below = [](int b) { return b >= 64 ? ~0ull : ((1ull << b) - 1ull); };
+    if (first <= 64) return (l0 | ~below(first)) == ~0ull;
+    return l0 == ~0ull && (l1 | ~below(first - 64)) == ~0ull;
+}
+
+// fp64 tail of tmsample::sample (tensormark/tmsample.h:185-199) for top-k
+// rows, one wave, n = K <= 2 * 64 sorted entries in srt.  The top-p cut and
+// the drawn index are decided from tree prefix sums within a proven error
+// margin of the reference's sequential ones; a decision inside the margin
+// (and any call that returns the per-entry probabilities) takes the
+// sequential path, tail_topk_exact.
+__device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
+                          int n, int K, double* pr, double* q) {
+    if (a.topk_cap && a.out_topk_probs) {
+        tail_topk_exact(a, row, P, srt, n, K, pr, q);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    uint32_t w0, w1;
+    row_uniform(a, row, P, w0, w1);
+    const double u = canonical(w0, w1);
+    const double mx = (double)ckey_val(srt[0]);
+    const bool h0 = lane < n, h1 = lane + 64 < n;
+    const double pr0 = h0 ? exp((double)ckey_val(srt[lane]) - mx) : 0.0;
+    const double pr1 = h1 ? exp((double)ckey_val(srt[lane + 64]) - mx) : 0.0;
+    const double s0 = wave_incl_scan_f64(pr0);
+    const double s1 = wave_incl_scan_f64(pr1) + readlane_f64(s0, 63);
+    const double z = readlane_f64(s1, 63);
+    const double q0 = pr0 / z, q1 = pr1 / z;
+    const double c0 = wave_incl_scan_f64(q0);
+    const double c1 = wave_incl_scan_f64(q1) + readlane_f64(c0, 63);
+    int fi;
+    bool ok = decide_first_ge(c0, c1, (double)P.top_p, n, fi);
+    int kp = fi < n ? fi + 1 : K;
+    if (P.min_p > 0.0f) {
+        const double mp = (double)P.min_p;
+        const uint64_t b0 = __ballot(lane >= 1 && h0 && pr0 < mp);
+        const uint64_t b1 = __ballot(h1 && pr1 < mp);
+        const int m = b0 ? __ffsll((unsigned long long)b0) - 1
+                         : (b1 ? 64 + __ffsll((unsigned long long)b1) - 1 : K);
+        if (m < kp) kp = m;
+    }
+    const int keep = kp;
+    int tokidx = 0;
+    if (ok && keep >= 2) {
+        const int e = keep - 1;   // the sum runs over entries 0 .. keep - 1
+        const double sum = e < 64 ? readlane_f64(s0, e) : readlane_f64(s1, e - 64);
+        const double p0 = lane < keep - 1 ? pr0 / sum : 0.0;
+        const double p1 = lane + 64 < keep - 1 ? pr1 / sum : 0.0;
+        const double d0 = wave_incl_scan_f64(p0);
+        const double d1 = wave_incl_scan_f64(p1) + readlane_f64(d0, 63);
+        ok = decide_first_ge(d0, d1, u, keep - 1, tokidx);
+    }
+    if (!ok) {
+        tail_topk_exact(a, row, P, srt, n, K, pr, q);
+        return;
+    }
+    if (lane == 0) {
+        a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
+        a.out_status[row] = TMS_ROW_OK;
+        if (a.out_keep) a.out_keep[row] = keep;
+    }
+    if (a.topk_cap && a.out_topk_ids)
+        for (int i = lane; i < a.topk_cap; i += 64)
+            a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i < n ? (int)ckey_id(srt[i]) : -1;
 }
 
 // The same tail for top-p rows (n <= kToppCap entries in LDS, exact prefix
@@ -643,7 +729,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
         sm.pbits[2 * t] = 0;
         sm.pbits[2 * t + 1] = 0;
-        __syncthreads();
+        lds_sync();
     }
     int own_off[kWin];
     float own_v[kWin];
@@ -672,7 +758,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 }
             }
         }
-        __syncthreads();
+        lds_sync();
         penbits = ((uint64_t)sm.pbits[2 * t + 1] << 32) | sm.pbits[2 * t];
     }
 
@@ -758,7 +844,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 }
             }
         }
-        __syncthreads();
+        lds_sync();
 #pragma unroll
         for (int j = 0; j < NVT; ++j) {
             const int v = t + j * kBlock;
@@ -819,7 +905,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             sm.wave_k[wv] = gb;
             sm.wave_i[wv] = nf;
         }
-        __syncthreads();
+        lds_sync();
         uint64_t b = sm.wave_k[0];
         int anynf = sm.wave_i[0];
 #pragma unroll
@@ -838,7 +924,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         const bool nf = __any(nonfinite != 0);
         sm.tkey[t] = okey(tmax);
         if (lane == 0) sm.wave_i[wv] = nf;
-        __syncthreads();
+        lds_sync();
         int anynf = 0;
 #pragma unroll
         for (int i = 0; i < kWaves; ++i) anynf |= sm.wave_i[i];
@@ -927,7 +1013,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 }
             }
             if (lane == 0) sm.wave_i[wv] = wcnt;
-            __syncthreads();
+            lds_sync();
             int cw[kWaves];
             int over = 0;
             n = 0;
@@ -943,7 +1029,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         sm.ncand = 0;
         sm.misc[2] = 0;   // the merger's read found an incomplete list
     }
-                __syncthreads();
+                lds_sync();
 #pragma unroll
                 for (int j = 0; j < NVT; ++j) {
                     if (vmax[j] >= thr) {
@@ -966,7 +1052,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                         if (pos < kCand) sm.cand[pos] = ((uint64_t)__float_as_uint(xo[i]) << 32) | io[i];
                     }
                 }
-                __syncthreads();
+                lds_sync();
                 n = sm.ncand;
                 cw[0] = n;
 #pragma unroll
@@ -996,7 +1082,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                     nv = wave_sum_dpp(nv);
                     if (lane == 0) sm.wave_i[wv] = nv;
                 }
-                __syncthreads();
+                lds_sync();
                 if (mode == MODE_TOPP) nout = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
                 else nout = n < K ? n : K;
                 for (int i = t; i < n; i += kBlock) {
@@ -1010,7 +1096,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                     if (jj < n) r0 += keys[jj] > k ? 1 : 0;
                     sm.cand[r0 + r1] = k;
                 }
-                __syncthreads();
+                lds_sync();
             }
         }
         if (!anynf && !bad_params && (fallback || n > kCand)) {
@@ -1026,39 +1112,58 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 
     // ---- publish, then take a ticket: the row's last workgroup to publish
     //      merges, and every other list is complete by then.
+    // Header and entries are stored together and complete before the
+    // ticket, so a reader that reads after its own ticket sees them all.
     // The merger reads the first r entries of every list at once (top-k and
     // greedy rows); slots past nout hold key 1, below every real key, so
-    // every word it reads is non-zero once written.
+    // every word it reads is non-zero once written.  That read is issued
+    // with the ticket, before the ticket tells whether this workgroup
+    // merges: it may see a list still in flight, which the merger checks
+    // word by word and reads again.
     const int r = (mode == MODE_TOPP || S > kRankLists) ? 0 : min(K, kUni / S - 1);
+    const int R1 = r + 1;   // words per list in uni: header, r entries
+    const bool spec = r > 0;
+    const uint64_t hdr = kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout;
     uint64_t* row_lists = a.lists + (int64_t)row * S * kListStride;
     if (wv == 0) {
         uint64_t* my_list = row_lists + (int64_t)c * kListStride;
-        for (int i = lane; i < max(nout, r); i += 64)
-            st_agent(&my_list[1 + i], i < nout ? sm.cand[i] : (uint64_t)1);
-        __builtin_amdgcn_s_waitcnt(0);   // entries complete before the header
-        if (lane == 0) {
-            st_agent(&my_list[0], kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout);
-            __builtin_amdgcn_s_waitcnt(0);   // the header before the ticket
-            const uint32_t ticket = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT);
-            sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
+        for (int i = lane; i <= max(nout, r); i += 64)
+            st_agent(&my_list[i], i == 0 ? hdr : (i <= nout ? sm.cand[i - 1] : (uint64_t)1));
+        __builtin_amdgcn_s_waitcnt(0);   // the list is complete before the ticket
+    }
+    lds_sync();
+    // Waves 1-3 read; wave 0 takes the ticket alone (a wave's loads return
+    // in order, so its own loads would hold the ticket back).
+    constexpr int kSpecThreads = kBlock - 64;
+    constexpr int kSpecPer = (kUni + kSpecThreads - 1) / kSpecThreads;
+    const int ts = t - 64;
+    uint64_t sp[kSpecPer];
+#pragma unroll
+    for (int u = 0; u < kSpecPer; ++u) {
+        const int idx = ts + u * kSpecThreads;
+        sp[u] = 0;
+        if (spec && wv != 0 && idx < S * R1) {
+            const int cc = idx / R1;
+            if (cc != c) sp[u] = ld_agent(&row_lists[(int64_t)cc * kListStride + (idx - cc * R1)]);
         }
     }
-    __syncthreads();
+    if (t == 0) {
+        const uint32_t ticket = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+        sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
+    }
+    lds_sync();
     if (!sm.misc[0]) return;
 
     // ================= merge: the last workgroup of the row =================
-    // Top-k rows read each list's header and first r entries (r = K where
-    // it fits) in one round.  Every list was published before its ticket,
-    // so that round normally finds them complete; a header not yet ready or
-    // an entry still 0 (the merger of the previous call zeroed every word it
-    // consumed; keys are never 0) is read again, boundedly.  The K best of
-    // the sample are the row's K best unless some list's last sampled entry
-    // is among them while the list holds more; only then, and for top-p
-    // rows, are whole lists merged.
-    if (t == 0) st_agent(&a.counters[row], 0u);   // ready for the next launch
-    const int R1 = r + 1;   // words per list in uni: header, r entries
-    const bool spec = r > 0;
+    // Top-k rows took each list's header and first r entries (r = K where
+    // it fits) with the ticket.  A header not yet ready or an entry still 0
+    // (the merger of the previous call zeroed every word it consumed; keys
+    // are never 0) is read again, boundedly.  The K best of the sample are
+    // the row's K best unless some list's last sampled entry is among them
+    // while the list holds more; only then, and for top-p rows, are whole
+    // lists merged.
+    if (t == 64) st_agent(&a.counters[row], 0u);   // ready for the next launch (wave 0 keeps no store in flight)
     uint64_t* uni = sm.big.m.uni;
     if (t == 0) {
         sm.theta = 0;     // lists to read again (bit per list)
@@ -1068,20 +1173,19 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         // Every word read must be set: a ready header, non-zero entries (the
         // writer padded its r slots).  Each thread checks its own words.
         int bad = 0;
-        for (int idx = t; idx < S * R1; idx += kBlock) {
-            const int cc = idx / R1, jj = idx - cc * R1;
-            uint64_t v;
-            if (cc == c) {
-                v = jj == 0 ? (kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout)
-                            : (jj <= nout ? sm.cand[jj - 1] : 1ull);
-            } else {
-                v = ld_agent(&row_lists[(int64_t)cc * kListStride + jj]);
-                bad |= (jj == 0 ? !(v & kReady) : v == 0) ? 1 : 0;
+#pragma unroll
+        for (int u = 0; u < kSpecPer; ++u) {
+            const int idx = ts + u * kSpecThreads;
+            if (wv != 0 && idx < S * R1) {
+                const int cc = idx / R1, jj = idx - cc * R1;
+                uint64_t v = sp[u];
+                if (cc == c) v = jj == 0 ? hdr : (jj <= nout ? sm.cand[jj - 1] : (uint64_t)1);
+                else bad |= (jj == 0 ? !(v & kReady) : v == 0) ? 1 : 0;
+                uni[idx] = v;
             }
-            uni[idx] = v;
         }
         if (__ballot(bad) && lane == 0) atomicOr(&sm.misc[2], 1);
-        __syncthreads();
+        lds_sync();
         // Lists read before they were complete are read again in rounds:
         // wave 0 waits (bounded) for their ready headers, then every thread
         // re-reads their sampled entries at once.
@@ -1093,15 +1197,15 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 if (!(h & kReady) || (jj >= 1 && jj <= m && uni[idx] == 0))
                     atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
             }
-            __syncthreads();
+            lds_sync();
             const uint64_t redo = sm.theta;
             if (redo == 0 || sm.misc[3]) break;
             if (round == kReadRounds) {
                 if (t == 0) sm.misc[3] = 1;
-                __syncthreads();
+                lds_sync();
                 break;
             }
-            __syncthreads();   // every thread has read theta
+            lds_sync();   // every thread has read theta
             if (t == 0) sm.theta = 0;
             if (wv == 0 && lane < S && ((redo >> lane) & 1)) {
                 uint64_t h = 0;
@@ -1113,14 +1217,14 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 uni[lane * R1] = h;
                 if (!(h & kReady)) sm.misc[3] = 1;
             }
-            __syncthreads();
+            lds_sync();
             for (int idx = t; idx < S * R1; idx += kBlock) {
                 const int cc = idx / R1, jj = idx - cc * R1;
                 if (jj == 0 || !((redo >> cc) & 1)) continue;
                 if (jj <= min((int)(uint32_t)uni[cc * R1], r))
                     uni[idx] = ld_agent(&row_lists[(int64_t)cc * kListStride + jj]);
             }
-            __syncthreads();
+            lds_sync();
         }
     } else {
         // Headers only; whole lists are read below.
@@ -1130,7 +1234,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             uni[t] = h;
             if (!(h & kReady)) atomicOr((unsigned long long*)&sm.theta, 1ull << t);
         }
-        __syncthreads();
+        lds_sync();
     }
     const int HW = spec ? R1 : 1;   // stride of the headers in uni
     if (wv == 0) {
@@ -1165,7 +1269,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             sm.misc[1] = 0;   // "a list ran out"
         }
     }
-    __syncthreads();
+    lds_sync();
     const int N = sm.misc[5];
     const int fo = sm.misc[4];
     int status = TMS_ROW_OK;
@@ -1218,13 +1322,13 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 if (tot > kCand) sm.misc[1] = 1;   // rare (a weak tau): whole lists below
             }
         }
-        __syncthreads();
+        lds_sync();
         const int nc = sm.ncand;
         if (nc <= kCand) {
             // Zero-pad to a multiple of 8 (keys are never 0), then count in
             // blocks of eight keys read 16 bytes at a time.
             if (t < 8 && nc + t < kCand) sm.cand[nc + t] = 0ull;
-            __syncthreads();
+            lds_sync();
             const uint4* c4 = (const uint4*)sm.cand;
             for (int i = t; i < nc; i += kBlock) {
                 const uint64_t k = sm.cand[i];
@@ -1242,7 +1346,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 if (r0 + r1 < n_acc) srt[r0 + r1] = k;
             }
         }
-        __syncthreads();
+        lds_sync();
         full = sm.misc[1] != 0;
     }
     if (status == TMS_ROW_OK && full) {
@@ -1253,7 +1357,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         if (t < S) sm.list_s[t] = mode == MODE_TOPP ? sm.list_n[t] : min(sm.list_n[t], K);
         n_acc = 0;
         int c_next = 0;
-        __syncthreads();
+        lds_sync();
         while (c_next < S) {
             if (t == 0) {
                 int off = n_acc, g = 1, cc = c_next;
@@ -1269,7 +1373,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                 sm.misc[6] = g;
                 sm.misc[7] = cc;
             }
-            __syncthreads();
+            lds_sync();
             const int ng = sm.misc[6];
             const int total = sm.hist[ng];
             for (int i = t; i < total; i += kBlock) {
@@ -1281,7 +1385,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
                          : (src == c ? sm.cand[jj]
                                      : ld_agent(&row_lists[(int64_t)src * kListStride + 1 + jj]));
             }
-            __syncthreads();
+            lds_sync();
             const int nkeep = total < keep_cap ? total : keep_cap;
             for (int i = t; i < total; i += kBlock) {
                 int lc = 0;
@@ -1296,7 +1400,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             }
             c_next = sm.misc[7];
             n_acc = nkeep;
-            __syncthreads();
+            lds_sync();
         }
     }
     // Every word the other chunks wrote this call (headers, entries) goes
@@ -1336,7 +1440,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         int tot;
         const int p = block_excl_scan(gap, tot, sm);
         if (gap && p < K - N) srt[N + p] = ckey(NEG_INF, (uint32_t)q);
-        __syncthreads();
+        lds_sync();
         n = K;
     }
     const float mx = ckey_val(srt[0]);
@@ -1359,14 +1463,14 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
             sig += ((double)ckey_val(srt[i]) - (double)mx >= -(double)kSigSpan) ? 1 : 0;
         sig = wave_sum_dpp(sig);
         if (lane == 0) sm.wave_i[wv] = sig;
-        __syncthreads();
+        lds_sync();
         n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
-        __syncthreads();
+        lds_sync();
     }
     double* pr = (double*)sm.big.m.uni;               // staging no longer needed
     double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
     for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
-    __syncthreads();
+    lds_sync();
     if (wv == 0) tail_topp(a, row, P, srt, n, K, pr, q);
 }
 

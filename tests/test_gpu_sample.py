@@ -256,14 +256,48 @@ def _edge_case(name, rng):
     return x, p, recent, mask
 
 
+@pytest.mark.parametrize("cap", [40, 0])
 @pytest.mark.parametrize("name", list(EDGE))
-def test_edge_cases(sampler, orc, name):
+def test_edge_cases(sampler, orc, name, cap):
+    """cap 40 asks for the per-entry probabilities (the sequential fp64
+    tail); cap 0 takes the tail that decides from tree sums."""
     rng = np.random.default_rng(abs(hash(name)) % 2**32)
     x, p, recent, mask = _edge_case(name, rng)
-    cap = 40
     want = orc.sample_batch(x, p, recent=recent, mask=mask, topk_cap=cap)
     g = run_gpu(sampler, x, p, recent=recent, mask=mask, topk_cap=cap)
     check(g, want, cap)
+
+
+def test_decisions_on_exact_boundaries(sampler, orc):
+    """Equal logits over 4 or 8 allowed ids make every prefix sum exact, so
+    the top-p cut can land exactly on top_p and the uniform exactly on a
+    partial sum: the tree-sum tail must defer those decisions to the
+    sequential sums and agree with the reference's lower_bound."""
+    V = 1000
+    u_words = {0.0: (0, 0), 0.25: (0, 0x40000000), 0.5: (0, 0x80000000),
+               0.75: (0, 0xC0000000), 0.375: (0, 0x60000000),
+               0.5 - 2.0**-53: (0xFFFFF800, 0x7FFFFFFF)}
+    rows = []
+    for n_allowed in (4, 8):
+        for top_p in (0.5, 0.75, 0.25, 0.9, 1.0):
+            for u in u_words:
+                rows.append((n_allowed, top_p, u))
+    B = len(rows)
+    x = np.full((B, V), 2.5, np.float32)
+    bits = np.zeros((B, ((V + 31) // 32) * 32), bool)
+    draws = np.zeros((B, 2), np.uint32)
+    p = params_array(B, temperature=1.0, top_k=40, top_p=0.9, seed=np.arange(B))
+    rng = np.random.default_rng(11)
+    for b, (na, tp, u) in enumerate(rows):
+        bits[b, rng.choice(V, size=na, replace=False)] = True
+        draws[b] = u_words[u]
+        p["top_p"][b] = tp
+        assert orc.canonical(int(draws[b, 0]), int(draws[b, 1])) == u
+    mask = workloads.pack_bits(bits)
+    for cap in (0, 8):
+        want = orc.sample_batch(x, p, mask=mask, draws=draws, topk_cap=cap)
+        g = run_gpu(sampler, x, p, mask=mask, draws=draws, topk_cap=cap)
+        check(g, want, cap)
 
 
 def test_repeated_calls_reuse_workspace(sampler, orc):
