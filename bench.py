@@ -42,6 +42,8 @@ def parse():
                     help="reuse one input batch (cache-resident after the first launch)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--eager", action="store_true", help="time eager launches, no graph")
+    ap.add_argument("--general", action="store_true",
+                    help="pass no row-kind hint (the general kernel for every batch)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 plain device copies of MIB MiB (a known-size kernel that "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -123,6 +125,7 @@ def main():
     import torch
 
     from tensormark_amd import Sampler
+    from tensormark_amd.sampler import ROWS_ANY, row_kinds_of
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
@@ -178,6 +181,8 @@ def main():
         mask0 = None if w.get("mask") is None else up(w["mask"], np.int32)
         s = Sampler(B, V)
         params = s.params_tensor(w["params"])
+        # the caller's row-kind hint, from the host-side parameters
+        kinds = ROWS_ANY if args.general else row_kinds_of(w["params"])
         out = {n: torch.empty(B, dtype=torch.int32, device=dev) for n in ("tokens", "status", "keep")}
         recs = []
         for i in range(n_sets):
@@ -185,7 +190,7 @@ def main():
             mask = mask0 if (i == 0 or mask0 is None) else mask0.clone()
             rc = recent if (i == 0 or recent is None) else recent.clone()
             keep += [x, mask, rc]
-            recs.append(s.make_args(x, params, recent=rc, mask=mask, out=out))
+            recs.append(s.make_args(x, params, recent=rc, mask=mask, out=out, row_kinds=kinds))
         fn = s.lib.tms_sample_batch
     ptrs = [ctypes.byref(a) for a in recs]
     h = s.handle

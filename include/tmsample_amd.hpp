@@ -246,6 +246,10 @@ private:
         a.out_tokens = &d->token;
         a.out_status = &d->status;
         a.out_keep = &d->keep;
+        // The row is known here: a greedy or top-k <= 128 row may take the
+        // library's top-k kernel.
+        a.row_kinds = (h.params.greedy != 0 || (h.params.top_k >= 1 && h.params.top_k <= 128))
+                          ? TMS_ROWS_TOPK : TMS_ROWS_ANY;
         check(tms_sample_batch(ctx_, &a, stream_), "tms_sample_batch");
         hip(hipMemcpyAsync(&h, d, sizeof(h), hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
         hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");

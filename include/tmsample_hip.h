@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define TMS_ABI_VERSION 1
+#define TMS_ABI_VERSION 2
 
 /* Return codes of the entry points. */
 enum {
@@ -64,6 +64,12 @@ enum {
     TMS_ROW_NONFINITE = 3,    /* NaN or +inf after masking, or lg overflowed */
     TMS_ROW_UNSUPPORTED = 4,  /* top-p-only row with too many candidates */
     TMS_ROW_INTERNAL = 5      /* a chunk list never arrived (bounded wait expired) */
+};
+
+/* tms_sample_args.row_kinds: what the caller knows of its rows. */
+enum {
+    TMS_ROWS_ANY = 0,    /* no promise: the general kernel */
+    TMS_ROWS_TOPK = 1    /* every row greedy, or top-k with 1 <= top_k <= 128 */
 };
 
 enum {
@@ -123,6 +129,11 @@ typedef struct tms_sample_args {
                                  top-k ids, -1 padded */
     float* out_topk_probs;    /* device, [batch][topk_cap], nullable:
                                  pr / z of the same entries */
+    uint32_t row_kinds;       /* TMS_ROWS_ANY, or TMS_ROWS_TOPK: the caller promises
+                                 every row is greedy or has 1 <= top_k <= 128, and
+                                 the library may take its top-k kernel (a row that
+                                 breaks the promise gets TMS_ROW_UNSUPPORTED) */
+    uint32_t reserved;        /* must be 0 */
 } tms_sample_args;
 
 typedef struct tms_spec_args {

@@ -14,6 +14,8 @@
 namespace tms {
 constexpr int kSpecMaxK = 16;      // draft tokens per sequence
 constexpr int kSpecParts = 64;     // vocabulary parts of the residual draw
+constexpr int kCounterStride = 64; // u32 between per-row arrival counters: one 256-byte line
+                                   // each, so the rows' atomics do not queue on one line
 }  // namespace tms
 
 // Statistics of one speculative-verify row (target or draft).
@@ -32,10 +34,10 @@ struct tms_context {
     int max_chunks;
     size_t bytes;
     void* ws;
-    uint32_t* counters;        // [max_batch] sampler arrival counters
+    uint32_t* counters;        // [max_batch][kCounterStride] sampler arrival counters (word 0)
     uint32_t* ones;            // all-ones mask row, for calls without a grammar mask
     uint64_t* lists;           // [max_batch][max_chunks][kListStride] chunk candidate lists
-    uint32_t* spec_tickets;    // [max_batch] verify arrival counters
+    uint32_t* spec_tickets;    // [max_batch][kCounterStride] verify arrival counters (word 0)
     uint64_t* spec_parts;      // [max_batch][kSpecParts][2] published partial sums
     tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]
 };

@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     if (t == 0) {
         st_agent(&pw[0], kPartReady | (uint64_t)wsum);
         st_agent(&pw[1], kPartReady | (uint64_t)tsum);
-        ticket = __hip_atomic_fetch_add(&a.tickets[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ticket = __hip_atomic_fetch_add(&a.tickets[b * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         misc[0] = (int)ticket;
     }
     __syncthreads();
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
 
     // ---- the last arriver: gather the parts (bounded wait on their ready
     //      bits), zero them and the ticket for the next call.
-    if (t == 0) st_agent(&a.tickets[b], 0u);
+    if (t == 0) st_agent(&a.tickets[b * kCounterStride], 0u);
     int timed_out = 0;
     if (t < a.P) {
         uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * 2;

@@ -23,6 +23,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmsample_hip.so")
 
 TMS_OK = 0
+ROWS_ANY, ROWS_TOPK = 0, 1
 ROW_OK, ROW_BAD_PARAMS, ROW_ALL_MASKED, ROW_NONFINITE, ROW_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -127,6 +128,7 @@ class SampleArgs(C.Structure):
         ("recent_stride", C.c_int64), ("mask", C.c_void_p), ("mask_stride", C.c_int64),
         ("draws", C.c_void_p), ("out_tokens", C.c_void_p), ("out_status", C.c_void_p),
         ("out_keep", C.c_void_p), ("out_topk_ids", C.c_void_p), ("out_topk_probs", C.c_void_p),
+        ("row_kinds", C.c_uint32), ("reserved", C.c_uint32),
     ]
 
 
@@ -140,6 +142,14 @@ class SpecArgs(C.Structure):
 
 
 _LIB = None
+
+
+def row_kinds_of(params: np.ndarray) -> int:
+    """ROWS_TOPK when every row is greedy or has 1 <= top_k <= 128 (the rows
+    the library's top-k kernel serves), else ROWS_ANY."""
+    p = np.asarray(params)
+    ok = (p["greedy"] != 0) | ((p["top_k"] >= 1) & (p["top_k"] <= 128))
+    return ROWS_TOPK if bool(np.all(ok)) else ROWS_ANY
 
 
 def load_library(path: str = LIB_PATH) -> C.CDLL:
@@ -224,9 +234,12 @@ def _dtype_code(t) -> int:
 class Sampler:
     """A context (device workspace) for batches up to max_batch x max_vocab."""
 
-    def __init__(self, max_batch: int, max_vocab: int, device: int = 0):
+    def __init__(self, max_batch: int, max_vocab: int, device: int = 0, kernel: str = "auto"):
+        if kernel not in ("auto", "general"):
+            raise ValueError("kernel must be 'auto' or 'general'")
         torch = _torch()
         self.torch = torch
+        self.kernel = kernel
         self.lib = load_library()
         self.device = device
         h = C.c_void_p()
@@ -253,14 +266,22 @@ class Sampler:
         return self.torch.from_numpy(raw.copy()).to(f"cuda:{self.device}")
 
     def sample(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
-               topk_cap: int = 0, out=None, stream=None):
+               topk_cap: int = 0, out=None, stream=None, row_kinds=None):
         """Sample one token per row of ``logits`` ([B, V] fp32/fp16/bf16, cuda).
 
         ``params`` is a device uint8 tensor from params_tensor() (or a numpy
-        ROW_DTYPE array, uploaded here).  Returns a dict of device tensors:
-        tokens, status, keep, and topk_ids/topk_probs when topk_cap > 0.
+        ROW_DTYPE array, uploaded here).  ``row_kinds`` is the hint of
+        tms_sample_args (ROWS_ANY / ROWS_TOPK); by default it is derived from
+        numpy params (ROWS_ANY for device params), and a Sampler created with
+        kernel="general" always passes ROWS_ANY.  Returns a dict of device
+        tensors: tokens, status, keep, and topk_ids/topk_probs when
+        topk_cap > 0.
         """
         torch = self.torch
+        if row_kinds is None:
+            row_kinds = ROWS_ANY
+            if self.kernel == "auto" and isinstance(params, np.ndarray):
+                row_kinds = row_kinds_of(params)
         if isinstance(params, np.ndarray):
             params = self.params_tensor(params)
         B, V = logits.shape
@@ -275,14 +296,14 @@ class Sampler:
                 out["topk_ids"] = torch.empty((B, topk_cap), dtype=torch.int32, device=dev)
                 out["topk_probs"] = torch.empty((B, topk_cap), dtype=torch.float32, device=dev)
         a = self.make_args(logits, params, recent=recent, n_recent=n_recent, mask=mask,
-                           draws=draws, topk_cap=topk_cap, out=out)
+                           draws=draws, topk_cap=topk_cap, out=out, row_kinds=row_kinds)
         s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
         _check(self.lib.tms_sample_batch(self.handle, C.byref(a), C.c_void_p(s)),
                "tms_sample_batch")
         return out
 
     def make_args(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
-                  topk_cap=0, out=None) -> SampleArgs:
+                  topk_cap=0, out=None, row_kinds=ROWS_ANY) -> SampleArgs:
         B, V = logits.shape
         a = SampleArgs()
         a.logits = logits.data_ptr()
@@ -303,6 +324,7 @@ class Sampler:
         a.topk_cap = topk_cap
         a.out_topk_ids = _ptr(out.get("topk_ids")) if topk_cap else None
         a.out_topk_probs = _ptr(out.get("topk_probs")) if topk_cap else None
+        a.row_kinds = row_kinds
         return a
 
     def spec_verify(self, target, draft, draft_tokens, params, *, draws=None, stream=None):

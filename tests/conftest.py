@@ -38,13 +38,16 @@ def golden():
     return np.load(os.path.join(ROOT, "tests", "golden", "sample_golden.npz"))
 
 
-@pytest.fixture(scope="session")
-def sampler():
+@pytest.fixture(scope="session", params=["auto", "general"])
+def sampler(request):
+    """The sampler twice: "auto" takes the top-k kernel for batches whose
+    rows are all greedy or top-k <= 128; "general" always takes the general
+    kernel, so every parity test covers both."""
     import torch
 
     from tensormark_amd import Sampler
 
     assert torch.cuda.is_available(), "GPU tests need a HIP device"
-    s = Sampler(max_batch=1024, max_vocab=262144)
+    s = Sampler(max_batch=1024, max_vocab=262144, kernel=request.param)
     yield s
     s.close()

@@ -32,7 +32,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_sizes():
     lib = sampler.load_library()
-    assert lib.tms_abi_version() == 1
+    assert lib.tms_abi_version() == 2
+    assert ctypes.sizeof(sampler.SampleArgs) == 136
     assert ctypes.sizeof(sampler.RowParams) == 56
     assert lib.tms_status_string(-2).decode().startswith("batch")
 
