@@ -36,6 +36,8 @@
 // drained (s_waitcnt) before the header that announces them; the merger's
 // wait for the headers is bounded.
 
+#include <algorithm>
+
 #include "tms_sample_common.h"
 
 namespace tms {
@@ -917,7 +919,9 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_st = off_l + nc * tms::kListStride * sizeof(uint64_t);
     const size_t off_sp = off_st + nb * tms::kCounterStride * 4;   // one 256-byte line per ticket
     const size_t off_ss = off_sp + nb * tms::kSpecParts * 2 * sizeof(uint64_t);
-    ctx->bytes = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
+    const size_t off_tl = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
+    const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kLeanMaxChunksHost);
+    ctx->bytes = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
     int rc = TMS_OK;
     if (hipMalloc(&ctx->ws, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipMemset(ctx->ws, 0, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;   // lists start zeroed
@@ -936,6 +940,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->spec_tickets = (uint32_t*)(p + off_st);
     ctx->spec_parts = (uint64_t*)(p + off_sp);
     ctx->spec_stats = (tms_spec_stat*)(p + off_ss);
+    ctx->tlists = (uint64_t*)(p + off_tl);
     (void)hipSetDevice(prev);
     *out = ctx;
     return TMS_OK;
@@ -996,6 +1001,7 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     k.topk_cap = (a->out_topk_ids || a->out_topk_probs) ? a->topk_cap : 0;
     k.counters = ctx->counters;
     k.lists = ctx->lists;
+    k.tlists = ctx->tlists;
 #ifdef TMS_TRACE
     k.trace = g_tms_trace_host;
 #endif

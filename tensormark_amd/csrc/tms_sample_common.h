@@ -44,6 +44,7 @@ constexpr int kUni = 2048;                 // merge staging (u64)
 constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
 constexpr int kLeanMaxChunksHost = 16;     // chunks per row of the top-k kernel (vocab <= 262,144)
+constexpr int kTopkListStride = 1280;      // u64 per (row, chunk) list of the top-k kernel
 constexpr int kRankLists = 16;             // most chunk lists the sampled merge reads in one round
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
@@ -75,6 +76,7 @@ struct KArgs {
     // workspace
     uint32_t* counters;    // [B] arrival tickets, reset by the merger
     uint64_t* lists;       // [B][S][kListStride]: header, entries; headers reset by the merger
+    uint64_t* tlists;      // [B][S][kTopkListStride]: the top-k kernel's lists, zeroed by the merger
 #ifdef TMS_TRACE
     uint64_t* trace;
 #endif

@@ -1,32 +1,33 @@
 // tms_topk.hip -- the sampler kernel for batches whose rows are all greedy or
 // top-k with k <= 128 (the host picks it from the caller's row-kind hint).
 //
-// One launch per call, as the general kernel: row b is cut into S chunks of
-// at most 16K ids, workgroup (b, c) streams its chunk once (nontemporal
-// 16-byte loads) and reduces it to its sorted top-K, and the last workgroup
-// of the row to take a ticket merges the S lists and runs the fp64 tail of
-// tmsample::sample (tensormark/tmsample.h:184-199).  What differs is that
-// every step is shaped for latency: the path has no top-p branch, so the
-// whole chunk stays in registers and the compiler keeps the per-slot work
-// where each slot's data lands.
+// One launch per call.  Row b is cut into S chunks of at most 16K ids and
+// workgroup (b, c) streams its chunk once (nontemporal 16-byte loads, 64
+// values per thread).  A chunk selects nothing: each thread keeps its three
+// largest entries (with ids) and its fourth value, and the chunk publishes
+// the keys, its history-penalised entries and the largest fourth value the
+// moment its stream is in.  The last workgroup of the row to take a ticket
+// merges: it bounds the row's K-th value from below by the 256 "group
+// maxima" (group j = thread j of every chunk), gathers every published key
+// above the bound, ranks them and runs the fp64 tail of tmsample::sample
+// (tensormark/tmsample.h:184-199).  Every entry >= the bound is one of a
+// thread's three entries or a penalised window entry, unless the chunk's
+// largest fourth value reaches the bound: such a chunk (very rare) is read
+// again.
 //
-//   pass 1     mask (bit extract + select), history penalties on the entries
-//              this thread holds (marked in LDS while the stream is in
-//              flight), and the running top two values per thread with the
-//              index of the first.
-//   threshold  the K-th largest of the 256 thread maxima by bisection on
-//              their order keys, four compares a round into separate masks.
-//   candidates a thread whose second value is below the threshold offers its
-//              maximum (one ballot); a thread holding several stages its
-//              values in LDS and the wave tests them an entry per lane.
-//   ticket     taken right after pass 1, so its round trip overlaps the
-//              selection; the last chunk of the row to take one merges, the
-//              others publish their sorted lists.  Keys are never 0 and the
-//              merger zeroes what it read, so a word still in flight reads 0
-//              and is read again.
-//   merge      keys above a proven lower bound of the row's K-th key are
-//              gathered and ranked by counting; wave 0 runs the tail while
-//              waves 1-3 zero the lists.
+//   pass 1     mask (bit extract + select; history ids masked out, counted
+//              while the stream is in flight), running top three values
+//              with ids and the fourth value, per thread.
+//   penalties  the thread that counted a window id first loaded its logit
+//              with the stream; it forms the compounding penalty
+//              (tmsample.h:58-61, then frequency/presence) and publishes the
+//              entry.
+//   publish    header, 3 x 256 keys, penalised entries: every word non-zero
+//              (keys never are); the merger reads each word before zeroing
+//              it, so a word still in flight reads 0 and is read again, and
+//              no store waits.
+//   merge      bound (bisection on order keys), gather from registers, rank
+//              by counting, tail on wave 0.
 // A row that is not greedy and not top-k <= 128 breaks the hint and reports
 // TMS_ROW_UNSUPPORTED.
 
@@ -34,59 +35,93 @@
 
 namespace tms {
 
-constexpr int kLeanMaxChunks = kLeanMaxChunksHost;       // vocab <= 262,144
-constexpr int kLeanUni = kLeanMaxChunks * (kTopkFast + 1);   // every list, header + K entries
-constexpr int kStage = 4;                                // threads a wave stages at a time
-constexpr int kLate = kWaves * kStage * kEpt;           // window ids past the preloaded positions
+constexpr int kLeanMaxChunks = kLeanMaxChunksHost;   // vocab <= 262,144
+constexpr int kPendRead = 64;                        // penalised entries per chunk in the first read
+constexpr int kWordKeys = 1;                         // list words: [0] header, [1, 769) keys (key j
+constexpr int kWordPend = kWordKeys + 3 * kBlock;    // of thread t at 1 + j * 256 + t), [769,
+                                                     // kTopkListStride) penalised entries
+constexpr int kPendCap = kTopkListStride - kWordPend;
+constexpr int kLate = 1024;                          // window ids past the preloaded positions
+static_assert(kPendCap > kPendRead, "list layout");
+static_assert(8 * kPendRead % kBlock == 0, "pending-entry read layout");
+static_assert(4 * kTopkFast >= kBlock, "gather junk slots");
+
+// Header word: ready bit, flags (bits 56-62), penalised entries (bits
+// 32-47), order key of the chunk's largest fourth value (bits 0-31).
+__device__ __forceinline__ uint64_t lean_header(int flags, int npen, uint32_t t4key) {
+    return kReady | ((uint64_t)(flags & 0x7F) << 56) | ((uint64_t)(npen & 0xFFFF) << 32) | t4key;
+}
+__device__ __forceinline__ int hdr_npen(uint64_t h) { return (int)((h >> 32) & 0xFFFF); }
+__device__ __forceinline__ int hdr_flags(uint64_t h) { return (int)((h >> 56) & 0x7F); }
+
+// Read in place of the caller's draws when there are none (never written).
+__device__ uint64_t kDeadWord = 1;
 
 struct LeanSmem {
     union {
-        uint32_t cnt[kChunk / 2];   // window counts (16 bits per id) during pass 1
+        uint32_t cnt[kChunk / 2];   // window counts (16 bits per id), chunk phase
         struct {
-            uint64_t uni[kLeanUni];     // the lists of the row (merger); candidate keys (chunk)
-            uint64_t srt[kCand + 8];    // the merged, sorted top-K
+            uint64_t keys[kCand + 8];   // candidate keys
+            uint64_t srt[kCand + 8];    // the sorted top-K
+            double pr[4 * kTopkFast];   // fp64 tail scratch
         } m;
+        uint32_t wbits[kChunk / 32];    // a re-read chunk's window ids (merge)
     } big;
-    uint64_t cand[kCand + 8];       // chunk candidates, then the chunk's sorted list
-    union {
-        float stage[kWaves][kStage * kEpt];   // per wave: the values of threads holding several candidates
-        int late[kLate];                      // window ids past the preloaded positions (before that)
-    } sl;
+    uint64_t cand[kCand + 8];       // merge candidates (raw value bits, id)
+    uint64_t pend[kPendCap];        // this chunk's penalised window entries (keys)
     uint32_t mw[kWaves * 128];      // per wave: the mask words of its slots
-    uint32_t wbits[kChunk / 32];    // ids of the chunk in the history window
-    uint64_t pend[kCand];           // penalised window entries: (value, id)
-    int npen, nlate;
-    uint32_t tkey[kBlock];          // order keys of the thread maxima
-    uint64_t wave_k[kWaves];
+    uint32_t gkey[kBlock];          // merge: group maxima order keys
+    int late[kLate];                // window ids past the preloaded positions
+    alignas(16) uint64_t hdr[kLeanMaxChunks];   // merge: the chunks' headers (1 past S)
     int wave_i[kWaves];
-    int wave_m[kWaves];
-    int list_n[kLeanMaxChunks];
-    int list_s[kLeanMaxChunks + 2];
-    int list_src[kLeanMaxChunks + 1];
+    uint32_t wave_u[kWaves];
     int hist[256];
     int ncand;
+    int npen, nlate;
     int misc[8];
-    uint64_t theta;
+#ifdef TMS_TRACE
+    uint64_t trs[kWaves * 24];   // trace stamps, written out at exit
+#endif
 };
 
-// Bitwise OR over the 64 lanes of a wave (DPP steps towards lane 63).
-__device__ __forceinline__ uint64_t wave_or_u64_dpp(uint64_t v) {
-#define TMS_ORSTEP(CTRL, RM, BZ)                                                  \
-    {                                                                             \
-        const uint32_t lo = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)v);               \
-        const uint32_t hi = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)(v >> 32));       \
-        v |= ((uint64_t)hi << 32) | lo;                                           \
-    }
-    TMS_ORSTEP(0x111, 0xF, true)
-    TMS_ORSTEP(0x112, 0xF, true)
-    TMS_ORSTEP(0x114, 0xF, true)
-    TMS_ORSTEP(0x118, 0xF, true)
-    TMS_ORSTEP(0x142, 0xA, false)
-    TMS_ORSTEP(0x143, 0xC, false)
-#undef TMS_ORSTEP
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
+#ifdef TMS_TRACE
+// Trace builds of this kernel stamp into LDS and write the stamps out when
+// the workgroup exits, so no trace store is outstanding at a vmcnt wait.
+#undef TMS_TR
+#undef TMS_TV
+#define TMS_TR(i)                                                                   \
+    do {                                                                            \
+        asm volatile("; trace point " #i);                                          \
+        if ((threadIdx.x & 63) == 0) sm.trs[(threadIdx.x >> 6) * 24 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#define TMS_TV(i, val)                                                              \
+    do {                                                                            \
+        if ((threadIdx.x & 63) == 0) sm.trs[(threadIdx.x >> 6) * 24 + (i)] = (uint64_t)(val); \
+    } while (0)
+#define TK_TRACE_INIT()                                                             \
+    do {                                                                            \
+        if ((threadIdx.x & 63) < 24) sm.trs[(threadIdx.x >> 6) * 24 + (threadIdx.x & 63)] = 0; \
+    } while (0)
+#define TK_TRACE_FLUSH()                                                            \
+    do {                                                                            \
+        if ((threadIdx.x & 63) < 24 && a.trace)                                     \
+            a.trace[(blockIdx.x * 4 + (threadIdx.x >> 6)) * 24 + (threadIdx.x & 63)] = \
+                sm.trs[(threadIdx.x >> 6) * 24 + (threadIdx.x & 63)];               \
+    } while (0)
+#else
+#define TK_TRACE_INIT() ((void)0)
+#define TK_TRACE_FLUSH() ((void)0)
+#endif
+
+// Maximum over the 64 lanes of a wave of u32 values (DPP steps towards lane 63).
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+    v = max(v, dpp_u32<0x111, 0xF, true>(0u, v));
+    v = max(v, dpp_u32<0x112, 0xF, true>(0u, v));
+    v = max(v, dpp_u32<0x114, 0xF, true>(0u, v));
+    v = max(v, dpp_u32<0x118, 0xF, true>(0u, v));
+    v = max(v, dpp_u32<0x142, 0xA, false>(0u, v));
+    v = max(v, dpp_u32<0x143, 0xC, false>(0u, v));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // 16-byte nontemporal load: the logits are read exactly once per call.
@@ -124,37 +159,182 @@ __device__ __forceinline__ void rank_sort(uint64_t* keys, int n, uint64_t* out, 
     lds_sync();
 }
 
-// List index of word idx when lists are R1 words long: (idx + 1/2) / R1 in
-// float, exact for idx < 4096 and R1 <= 129 (the product is at least
-// 1/(2 R1) away from an integer, far beyond the float error).
-__device__ __forceinline__ int list_of(int idx, float rcp_r1) {
-    return (int)(((float)idx + 0.5f) * rcp_r1);
+// Id of entry q (slot q / vec, element q % vec) of thread j of the chunk at e0.
+template <int VEC>
+__device__ __forceinline__ uint32_t id_of(int j, int q, int e0) {
+    return (uint32_t)(e0 + (j + (q / VEC) * kBlock) * VEC + q % VEC);
 }
 
-// Zero every word of the row's lists the merger read (header and r entries
-// of every list but its own, which it never publishes), threads tid0 ..
-// nthr-1 of the workgroup.  Each word was read as written first, so its zero
-// is ordered after its key.
-__device__ __forceinline__ void zero_lean_lists(uint64_t* row_lists, int S, int r, int c, int tid0,
-                                                int nthr) {
-    for (int cc = 0; cc < S; ++cc) {
-        if (cc == c) continue;
-        uint64_t* L = row_lists + (int64_t)cc * kListStride;
-        for (int jj = tid0; jj <= r; jj += nthr) st_agent(&L[jj], (uint64_t)0);
+// Appends `key` where `take` holds to sm.cand after the first base0 entries
+// (one ballot and one LDS atomic per wave, counted in sm.ncand); past kCand
+// the count still grows and nothing is stored.
+template <typename SM>
+__device__ __forceinline__ void append_cand(SM& sm, bool take, uint64_t key, int base0) {
+    const uint64_t m = __ballot(take);
+    if (!m) return;
+    int wb = 0;
+    if ((threadIdx.x & 63) == 0) wb = atomicAdd(&sm.ncand, __popcll(m));
+    wb = __builtin_amdgcn_readfirstlane(wb);
+    const int pos = base0 + wb + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (take && pos < kCand) sm.cand[pos] = key;
+}
+
+// The published value of id in a row: the penalised value of a window entry
+// (found in `pend`, np entries), else the logit masked.
+template <typename T>
+__device__ __forceinline__ float row_value(const T* base, const uint32_t* mrow, const uint64_t* pend,
+                                           int np, int id) {
+    for (int i = 0; i < np; ++i)
+        if ((int)ckey_id(pend[i]) == id) return ckey_val(pend[i]);
+    return ((mrow[id >> 5] >> (id & 31)) & 1u) ? Elt<T>::scalar(base + id) : -__builtin_huge_valf();
+}
+
+// The exact top-K of a whole row by (lg desc, id asc), for rows the bound
+// cannot narrow (massive ties, or more penalised entries than a list holds):
+// a radix select over the keys of lg = v / T, 8 bits a pass, with the row
+// read again from memory (row_value).  `pend` holds every penalised entry of
+// the row (np of them, read from the lists).  Writes sm.cand as ckey(value,
+// id), unsorted; returns the count (<= K).
+template <typename T, typename SM>
+__device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, const uint64_t* pend,
+                                           int np, int V, int K, float temp, bool divide, SM& sm) {
+    const int t = threadIdx.x;
+    const float NEG_INF = -__builtin_huge_valf();
+    auto lkey = [&](float v) { return okey(divide ? v / temp : v); };
+    uint32_t prefix = 0, pmask = 0;
+    int remaining = K;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        sm.hist[t] = 0;
+        if (t == 0) sm.ncand = 0;
+        lds_sync();
+        for (int id = t; id < V; id += kBlock) {
+            const float v = row_value(base, mrow, pend, np, id);
+            if (v == NEG_INF) continue;
+            const uint32_t k = lkey(v);
+            if ((k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 0xFF], 1);
+        }
+        lds_sync();
+        const int h = sm.hist[255 - t];   // thread t holds digit 255 - t
+        int total;
+        const int above = block_excl_scan(h, total, sm);
+        if (shift == 24 && total <= K) {
+            // At most K finite entries: all of them.
+            for (int id = t; id < V; id += kBlock) {
+                const float v = row_value(base, mrow, pend, np, id);
+                if (v == NEG_INF) continue;
+                const int pos = atomicAdd(&sm.ncand, 1);
+                sm.cand[pos] = ckey(v, (uint32_t)id);
+            }
+            lds_sync();
+            return sm.ncand;
+        }
+        if (above < remaining && above + h >= remaining) {
+            sm.misc[0] = 255 - t;
+            sm.misc[1] = above;
+        }
+        lds_sync();
+        remaining -= sm.misc[1];
+        prefix |= (uint32_t)sm.misc[0] << shift;
+        pmask |= 0xFFu << shift;
+        lds_sync();
+    }
+    // prefix is the K-th largest key; K - remaining keys are strictly greater.
+    for (int id = t; id < V; id += kBlock) {
+        const float v = row_value(base, mrow, pend, np, id);
+        if (v == NEG_INF) continue;
+        if (lkey(v) > prefix) {
+            const int pos = atomicAdd(&sm.ncand, 1);
+            sm.cand[pos] = ckey(v, (uint32_t)id);
+        }
+    }
+    lds_sync();
+    const int g = sm.ncand;
+    // Ties in id order, kBlock consecutive ids per step.
+    int taken = 0;
+    for (int b0 = 0; b0 < V && taken < remaining; b0 += kBlock) {
+        const int id = b0 + t;
+        float v = NEG_INF;
+        int tie = 0;
+        if (id < V) {
+            v = row_value(base, mrow, pend, np, id);
+            tie = v != NEG_INF && lkey(v) == prefix;
+        }
+        int tot;
+        const int p = block_excl_scan(tie, tot, sm);
+        if (tie && taken + p < remaining)
+            sm.cand[g + taken + p] = ckey(v, (uint32_t)id);
+        taken += tot;
+    }
+    lds_sync();
+    return g + (taken < remaining ? taken : remaining);
+}
+
+// A chunk read again by the merger (its largest fourth value reaches the
+// bound kb): the whole chunk [ce0, ce1) in one round of loads (pass 1's
+// layout), every entry >= kb that is not a window id of the chunk (bitmap
+// sm.big.wbits, chunk-relative) appended to sm.cand after the first base0
+// entries (one LDS atomic per wave on sm.ncand).
+template <typename T, bool FAST>
+__device__ __noinline__ void reread_chunk(const T* base, const uint32_t* mrow, int ce0, int ce1, uint32_t kb,
+                                          int base0, LeanSmem& sm) {
+    constexpr int VEC = Elt<T>::kVec;
+    constexpr int NVT = kEpt / VEC;
+    const int t = threadIdx.x, lane = t & 63;
+    const int cnv = (ce1 - ce0 + VEC - 1) / VEC;
+    float f[kEpt];
+    uint32_t mk[NVT];
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+        const int v = min(t + j * kBlock, cnv - 1);
+        const int eb = ce0 + v * VEC;
+        mk[j] = mrow[eb >> 5];
+        if constexpr (FAST) {
+            const uint4 q = *(const uint4*)(base + eb);
+            float g[VEC];
+            Elt<T>::widen(q, g);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) f[j * VEC + e] = g[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) f[j * VEC + e] = Elt<T>::scalar(base + min(eb + e, ce1 - 1));
+        }
+    }
+    uint64_t take = 0;   // bit q: entry q of this thread
+#pragma unroll
+    for (int j = 0; j < NVT; ++j) {
+        const int v = t + j * kBlock;
+        const int eb = ce0 + v * VEC;
+        const uint32_t wb = v < cnv ? sm.big.wbits[(eb - ce0) >> 5] : 0u;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            const int id = eb + e;
+            const bool ok = v < cnv && id < ce1 && ((mk[j] >> (id & 31)) & 1u) && !((wb >> (id & 31)) & 1u) &&
+                            okey(f[j * VEC + e]) >= kb;
+            take |= (uint64_t)ok << (j * VEC + e);
+        }
+    }
+    const int m = __popcll(take);
+    const int inc = wave_incl_scan_i32(m);
+    int wb0 = 0;
+    if (lane == 63 && inc) wb0 = atomicAdd(&sm.ncand, inc);
+    int q = base0 + __builtin_amdgcn_readlane(wb0, 63) + inc - m;
+#pragma unroll
+    for (int b = 0; b < kEpt; ++b) {
+        if ((take >> b) & 1u) {
+            const int id = ce0 + (t + (b / VEC) * kBlock) * VEC + b % VEC;
+            if (q < kCand) sm.cand[q] = ckey(f[b], (uint32_t)id);
+            ++q;
+        }
     }
 }
 
-// Id of entry q (slot q / vec, element q % vec) of thread t in the chunk at e0.
-template <int VEC>
-__device__ __forceinline__ uint32_t id_of(int t, int q, int e0) {
-    return (uint32_t)(e0 + (t + (q / VEC) * kBlock) * VEC + q % VEC);
-}
-
-template <typename T, bool FAST>
+// MS: the merge's chunk slots, 8 or 16 (>= S).
+template <typename T, bool FAST, int MS>
 __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
+    static_assert(MS == 8 || MS == 16, "merge slots");
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NVT = kEpt / VEC;
-    constexpr uint64_t kLaneMask = (1ull << VEC) - 1ull;
     constexpr int kWin = 4;   // history ids loaded per thread with the stream
     __shared__ LeanSmem sm;
     const float NEG_INF = -__builtin_huge_valf();
@@ -167,10 +347,12 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     const int e0 = c * a.CE;   // a multiple of 32: the chunk starts on a mask word
     const int e1 = min(e0 + a.CE, V);
     const int nvec = (e1 - e0 + VEC - 1) / VEC;
+    TK_TRACE_INIT();
     TMS_TR(0);
 
     // ---- loads in the order they are needed: history window, row
-    //      parameters, this wave's mask words, then the stream.
+    //      parameters, this wave's mask words, then the stream, then the
+    //      logits of the window ids in this chunk (their owners' loads).
     const int32_t* hist = a.recent + (int64_t)row * a.recent_stride;
     int wid[kWin];
     if (a.recent) {
@@ -179,6 +361,10 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         for (int i = 0; i < kWin; ++i) wid[i] = hist[min(t + i * kBlock, rs - 1)];
     }
     const tms_row_params P = a.params[row];
+    // the caller's draw for the row, if given, loaded now (no branch: a
+    // dummy word otherwise) so the merge never waits for it
+    const uint32_t* dp = a.draws ? a.draws + 2 * row : (const uint32_t*)&kDeadWord;
+    const uint32_t dw0 = dp[0], dw1 = dp[1];
     int nrec = 0;
     if (a.recent) {
         nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
@@ -200,22 +386,33 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
     const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
+    // 16-byte slots: the first kLook now, slot j + kLook once slot j is
+    // worked (the queue of a CU's loads is full while the row streams, so a
+    // wave that issued everything first would wait there and then work
+    // every slot after the data is in).
+#ifdef TMS_TOPK_LOOK
+    constexpr int kLook = TMS_TOPK_LOOK < NVT ? TMS_TOPK_LOOK : NVT;
+#else
+    constexpr int kLook = NVT < 4 ? NVT : 4;
+#endif
     uint4 raw[NVT];
     float sx[FAST ? 1 : kEpt];
+    auto issue = [&](int j) {
+        const int v = min(t + j * kBlock, nvec - 1);
+        raw[j] = ld_stream(base + e0 + v * VEC);
+    };
 #pragma unroll
     for (int j = 0; j < NVT; ++j) {
         const int v = min(t + j * kBlock, nvec - 1);
         const int eb = e0 + v * VEC;
         if constexpr (FAST) {
-            raw[j] = ld_stream(base + eb);
+            if (j < kLook) issue(j);
         } else {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) sx[j * VEC + e] = Elt<T>::scalar(base + min(eb + e, V - 1));
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    // The owners' loads: the logit and mask word of each preloaded window id
-    // in this chunk (returned in order after this thread's stream).
     float own_v[kWin];
     uint32_t own_m[kWin];
 #pragma unroll
@@ -235,39 +432,38 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     pn.freq = P.frequency_penalty;
     pn.pres = P.presence_penalty;
     const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
-    // While the stream is in flight: this wave's mask words into its own LDS
-    // words (a wave-level sync, no workgroup barrier), and the window count
-    // table zeroed for the count after pass 1.
+
+    // ---- while the stream is in flight: this wave's mask words into its
+    //      LDS words, and the window count table cleared.
     uint32_t* mw = sm.mw + wv * kWaveWords;
     mw[2 * lane] = mwd[0];
     mw[2 * lane + 1] = mwd[1];
     if (pn.on) {
         uint4* c4 = (uint4*)sm.big.cnt;
         for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
-        sm.wbits[2 * t] = 0;
-        sm.wbits[2 * t + 1] = 0;
     }
     if (t == 0) {
-        sm.ncand = 0;
         sm.npen = 0;
         sm.nlate = 0;
-        sm.misc[2] = 0;   // the merger's read found an incomplete list
     }
-    wave_lds_sync();
+    if (pn.on) lds_sync();
+    else wave_lds_sync();
     TMS_TR(2);
 
-    // ---- pass 1, as each slot lands: widen and mask (bit -> value or -inf),
-    //      kept as the chunk's values in registers, with the thread's running
-    //      top two values and the slot index of the first maximum (ids grow
-    //      with the index, so a strict > keeps the lowest id).  The maxima
-    //      propagate NaN (IEEE maximum): a NaN or +inf anywhere in the chunk
-    //      shows in t1.  History penalties come after, on the few entries
-    //      they touch.
-    float xv[kEpt];
-    float t1 = NEG_INF, t2 = NEG_INF;
-    int i1 = 0;
+    // ---- pass 1, as each slot lands: widen and mask (mask bit -> value,
+    //      else -inf), with the thread's running top
+    //      three values and their slot indices and its fourth value.  Ids grow
+    //      with the index, so a strict > keeps the lowest id.  t1 propagates
+    //      NaN (IEEE maximum): a NaN or +inf anywhere in the chunk shows in
+    //      t1.
+    float t1 = NEG_INF, t2 = NEG_INF, t3 = NEG_INF, t4 = NEG_INF;
+    int i1 = 0, i2 = 0, i3 = 0;
 #pragma unroll
     for (int j = 0; j < NVT; ++j) {
+        if constexpr (FAST) {
+            if (j + kLook < NVT) issue(j + kLook);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         const int v = t + j * kBlock;
         float f[VEC];
         if constexpr (FAST) {
@@ -277,44 +473,47 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
             for (int e = 0; e < VEC; ++e) f[e] = sx[j * VEC + e];
         }
         // this lane's word of slot j: (lane * VEC / 32) within the slot's run
-        const uint32_t mb = v < nvec ? mw[j * kWpS + ((lane * VEC) >> 5)] >> ((v * VEC) & 31) : 0u;
+        uint32_t mb = v < nvec ? mw[j * kWpS + ((lane * VEC) >> 5)] >> ((v * VEC) & 31) : 0u;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
             const uint32_t sel = (uint32_t)__builtin_amdgcn_sbfe((int)mb, e, 1);
             uint32_t bits = (__float_as_uint(f[e]) & sel) | (0xFF800000u & ~sel);
             if constexpr (!FAST) bits = (e0 + v * VEC + e < e1) ? bits : 0xFF800000u;
             const float g = __uint_as_float(bits);
-            i1 = g > t1 ? j * VEC + e : i1;
-            t2 = __builtin_elementwise_maximum(t2, __builtin_elementwise_minimum(t1, g));
+            const int q = j * VEC + e;
+            const bool c1 = g > t1, c2 = g > t2, c3 = g > t3;
+            i3 = c2 ? i2 : (c3 ? q : i3);
+            i2 = c1 ? i1 : (c2 ? q : i2);
+            i1 = c1 ? q : i1;
+            // t(k+1) <= t(k): the median of the two and g is the new t(k+1)
+            t4 = __builtin_amdgcn_fmed3f(t3, t4, g);
+            t3 = __builtin_amdgcn_fmed3f(t2, t3, g);
+            t2 = __builtin_amdgcn_fmed3f(t1, t2, g);
             t1 = __builtin_elementwise_maximum(t1, g);
-            xv[j * VEC + e] = g;
         }
         // The running state is complete after each slot, so none of this
         // slot's work is deferred past the next slot's wait.
-        asm volatile("" : "+v"(t1), "+v"(t2), "+v"(i1));
+        asm volatile("" : "+v"(t1), "+v"(t2), "+v"(t3), "+v"(t4), "+v"(i1), "+v"(i2), "+v"(i3));
         __builtin_amdgcn_sched_barrier(0);
     }
     TMS_TR(3);
 #ifdef TMS_PROBE_PASS1ONLY
     // Measurement builds stop here, to time the stream and pass 1 alone.
-    if (t1 == 12345.0f && t2 == 1.0f && i1 == 7) a.out_tokens[row] = 0;   // keep the work live
+    if (t1 == 12345.0f && t2 == 1.0f && i1 == 7 && t3 == 2.0f && i2 == 3 && t4 == 0.5f && i3 == 1)
+        a.out_tokens[row] = 0;
     return;
 #endif
 
-    // ---- history penalties.  A chunk entry whose id is in the row's window
-    //      is taken out of the holders' selection (a bitmap of window ids) and
-    //      offered instead, with its penalised value, by the thread that
-    //      counted that id first: the "owner", which loaded the logit with the
-    //      stream.  The compounding penalty (tmsample.h:58-61) needs the id's
-    //      count, from a 16-bit count table.
-    int n_pen = 0;      // penalised candidates in sm.pend (all >= -inf; filtered by thr below)
-    int m_win = 0;      // threads whose maximum is a window entry (the threshold skips them)
-    bool pen_nf = false;
-    if (pn.on) {
-        lds_sync();   // the count table and bitmap are zeroed
-        bool first[kWin];
+    // ---- the history window, counted now that the ids are surely in: each
+    //      window id in this chunk is counted (16 bits per id) and the
+    //      position that counted it first owns it.  Pass 1 saw window ids
+    //      with their raw logits; a thread leaves them out of what it
+    //      publishes (every entry it does not publish stays <= its fourth
+    //      value, so the bound test is unchanged).
+    bool first[kWin];
 #pragma unroll
-        for (int i = 0; i < kWin; ++i) first[i] = false;
+    for (int i = 0; i < kWin; ++i) first[i] = false;
+    if (pn.on) {
         for (int p0 = 0; p0 < nrec; p0 += kWin * kBlock) {
 #pragma unroll
             for (int i = 0; i < kWin; ++i) {
@@ -322,24 +521,25 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                 const int id = (p < from || p >= nrec) ? -1 : (p0 == 0 ? wid[i] : hist[p]);
                 if (id >= e0 && id < e1) {
                     const int off = id - e0;
-                    atomicAdd(&sm.big.cnt[off >> 1], 1u << ((off & 1) * 16));
-                    const uint32_t old = atomicOr(&sm.wbits[off >> 5], 1u << (off & 31));
-                    if (!((old >> (off & 31)) & 1u)) {
+                    const uint32_t sh = (off & 1) * 16;
+                    const uint32_t old = atomicAdd(&sm.big.cnt[off >> 1], 1u << sh);
+                    if (((old >> sh) & 0xFFFFu) == 0) {
                         if (p0 == 0) {
                             first[i] = true;
                         } else {
-                            // past the preloaded positions (windows over
-                            // kWin * kBlock ids): remembered for a late load
-                            const int k = atomicAdd(&sm.nlate, 1);
-                            if (k < kLate) sm.sl.late[k] = id;
+                            const int k = atomicAdd(&sm.nlate, 1);   // long windows: loaded late
+                            if (k < kLate) sm.late[k] = id;
                         }
                     }
                 }
             }
         }
         lds_sync();
-        // owners of the preloaded positions
-        uint32_t flags_nf = 0;
+    }
+
+    // ---- penalised window entries, from their owners
+    bool my_nf = !(t1 < __builtin_huge_valf());   // +inf or NaN among this thread's entries
+    if (pn.on) {
 #pragma unroll
         for (int i = 0; i < kWin; ++i) {
             if (first[i]) {
@@ -348,103 +548,260 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                 const uint32_t cnt = (sm.big.cnt[off >> 1] >> ((off & 1) * 16)) & 0xFFFFu;
                 float g = ((own_m[i] >> (id & 31)) & 1u) ? own_v[i] : NEG_INF;
                 g = apply_pen(g, cnt, pn);
-                flags_nf |= !(g < __builtin_huge_valf()) && g == g ? 1u : 0u;   // +inf after the penalty
-                flags_nf |= g != g ? 1u : 0u;
+                my_nf |= !(g < __builtin_huge_valf()) && g != NEG_INF;   // NaN or +inf
                 const int k = atomicAdd(&sm.npen, 1);
-                if (k < kCand) sm.pend[k] = ((uint64_t)__float_as_uint(g) << 32) | (uint32_t)id;
+                if (k < kPendCap) sm.pend[k] = ckey(g, (uint32_t)id);
             }
         }
-        // owners past the preloaded positions (long windows only)
         const int nlate = min(sm.nlate, kLate);
-        for (int k0 = 0; k0 < nlate; k0 += kBlock) {
+        for (int k0 = 0; k0 < nlate; k0 += kBlock) {   // long windows only
             const int k = k0 + t;
             if (k < nlate) {
-                const int id = sm.sl.late[k];
+                const int id = sm.late[k];
                 const int off = id - e0;
                 const uint32_t cnt = (sm.big.cnt[off >> 1] >> ((off & 1) * 16)) & 0xFFFFu;
-                float g = slow_value(base, mrow, id, e0, Pen{false, false, false, 0.f, 0.f, 0.f}, sm);
+                float g = ((mrow[id >> 5] >> (id & 31)) & 1u) ? Elt<T>::scalar(base + id) : NEG_INF;
                 g = apply_pen(g, cnt, pn);
-                flags_nf |= !(g < __builtin_huge_valf()) ? 1u : 0u;
+                my_nf |= !(g < __builtin_huge_valf()) && g != NEG_INF;
                 const int q = atomicAdd(&sm.npen, 1);
-                if (q < kCand) sm.pend[q] = ((uint64_t)__float_as_uint(g) << 32) | (uint32_t)id;
+                if (q < kPendCap) sm.pend[q] = ckey(g, (uint32_t)id);
             }
         }
-        pen_nf = flags_nf != 0;
-        // threads whose maximum is a window entry
-        const int off1 = (int)id_of<VEC>(t, i1, e0) - e0;
-        const bool w1 = t1 != NEG_INF && ((sm.wbits[off1 >> 5] >> (off1 & 31)) & 1u);
-        m_win = __popcll(__ballot(w1));
     }
-    TMS_TR(18);
+    // per wave: any non-finite entry, and the largest fourth value's key
+    const uint32_t t4k = okey(t4);
+    const bool wnf = __any(my_nf);
+    const uint32_t wt4 = wave_max_u32_dpp(t4k);
+    if (lane == 0) {
+        sm.wave_i[wv] = wnf;
+        sm.wave_u[wv] = wt4;
+    }
+    lds_sync();
+    TMS_TR(13);
+    int flags = (sm.wave_i[0] | sm.wave_i[1] | sm.wave_i[2] | sm.wave_i[3]) ? FLAG_NONFINITE : 0;
+    const uint32_t t4max = max(max(sm.wave_u[0], sm.wave_u[1]), max(sm.wave_u[2], sm.wave_u[3]));
+    const int npen_all = sm.npen;
+    if (npen_all > kPendCap) flags |= FLAG_OVERFLOW;
+    const int npen = min(npen_all, kPendCap);
+    const uint64_t hdr = lean_header(flags, npen, t4max);
 
-    // ---- row mode
+    // ---- publish (no store waits), then the ticket.  Thread t stores its
+    //      three keys, thread i % kBlock penalised entry i, thread 0 the
+    //      header; the same lanes zero them if this workgroup merges (one
+    //      lane stores each word, so its zero lands after it).
+    const uint32_t id1 = id_of<VEC>(t, i1, e0), id2 = id_of<VEC>(t, i2, e0), id3 = id_of<VEC>(t, i3, e0);
+    auto windowed = [&](uint32_t id) {
+        const int off = (int)id - e0;
+        return pn.on && ((sm.big.cnt[off >> 1] >> ((off & 1) * 16)) & 0xFFFFu) != 0;
+    };
+    // a window entry's key is 1: never 0 (data as flag), below every bound
+    const uint64_t k1 = windowed(id1) ? 1ull : ckey(t1, id1);
+    const uint64_t k2 = windowed(id2) ? 1ull : ckey(t2, id2);
+    const uint64_t k3 = windowed(id3) ? 1ull : ckey(t3, id3);
+    uint64_t* row_lists = a.tlists + (int64_t)row * S * kTopkListStride;
+    uint64_t* my_list = row_lists + (int64_t)c * kTopkListStride;
+    st_agent(&my_list[kWordKeys + t], k1);
+    st_agent(&my_list[kWordKeys + kBlock + t], k2);
+    st_agent(&my_list[kWordKeys + 2 * kBlock + t], k3);
+    for (int i = t; i < npen; i += kBlock) st_agent(&my_list[kWordPend + i], sm.pend[i]);
+    if (t == 0) {
+        st_agent(&my_list[0], hdr);
+        const uint32_t ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
+    }
+    TMS_TR(4);
+    lds_sync();
+    if (!sm.misc[0]) {
+        TK_TRACE_FLUSH();
+        return;
+    }
+    TMS_TR(5);
+
+    // ================= merge: the last workgroup of the row =================
+    // Thread t reads the three keys of thread t of every other chunk and the
+    // first kPendRead penalised entries of each chunk (a share of them);
+    // threads < S read the headers.  A word still 0 is read again.
+    if (t == 64) st_agent(&a.counters[row * kCounterStride], 0u);   // ready for the next launch
     const bool greedy = P.greedy != 0;
     const bool bad_params = !greedy && !(P.temperature > 0.0f && P.temperature <= FLT_MAX);
     const int K = greedy ? 1 : ((P.top_k <= 0 || P.top_k > V) ? V : P.top_k);
     const bool unsupported = K > kTopkFast;   // the caller's hint does not hold for this row
     const float temp = P.temperature;
     const bool divide = !greedy && temp != 1.0f;
-    const uint32_t id1 = id_of<VEC>(t, i1, e0);
-    const bool nf = __any(!(t1 < __builtin_huge_valf()));   // +inf or NaN in this wave's entries
-
-    if (lane == 0) {
-        sm.wave_i[wv] = nf || __any(pen_nf);
-        sm.wave_m[wv] = m_win;
-    }
-    sm.tkey[t] = okey(t1);
-    // Greedy rows without penalties take the chunk's best key directly;
-    // others go through the selection below (greedy as K = 1).
-    const bool greedy_fast = greedy && !pn.on;
-    if (greedy_fast) {
-        const uint64_t gb = wave_max_u64_dpp(t1 != NEG_INF ? ckey(t1, id1) : 0ull);
-        if (lane == 0) sm.wave_k[wv] = gb;
-    }
-    // The row ticket, taken as soon as this chunk's stream is in: its round
-    // trip overlaps the selection below.  The last chunk of the row to get
-    // here merges; every other chunk publishes its list (and those all took
-    // their tickets earlier, so none of them waits on the merger).
-    uint32_t ticket = 0;
-    if (t == 0)
-        ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-    lds_sync();
-    TMS_TR(13);
-
-    // ---- selection: the chunk's candidates, sorted, into sm.cand[0..nout).
-    int flags = 0;
-    int nout = 0;
-    const bool anynf = (sm.wave_i[0] | sm.wave_i[1] | sm.wave_i[2] | sm.wave_i[3]) != 0;
-    if (anynf) flags |= FLAG_NONFINITE;
-    if (greedy_fast) {
-        uint64_t b = sm.wave_k[0];
+    // Every word is loaded without a branch (a load under a condition makes
+    // the compiler wait for it where the paths join): slots S..MS-1 read
+    // chunk S-1's words again and are left out where the words are used,
+    // and this workgroup reads its own list back like the others.  Keys and
+    // headers first, then the penalised entries, then the third keys, which
+    // the gather is the first to need.
+    const uint32_t slots = (1u << S) - 1u;   // S <= 16
+    // (tid: the thread index, passed opaque on the rare re-read paths so the
+    // compiler recomputes these addresses there rather than keeping them)
+    auto key_at = [&](int cc, int j, int tid) -> const uint64_t* {
+        return &row_lists[(int64_t)min(cc, S - 1) * kTopkListStride + kWordKeys + j * kBlock + tid];
+    };
+    auto pend_at = [&](int idx) -> const uint64_t* {
+        return &row_lists[(int64_t)min(idx / kPendRead, S - 1) * kTopkListStride + kWordPend + idx % kPendRead];
+    };
+    auto opaque = [](int v) {
+        asm volatile("" : "+v"(v));
+        return v;
+    };
+    const uint64_t* const hdr_at = &row_lists[(int64_t)min(t, S - 1) * kTopkListStride];
+    uint64_t kk[2 * MS];
 #pragma unroll
-        for (int i = 1; i < kWaves; ++i) b = sm.wave_k[i] > b ? sm.wave_k[i] : b;
-        if (t == 0 && b) sm.cand[0] = b;
-        nout = (b && !anynf) ? 1 : 0;
-    } else if (!anynf && !bad_params && !unsupported) {
-        // The (K + M)-th largest of the 256 thread maxima, M the threads
-        // whose maximum is a window entry: K threads then hold a non-window
-        // entry >= it, so it bounds the K-th value from below.  Found bit by
-        // bit on the sixteen high bits of their order keys: `pre` stays a
-        // lower bound, and the few extra candidates it admits are ranked away.
-        const int Kt = K + sm.wave_m[0] + sm.wave_m[1] + sm.wave_m[2] + sm.wave_m[3];
-        const uint4 k4 = ((const uint4*)sm.tkey)[lane];   // 4 keys per lane, all 256
+    for (int cc = 0; cc < MS; ++cc) {
+        kk[2 * cc] = ld_agent(key_at(cc, 0, t));
+        kk[2 * cc + 1] = ld_agent(key_at(cc, 1, t));
+    }
+    uint64_t h = ld_agent(hdr_at);
+    constexpr int kPendPer = MS * kPendRead / kBlock;
+    uint64_t pw[kPendPer];
+#pragma unroll
+    for (int u = 0; u < kPendPer; ++u) pw[u] = ld_agent(pend_at(t + u * kBlock));
+    uint64_t kt[MS];
+#pragma unroll
+    for (int cc = 0; cc < MS; ++cc) kt[cc] = ld_agent(key_at(cc, 2, t));
+    uint32_t w0 = 0, w1 = 0;
+    if (wv == 0) {   // the row's uniform, while the reads are in flight
+        if (a.draws) {
+            w0 = dw0;
+            w1 = dw1;
+        } else {
+            row_words(P.seed, P.offset, 0u, w0, w1);
+        }
+    }
+    // A word still 0 is in flight: the thread reads all of its words again
+    // (a non-zero word does not change until this workgroup zeroes it), a
+    // bounded number of times; spins reaching kPollCap marks the row lost.
+    int spins = 0;
+    bool zero = h == 0;
+#pragma unroll
+    for (int i = 0; i < 2 * MS; ++i) zero |= kk[i] == 0;
+    for (; zero && spins < kPollCap; ++spins) {   // rare
+        __builtin_amdgcn_s_sleep(1);
+        const int tid = opaque(t);
+#pragma unroll
+        for (int cc = 0; cc < MS; ++cc) {
+            kk[2 * cc] = ld_agent(key_at(cc, 0, tid));
+            kk[2 * cc + 1] = ld_agent(key_at(cc, 1, tid));
+        }
+        h = ld_agent(&row_lists[(int64_t)min(tid, S - 1) * kTopkListStride]);
+        zero = h == 0;
+#pragma unroll
+        for (int i = 0; i < 2 * MS; ++i) zero |= kk[i] == 0;
+    }
+    if (zero) spins = kPollCap;
+    auto settle = [&](uint64_t& v, const uint64_t* p) {   // one word, on the rare paths
+        while (v == 0 && spins < kPollCap) {
+            __builtin_amdgcn_s_sleep(1);
+            v = ld_agent(p);
+            ++spins;
+        }
+    };
+    if (t < kLeanMaxChunks) sm.hdr[t] = t < S ? h : 1ull;   // 1: no flags, entries or fourth value
+    if (t == 0) {
+        sm.misc[3] = 0;   // a word never arrived
+        sm.ncand = 0;
+    }
+    // group maxima: the largest first key of thread t over the chunks
+    uint32_t gm = 0;
+#pragma unroll
+    for (int cc = 0; cc < MS; ++cc) gm = max(gm, cc < S ? (uint32_t)(kk[2 * cc] >> 32) : 0u);
+    sm.gkey[t] = gm;
+    lds_sync();
+    TMS_TR(6);
+    // the penalised entries read with the keys; past kPendRead (rare) below
+    bool plive[kPendPer];
+#pragma unroll
+    for (int u = 0; u < kPendPer; ++u) {
+        const int idx = t + u * kBlock;
+        const int cc = idx / kPendRead;
+        plive[u] = cc < S && cc != c && idx % kPendRead < hdr_npen(sm.hdr[cc]);
+    }
+    // The third keys and penalised entries, first needed by the gather:
+    // waited for there (their loads stay in flight through the bound), and
+    // on an error row before the words are zeroed.
+    auto late_zero = [&]() {
+        bool z = false;
+#pragma unroll
+        for (int u = 0; u < kPendPer; ++u) z |= plive[u] && pw[u] == 0;
+#pragma unroll
+        for (int cc = 0; cc < MS; ++cc) z |= kt[cc] == 0;
+        return z;
+    };
+    auto settle_late = [&]() {
+        bool z = late_zero();
+        for (; z && spins < kPollCap; ++spins) {   // rare: read them all again
+            __builtin_amdgcn_s_sleep(1);
+            const int tid = opaque(t);
+#pragma unroll
+            for (int cc = 0; cc < MS; ++cc) kt[cc] = ld_agent(key_at(cc, 2, tid));
+#pragma unroll
+            for (int u = 0; u < kPendPer; ++u) pw[u] = ld_agent(pend_at(tid + u * kBlock));
+            z = late_zero();
+        }
+        if (z) spins = kPollCap;
+        if (spins >= kPollCap) sm.misc[3] = 1;
+    };
+    if (spins >= kPollCap) sm.misc[3] = 1;
+    // the headers (1 past S): flags, largest fourth values, penalised
+    // entries past the first read
+    int fo = 0;
+    uint32_t t4all = 0;
+    int pextra = 0;
+    {
+        const uint4* h4 = (const uint4*)sm.hdr;
+#pragma unroll
+        for (int i = 0; i < kLeanMaxChunks / 2; ++i) {
+            const uint4 q = h4[i];
+            const uint64_t hh[2] = {((uint64_t)q.y << 32) | q.x, ((uint64_t)q.w << 32) | q.z};
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                fo |= hdr_flags(hh[e]);
+                t4all = max(t4all, (uint32_t)hh[e]);
+                pextra += 2 * i + e == c ? 0 : max(hdr_npen(hh[e]) - kPendRead, 0);
+            }
+        }
+    }
+    lds_sync();   // misc[3]
+    TMS_TR(10);
+    int status = TMS_ROW_OK;
+    if (sm.misc[3]) status = TMS_ROW_INTERNAL;
+    else if (unsupported) status = TMS_ROW_UNSUPPORTED;
+    else if (bad_params) status = TMS_ROW_BAD_PARAMS;
+    else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
+
+    uint64_t* srt = sm.big.m.srt;
+    int n = 0;        // candidates gathered, then the sorted top-K kept
+    int N = 0;        // finite entries of the row when fewer than K, else >= K
+    bool all_finite = false;
+    int ngath = 0;    // keys placed by the gather's scan
+    bool late_done = false;   // third keys and penalised entries waited for
+    if (status == TMS_ROW_OK) {
+        // ---- the bound: the K-th largest of the 256 group maxima (K groups
+        //      hold an entry >= it, so it bounds the row's K-th value from
+        //      below), bit by bit on the sixteen high bits of the order keys.
+        const uint4 g4 = ((const uint4*)sm.gkey)[lane];
         uint32_t pre = 0;
         for (int bit = 31; bit >= 16; --bit) {
             const uint32_t cand = pre | (1u << bit);
-            const uint64_t m0 = __builtin_amdgcn_uicmp(k4.x, cand, 35);   // unsigned >=
-            const uint64_t m1 = __builtin_amdgcn_uicmp(k4.y, cand, 35);
-            const uint64_t m2 = __builtin_amdgcn_uicmp(k4.z, cand, 35);
-            const uint64_t m3 = __builtin_amdgcn_uicmp(k4.w, cand, 35);
-            if (__popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3) >= Kt) pre = cand;
+            const uint64_t m0 = __builtin_amdgcn_uicmp(g4.x, cand, 35);   // unsigned >=
+            const uint64_t m1 = __builtin_amdgcn_uicmp(g4.y, cand, 35);
+            const uint64_t m2 = __builtin_amdgcn_uicmp(g4.z, cand, 35);
+            const uint64_t m3 = __builtin_amdgcn_uicmp(g4.w, cand, 35);
+            if (__popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3) >= K) pre = cand;
         }
+        TMS_TR(11);
         // Keys below okey(-FLT_MAX) decode to -inf or NaN: every finite entry.
-        float thr = pre < 0x00800000u ? -FLT_MAX : okey_inv(pre);
-        // Division can merge neighbouring values: lower the threshold to the
+        all_finite = pre < 0x00800000u;
+        float thr = all_finite ? -FLT_MAX : okey_inv(pre);
+        // Division can merge neighbouring values: lower the bound to the
         // smallest float with the same quotient, so every entry tying the
         // K-th quotient is a candidate.
-        bool fallback = false;
-        if (divide && thr != NEG_INF) {
+        bool radix = (fo & FLAG_OVERFLOW) != 0;
+        if (divide && !all_finite) {
             const float qt = thr / temp;
             int it = 0;
             for (; it < 64; ++it) {
@@ -452,290 +809,206 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                 if (p / temp == qt) thr = p;
                 else break;
             }
-            fallback = it == 64;
+            radix |= it == 64;
+            if (thr == -__builtin_huge_valf()) thr = -FLT_MAX;
         }
-        if (thr == NEG_INF) thr = -FLT_MAX;   // every finite entry
+        const uint32_t kb = okey(thr);
+        settle_late();
+        late_done = true;
         TMS_TR(9);
-        int n = kCand + 1;
-        if (!fallback) {
-            // A thread whose second value is below thr holds at most one
-            // entry >= thr, its maximum: one ballot places those.  A thread
-            // holding several stages its values in LDS, and the wave tests
-            // one staged thread per step, an entry per lane.
-            auto in_window = [&](uint32_t id) -> bool {
-                const int off = (int)id - e0;
-                return pn.on && ((sm.wbits[off >> 5] >> (off & 31)) & 1u);
-            };
-            const bool multi = t2 >= thr;
-            const bool one = t1 >= thr && !multi && !in_window(id1);
-            const uint64_t m1 = __ballot(one);
-            int wbase = 0;
-            if (lane == 0 && m1) wbase = atomicAdd(&sm.ncand, __popcll(m1));
-            wbase = __builtin_amdgcn_readfirstlane(wbase);
-            const int r1 = __builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32),
-                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m1, 0u));
-            if (one && wbase + r1 < kCand)
-                sm.cand[wbase + r1] = ((uint64_t)__float_as_uint(t1) << 32) | id1;
-            uint64_t mm = __ballot(multi);
-            float* stage = sm.sl.stage[wv];
-            while (mm) {
-                // up to kStage threads of the wave at a time
-                const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
-                const bool mine = ((mm >> lane) & 1ull) && rank < kStage;
-                if (mine) {
-                    float4* dst = (float4*)(stage + rank * kEpt);
+        // Chunks whose largest fourth value reaches the bound are read again
+        // whole; their published keys are left out.
+        uint32_t reread = 0;
+        if (t4all >= kb)
+            for (int cc = 0; cc < S; ++cc)
+                if ((uint32_t)sm.hdr[cc] >= kb) reread |= 1u << cc;
+        const uint32_t use = slots & ~reread;   // chunk slots whose keys are gathered
+        TMS_TV(14, __popc(reread) + 1);
+        // ---- the gather from registers: each thread counts the keys it
+        //      takes (its three keys of every chunk not read again, its share
+        //      of the first penalised reads, this workgroup's penalised entry
+        //      t), one block scan places them, and every key is stored, the
+        //      ones not taken to a slot of this thread's own (no branches);
+        //      sm.ncand then counts what the rare paths below append.
+                auto above = [&](uint64_t k) { return (uint32_t)(k >> 32) >= kb; };
+        int mine = 0;
 #pragma unroll
-                    for (int q = 0; q < kEpt / 4; ++q)
-                        dst[q] = make_float4(xv[4 * q], xv[4 * q + 1], xv[4 * q + 2], xv[4 * q + 3]);
-                }
-                const uint64_t taken = __ballot(mine);
-                wave_lds_sync();
-                uint64_t tk = taken;
-                for (int si = 0; tk; ++si) {
-                    const int L = __builtin_ctzll(tk);   // the staged thread: wave lane L
-                    tk &= tk - 1;
-                    // lane q tests entry q of thread L (slot q / VEC, element q % VEC)
-                    const float f = stage[si * kEpt + lane];
-                    const int tt = wv * 64 + L;
-                    const uint32_t idq = id_of<VEC>(tt, lane, e0);
-                    const bool hit = f >= thr && !in_window(idq);
-                    const uint64_t mh = __ballot(hit);
-                    int hb = 0;
-                    if (lane == 0) hb = atomicAdd(&sm.ncand, __popcll(mh));
-                    hb = __builtin_amdgcn_readfirstlane(hb);
-                    const int pos = hb + __builtin_amdgcn_mbcnt_hi((uint32_t)(mh >> 32),
-                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mh, 0u));
-                    if (hit && pos < kCand) sm.cand[pos] = ((uint64_t)__float_as_uint(f) << 32) | idq;
-                }
-                mm &= ~taken;
-                wave_lds_sync();
-            }
-            if (pn.on) {
-                // the window entries, with their penalised values
-                const int np = min(sm.npen, kCand);
-                for (int i0 = 0; i0 < np; i0 += kBlock) {
+        for (int i = 0; i < 2 * MS; ++i) mine += (int)(((use >> (i / 2)) & 1u) && above(kk[i]));
+#pragma unroll
+        for (int i = 0; i < MS; ++i) mine += (int)(((use >> i) & 1u) && above(kt[i]));
+        bool pl[kPendPer];
+#pragma unroll
+        for (int u = 0; u < kPendPer; ++u) {
+            pl[u] = plive[u] && above(pw[u]);
+            mine += (int)pl[u];
+        }
+        const uint64_t op = t < npen ? sm.pend[t] : 0ull;
+        const bool ownp = t < npen && above(op);
+        mine += (int)ownp;
+        int pos = block_excl_scan(mine, ngath, sm);
+        uint64_t* const junk = (uint64_t*)sm.big.m.pr + t;   // the tail's scratch, free until then
+        auto put = [&](bool take, uint64_t k) {
+            *(take && pos < kCand ? &sm.cand[pos] : junk) = k;
+            pos += (int)take;
+        };
+#pragma unroll
+        for (int i = 0; i < 2 * MS; ++i) put(((use >> (i / 2)) & 1u) && above(kk[i]), kk[i]);
+#pragma unroll
+        for (int i = 0; i < MS; ++i) put(((use >> i) & 1u) && above(kt[i]), kt[i]);
+#pragma unroll
+        for (int u = 0; u < kPendPer; ++u) put(pl[u], pw[u]);
+        put(ownp, op);
+        TMS_TR(18);
+        for (int i0 = kBlock; i0 < npen; i0 += kBlock) {   // this workgroup's own past kBlock
+            const int i = i0 + t;
+            const uint64_t v = i < npen ? sm.pend[i] : 0ull;
+            append_cand(sm, i < npen && above(v), v, ngath);
+        }
+        if (pextra) {
+            // penalised entries past the first read (more than kPendRead
+            // window ids in a chunk)
+            for (int cc = 0; cc < S; ++cc) {
+                if (cc == c) continue;
+                const int npc = hdr_npen(sm.hdr[cc]);
+                for (int i0 = kPendRead; i0 < npc; i0 += kBlock) {
                     const int i = i0 + t;
-                    const uint64_t pe = i < np ? sm.pend[i] : 0ull;
-                    const bool hit = i < np && __uint_as_float((uint32_t)(pe >> 32)) >= thr;
-                    const uint64_t mh = __ballot(hit);
-                    int hb = 0;
-                    if (lane == 0 && mh) hb = atomicAdd(&sm.ncand, __popcll(mh));
-                    hb = __builtin_amdgcn_readfirstlane(hb);
-                    const int pos = hb + __builtin_amdgcn_mbcnt_hi((uint32_t)(mh >> 32),
-                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mh, 0u));
-                    if (hit && pos < kCand) sm.cand[pos] = pe;
+                    uint64_t v = 0;
+                    if (i < npc) {
+                        const uint64_t* p = &row_lists[(int64_t)cc * kTopkListStride + kWordPend + i];
+                        v = ld_agent(p);
+                        settle(v, p);
+                    }
+                    append_cand(sm, i < npc && above(v), v, ngath);
                 }
-                if (sm.npen > kCand && t == 0) atomicAdd(&sm.ncand, kCand);   // overflow: the fallback
             }
+            if (spins >= kPollCap) sm.misc[3] = 1;
+        }
+        // ---- chunks read again (rare): the whole chunk in one round of
+        //      loads (pass 1's layout), every entry >= the bound that is not
+        //      a window id of the chunk (a bitmap from its penalised entries)
+        for (int cc = 0; cc < S && !radix; ++cc) {
+            if (!((reread >> cc) & 1u)) continue;
+            // the chunk's window ids as a bitmap: from registers, the list
+            // past the first read
+            const int ce0 = cc * a.CE;
+            auto mark = [&](uint64_t pe) {
+                const int off = (int)ckey_id(pe) - ce0;
+                atomicOr(&sm.big.wbits[off >> 5], 1u << (off & 31));
+            };
             lds_sync();
-            n = sm.ncand;
-        }
-        TMS_TR(10);
-        TMS_TV(15, n + 1);
-        if (n <= kCand) {
-            // Divide the candidates and form their keys, then rank them by
-            // counting; the chunk's list is its top min(n, K).
-            uint64_t* keys = sm.big.m.uni;
-            for (int i = t; i < n; i += kBlock) {
-                const uint64_t rw = sm.cand[i];
-                const float f = __uint_as_float((uint32_t)(rw >> 32));
-                keys[i] = ckey(divide ? f / temp : f, (uint32_t)rw);
-            }
-            TMS_TR(11);
-            rank_sort(keys, n, sm.cand, K);
-            nout = n < K ? n : K;
-        } else {
-            nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn, sm);
-            sort_cand(nout, sm);
-        }
-    }
-    TMS_TR(4);
-
-    // ---- publish, or merge.  Each list is a ready header and K entries (key
-    //      1 past nout), all non-zero; the merger zeroes what it read, so a
-    //      word still in flight reads 0 and is read again.
-    const int r = K > kTopkFast ? 0 : K;
-    const int R1 = r + 1;
-    const int NW = S * R1;
-    const float rcp_r1 = 1.0f / (float)R1;
-    const uint64_t hdr = kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout;
-    uint64_t* row_lists = a.lists + (int64_t)row * S * kListStride;
-    if (t == 0) sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
-    lds_sync();
-    if (!sm.misc[0]) {
-        uint64_t* my_list = row_lists + (int64_t)c * kListStride;
-        for (int i = t; i <= r; i += kBlock)
-            st_agent(&my_list[i], i == 0 ? hdr : (i <= nout ? sm.cand[i - 1] : (uint64_t)1));
-        return;
-    }
-    TMS_TR(5);
-
-    // ================= merge: the last workgroup of the row =================
-    // Read every other list whole (waves 0-3), the row's uniform formed by
-    // wave 0 meanwhile.
-    constexpr int kReadPer = (kLeanUni + kBlock - 1) / kBlock;
-    uint64_t sp[kReadPer];
-#pragma unroll
-    for (int u = 0; u < kReadPer; ++u) {
-        const int idx = t + u * kBlock;
-        sp[u] = 0;
-        if (idx < NW) {
-            const int cc = list_of(idx, rcp_r1);
-            if (cc != c) sp[u] = ld_agent(&row_lists[(int64_t)cc * kListStride + (idx - cc * R1)]);
-        }
-    }
-    uint32_t w0 = 0, w1 = 0;
-    if (wv == 0) row_uniform(a, row, P, w0, w1);
-    if (t == 64) st_agent(&a.counters[row * kCounterStride], 0u);   // ready for the next launch
-    uint64_t* uni = sm.big.m.uni;
-    if (t == 0) {
-        sm.theta = 0;     // lists to read again (bit per list)
-        sm.misc[3] = 0;   // a list never arrived
-    }
-    {
-        // Every word read must be set: a ready header, non-zero entries.
-        int bad = 0;
-#pragma unroll
-        for (int u = 0; u < kReadPer; ++u) {
-            const int idx = t + u * kBlock;
-            if (idx < NW) {
-                const int cc = list_of(idx, rcp_r1), jj = idx - cc * R1;
-                uint64_t v = sp[u];
-                if (cc == c) v = jj == 0 ? hdr : (jj <= nout ? sm.cand[jj - 1] : (uint64_t)1);
-                else bad |= (jj == 0 ? !(v & kReady) : v == 0) ? 1 : 0;
-                uni[idx] = v;
-            }
-        }
-        if (__ballot(bad) && lane == 0) atomicOr(&sm.misc[2], 1);
-        lds_sync();
-        // Lists read before they were complete are read again in rounds:
-        // wave 0 waits (bounded) for their ready headers, then every thread
-        // re-reads their entries at once.
-        int rounds = 0;
-        for (int round = 0; sm.misc[2]; ++round) {
-            rounds = round + 1;
-            for (int idx = t; idx < NW; idx += kBlock) {
-                const int cc = list_of(idx, rcp_r1), jj = idx - cc * R1;
-                const uint64_t h = uni[cc * R1];
-                if (!(h & kReady) || (jj >= 1 && uni[idx] == 0))
-                    atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
-            }
+            for (int i = t; i < kChunk / 32; i += kBlock) sm.big.wbits[i] = 0;
             lds_sync();
-            const uint64_t redo = sm.theta;
-            if (redo == 0 || sm.misc[3]) break;
-            if (round == kReadRounds) {
-                if (t == 0) sm.misc[3] = 1;
-                lds_sync();
-                break;
-            }
-            lds_sync();   // every thread has read theta
-            if (t == 0) sm.theta = 0;
-            if (wv == 0 && lane < S && ((redo >> lane) & 1)) {
-                uint64_t h = 0;
-                for (int it = 0; it < kPollCap; ++it) {
-                    h = ld_agent(&row_lists[(int64_t)lane * kListStride]);
-                    if (h & kReady) break;
-                    __builtin_amdgcn_s_sleep(1);
+            const int npc = hdr_npen(sm.hdr[cc]);
+            if (cc == c) {
+                for (int i = t; i < npen; i += kBlock) mark(sm.pend[i]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < kPendPer; ++u) {
+                    const int idx = t + u * kBlock;
+                    if (idx / kPendRead == cc && idx % kPendRead < npc) mark(pw[u]);
                 }
-                uni[lane * R1] = h;
-                if (!(h & kReady)) sm.misc[3] = 1;
+                for (int i = kPendRead + t; i < npc; i += kBlock)
+                    mark(ld_agent(&row_lists[(int64_t)cc * kTopkListStride + kWordPend + i]));
             }
             lds_sync();
-            for (int idx = t; idx < NW; idx += kBlock) {
-                const int cc = list_of(idx, rcp_r1), jj = idx - cc * R1;
-                if (jj == 0 || !((redo >> cc) & 1)) continue;
-                uni[idx] = ld_agent(&row_lists[(int64_t)cc * kListStride + jj]);
-            }
-            lds_sync();
-        }
-        TMS_TV(14, rounds + 1);
-    }
-    TMS_TR(6);
-    // Headers: counts and flags; lower bounds tau on the row's K-th key: a
-    // list's K-th entry (that list alone holds K keys >= it), or the
-    // smallest m-th entry over all lists, m = ceil(K / S) (the S lists hold
-    // S * m >= K keys >= it).  Every wave forms them, so no barrier follows.
-    int n_c = 0, f_c = 0;
-    uint64_t kth = 0, mth = ~0ull;
-    if (lane < S) {
-        const uint64_t h = uni[lane * R1];
-        n_c = (int)(uint32_t)h;
-        f_c = (int)((h >> 32) & 0xFF);
-        const int m = (K + S - 1) / S;
-        kth = (r > 0 && n_c >= K) ? uni[lane * R1 + K] : 0ull;
-        mth = (r > 0 && n_c >= m) ? uni[lane * R1 + m] : 0ull;
-        if (wv == 0) sm.list_n[lane] = n_c;
-    }
-    const int N = wave_sum_dpp(n_c);
-    const bool any_nf = __ballot(lane < S && (f_c & FLAG_NONFINITE)) != 0;
-    const uint64_t tau = max(wave_max_u64_dpp(kth), ~wave_max_u64_dpp(~mth));
-    int status = TMS_ROW_OK;
-    if (sm.misc[3]) status = TMS_ROW_INTERNAL;
-    else if (unsupported) status = TMS_ROW_UNSUPPORTED;
-    else if (bad_params) status = TMS_ROW_BAD_PARAMS;
-    else if (any_nf) status = TMS_ROW_NONFINITE;
-    else if (N == 0) status = TMS_ROW_ALL_MASKED;
-
-    uint64_t* srt = sm.big.m.srt;
-    const int n_acc = min(N, K);
-    bool whole = false;
-    if (status == TMS_ROW_OK) {
-        // Every key >= tau, gathered in parallel (unordered), then ranked by
-        // counting within that set: it is closed upward, so ranks are exact.
-        if (t == 0) sm.ncand = 0;
-        lds_sync();
-        for (int i0 = 0; i0 < NW; i0 += kBlock) {
-            const int idx = i0 + t;
-            bool keepit = false;
-            uint64_t k = 0;
-            if (idx < NW) {
-                const int cc = list_of(idx, rcp_r1), jj = idx - cc * R1;
-                k = uni[idx];
-                keepit = jj >= 1 && jj <= (int)(uint32_t)uni[cc * R1] && k >= tau;
-            }
-            const uint64_t m = __ballot(keepit);
-            int wb = 0;
-            if (lane == 0 && m) wb = atomicAdd(&sm.ncand, __popcll(m));
-            wb = __builtin_amdgcn_readfirstlane(wb);
-            const int pos = wb + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (keepit && pos < kCand) sm.cand[pos] = k;
+            reread_chunk<T, FAST>(base, mrow, ce0, min(ce0 + a.CE, V), kb, ngath, sm);
         }
         lds_sync();
         TMS_TR(12);
-        const int nc = sm.ncand;
-        TMS_TV(17, nc + 1);
-        if (nc <= kCand) {
-            rank_sort(sm.cand, nc, srt, n_acc);
-        } else {
-            // A weak tau (rare): rank every list entry by binary search in
-            // the other lists, all of them in LDS (uni).
-            whole = true;
-            for (int idx = t; idx < NW; idx += kBlock) {
-                const int cc = list_of(idx, rcp_r1), jj = idx - cc * R1;
-                if (jj == 0 || jj > sm.list_n[cc]) continue;
-                const uint64_t k = uni[idx];
-                int rank = jj - 1;
-                for (int o = 0; o < S; ++o)
-                    if (o != cc) rank += count_greater(uni + o * R1 + 1, sm.list_n[o], k);
-                if (rank < n_acc) srt[rank] = k;
+        n = ngath + sm.ncand;
+        TMS_TV(17, n + 1);
+        if (sm.misc[3]) {
+            status = TMS_ROW_INTERNAL;
+        } else if (radix || n > kCand) {
+            // Massive ties (or too many penalised entries for the lists): the
+            // exact top-K by a radix select over the whole row read again,
+            // with every penalised entry of the row in sm.big.m.keys.
+            if (t == 0) sm.ncand = 0;
+            lds_sync();
+            for (int cc = 0; cc < S; ++cc) {
+                const int npc = hdr_npen(sm.hdr[cc]);
+                for (int i = t; i < npc; i += kBlock) {
+                    const uint64_t pe = cc == c ? sm.pend[i]
+                                                : ld_agent(&row_lists[(int64_t)cc * kTopkListStride + kWordPend + i]);
+                    const int pos = atomicAdd(&sm.ncand, 1);
+                    if (pos < kCand) sm.big.m.keys[pos] = pe;
+                }
             }
             lds_sync();
+            const int np = min(sm.ncand, kCand);
+            lds_sync();
+            if ((fo & FLAG_OVERFLOW) || sm.ncand > kCand) {
+                status = TMS_ROW_UNSUPPORTED;   // more window ids in the row than staging holds
+            } else {
+                n = lean_row_radix<T>(base, mrow, sm.big.m.keys, np, V, K, temp, divide, sm);
+                all_finite = n < K;
+                TMS_TV(16, 2);
+            }
+        }
+        if (status == TMS_ROW_OK) {
+            // Divide the candidates and form their keys, then rank them by
+            // counting; the row's sorted top min(n, K) lands in srt.
+            uint64_t* keys = sm.big.m.keys;
+            for (int i = t; i < n; i += kBlock) {
+                const uint64_t rw = sm.cand[i];
+                const float f = ckey_val(rw);
+                keys[i] = ckey(divide ? f / temp : f, ckey_id(rw));
+            }
+            rank_sort(keys, n, srt, K);
+            // With the bound at "every finite entry" the gather holds every
+            // finite entry of the row.
+            N = all_finite ? n : K;
+            if (N == 0) status = TMS_ROW_ALL_MASKED;
+            n = min(n, K);
         }
     }
-    (void)whole;
-    // Every word of this call's lists goes back to zero for the next call;
-    // on a sampled row's success path waves 1-3 do it while wave 0 runs the
-    // tail.
-    const bool defer_zero = status == TMS_ROW_OK && !greedy && !sm.misc[3];
-    if (!defer_zero && !sm.misc[3]) zero_lean_lists(row_lists, S, r, c, t, kBlock);
+    // Every word read goes back to zero for the next call: the other
+    // chunks' headers, keys and penalised entries; this workgroup's own by
+    // the lanes that stored them.  Waves 1-3 zero the other chunks' words
+    // while wave 0 runs a sampled row's tail.
+    const bool lost = sm.misc[3] != 0;
+    auto zero_own = [&]() {
+        st_agent(&my_list[kWordKeys + t], (uint64_t)0);
+        st_agent(&my_list[kWordKeys + kBlock + t], (uint64_t)0);
+        st_agent(&my_list[kWordKeys + 2 * kBlock + t], (uint64_t)0);
+        for (int i = t; i < npen; i += kBlock) st_agent(&my_list[kWordPend + i], (uint64_t)0);
+        if (t == 0) st_agent(&my_list[0], (uint64_t)0);
+    };
+    auto zero_others = [&](int tid0, int nthr) {
+        for (int cc = 0; cc < S; ++cc) {
+            if (cc == c) continue;
+            uint64_t* L = row_lists + (int64_t)cc * kTopkListStride;
+            const int npc = hdr_npen(sm.hdr[cc]);
+            for (int i = tid0; i < kWordPend; i += nthr) st_agent(&L[i], (uint64_t)0);
+            for (int i = tid0; i < npc; i += nthr) st_agent(&L[kWordPend + i], (uint64_t)0);
+        }
+    };
+    if (!late_done) {   // a row that ended before the bound (uniform)
+        if (!sm.misc[3]) settle_late();
+        lds_sync();
+    }
+    if (!lost && pextra && status != TMS_ROW_OK) {
+        // penalised words past the first read: read (once written) before
+        // they are zeroed
+        for (int cc = 0; cc < S; ++cc) {
+            if (cc == c) continue;
+            const int npc = hdr_npen(sm.hdr[cc]);
+            for (int i = kPendRead + t; i < npc; i += kBlock) {
+                const uint64_t* p = &row_lists[(int64_t)cc * kTopkListStride + kWordPend + i];
+                uint64_t v = ld_agent(p);
+                settle(v, p);
+            }
+        }
+    }
+    if (!lost) zero_own();
+    const bool sampled_ok = status == TMS_ROW_OK && !greedy;
+    if (!lost && !sampled_ok) zero_others(t, kBlock);
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
+        TK_TRACE_FLUSH();
         return;
     }
     TMS_TR(7);
-
     if (greedy) {
         const int tok = (int)ckey_id(srt[0]);
         if (t == 0) {
@@ -747,10 +1020,9 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
             if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
             if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
         }
+        TK_TRACE_FLUSH();
         return;
     }
-
-    int n = n_acc;
     if (N < K) {
         // Fewer than K finite ids: the tail goes on with -inf entries in
         // ascending id order, i.e. the ids in [0, K + N) missing from the
@@ -766,17 +1038,13 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         lds_sync();
         n = K;
     }
-    if (ckey_val(srt[0]) == __builtin_huge_valf()) {
-        zero_lean_lists(row_lists, S, r, c, t, kBlock);
-        write_row_error(a, row, TMS_ROW_NONFINITE);
-        return;
-    }
     if (wv == 0) {
-        tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand, w0, w1);
+        tail_topk(a, row, P, srt, n, K, sm.big.m.pr, (double*)sm.cand, w0, w1);
         TMS_TR(8);
     } else {
-        zero_lean_lists(row_lists, S, r, c, t - 64, kBlock - 64);
+        zero_others(t - 64, kBlock - 64);
     }
+    TK_TRACE_FLUSH();
 }
 
 }  // namespace tms
@@ -785,7 +1053,11 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
 // tms_sample_common.h): same argument block as the general kernel.
 int tms_launch_topk(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream) {
     const dim3 grid((unsigned)(batch * k.S)), block(tms::kBlock);
-#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::topk_kernel<T, F>), grid, block, 0, stream, k)
+#define TMS_LAUNCH(T, F)                                                                  \
+    do {                                                                                  \
+        if (k.S <= 8) hipLaunchKernelGGL((tms::topk_kernel<T, F, 8>), grid, block, 0, stream, k); \
+        else hipLaunchKernelGGL((tms::topk_kernel<T, F, 16>), grid, block, 0, stream, k);        \
+    } while (0)
     switch (dtype) {
         case TMS_DTYPE_F32:
             if (fast) TMS_LAUNCH(float, true);
