@@ -7,6 +7,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -22,7 +23,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-fno-fast-math",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
@@ -31,21 +31,44 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
 ]
 
+# Per-file flags.  The top-k kernel takes its row ticket as soon as its
+# stream is in and uses the result only after publishing; the atomic
+# optimizer would rewrite that single-lane atomic into a wave-wide one whose
+# result is broadcast at once, waiting out the round trip there.
+FILE_FLAGS = {
+    "tms_topk.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+BUILD_DIR = os.path.join(HERE, "_build")
+
 
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", LIB + ".tmp", *srcs]
+def _run(cmd: list, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed building libtmsample_hip.so")
+        raise RuntimeError("hipcc failed building libtmsample_hip.so: " + " ".join(cmd))
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every source to an object (in parallel), then links the library."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include")]
+    jobs = []
+    for src in SOURCES:
+        obj = os.path.join(BUILD_DIR, src + ".o")
+        jobs.append((obj, [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), *inc, "-c", "-o", obj,
+                           os.path.join(CSRC, src)]))
+    workers = min(len(jobs), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        list(ex.map(lambda j: _run(j[1], verbose), jobs))
+    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB + ".tmp", *[j[0] for j in jobs]], verbose)
     os.replace(LIB + ".tmp", LIB)
     return LIB
 

@@ -75,7 +75,8 @@ struct LeanSmem {
     alignas(16) uint64_t hdr[kLeanMaxChunks];   // merge: the chunks' headers (1 past S)
     int wave_i[kWaves];
     uint32_t wave_u[kWaves];
-    int hist[256];
+    alignas(16) int hist[256];
+    alignas(16) int hist2[256];
     int ncand;
     int npen, nlate;
     int misc[8];
@@ -180,28 +181,31 @@ __device__ __forceinline__ void append_cand(SM& sm, bool take, uint64_t key, int
     if (take && pos < kCand) sm.cand[pos] = key;
 }
 
-// The published value of id in a row: the penalised value of a window entry
-// (found in `pend`, np entries), else the logit masked.
+// The key value of id in a row (the logit divided by the temperature when
+// `divide`): a window entry's penalised value as published (in `pend`, np
+// entries, already divided), else the logit masked.
 template <typename T>
 __device__ __forceinline__ float row_value(const T* base, const uint32_t* mrow, const uint64_t* pend,
-                                           int np, int id) {
+                                           int np, int id, float temp, bool divide) {
     for (int i = 0; i < np; ++i)
         if ((int)ckey_id(pend[i]) == id) return ckey_val(pend[i]);
-    return ((mrow[id >> 5] >> (id & 31)) & 1u) ? Elt<T>::scalar(base + id) : -__builtin_huge_valf();
+    if (!((mrow[id >> 5] >> (id & 31)) & 1u)) return -__builtin_huge_valf();
+    const float x = Elt<T>::scalar(base + id);
+    return divide ? x / temp : x;
 }
 
 // The exact top-K of a whole row by (lg desc, id asc), for rows the bound
 // cannot narrow (massive ties, or more penalised entries than a list holds):
 // a radix select over the keys of lg = v / T, 8 bits a pass, with the row
 // read again from memory (row_value).  `pend` holds every penalised entry of
-// the row (np of them, read from the lists).  Writes sm.cand as ckey(value,
+// the row (np of them, read from the lists).  Writes sm.cand as ckey(lg,
 // id), unsorted; returns the count (<= K).
 template <typename T, typename SM>
 __device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, const uint64_t* pend,
                                            int np, int V, int K, float temp, bool divide, SM& sm) {
     const int t = threadIdx.x;
     const float NEG_INF = -__builtin_huge_valf();
-    auto lkey = [&](float v) { return okey(divide ? v / temp : v); };
+    auto lkey = [](float v) { return okey(v); };
     uint32_t prefix = 0, pmask = 0;
     int remaining = K;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -209,7 +213,7 @@ __device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, 
         if (t == 0) sm.ncand = 0;
         lds_sync();
         for (int id = t; id < V; id += kBlock) {
-            const float v = row_value(base, mrow, pend, np, id);
+            const float v = row_value(base, mrow, pend, np, id, temp, divide);
             if (v == NEG_INF) continue;
             const uint32_t k = lkey(v);
             if ((k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 0xFF], 1);
@@ -221,7 +225,7 @@ __device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, 
         if (shift == 24 && total <= K) {
             // At most K finite entries: all of them.
             for (int id = t; id < V; id += kBlock) {
-                const float v = row_value(base, mrow, pend, np, id);
+                const float v = row_value(base, mrow, pend, np, id, temp, divide);
                 if (v == NEG_INF) continue;
                 const int pos = atomicAdd(&sm.ncand, 1);
                 sm.cand[pos] = ckey(v, (uint32_t)id);
@@ -241,7 +245,7 @@ __device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, 
     }
     // prefix is the K-th largest key; K - remaining keys are strictly greater.
     for (int id = t; id < V; id += kBlock) {
-        const float v = row_value(base, mrow, pend, np, id);
+        const float v = row_value(base, mrow, pend, np, id, temp, divide);
         if (v == NEG_INF) continue;
         if (lkey(v) > prefix) {
             const int pos = atomicAdd(&sm.ncand, 1);
@@ -257,7 +261,7 @@ __device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, 
         float v = NEG_INF;
         int tie = 0;
         if (id < V) {
-            v = row_value(base, mrow, pend, np, id);
+            v = row_value(base, mrow, pend, np, id, temp, divide);
             tie = v != NEG_INF && lkey(v) == prefix;
         }
         int tot;
@@ -270,14 +274,40 @@ __device__ __noinline__ int lean_row_radix(const T* base, const uint32_t* mrow, 
     return g + (taken < remaining ? taken : remaining);
 }
 
+// Wave 0: the digit d of the K-th largest count in the 256-bin histogram
+// h (K >= 1, at least K counted) and the count in the bins above d, into
+// sm.misc[4] and sm.misc[5].  Lane l sums bins 255-4l .. 252-4l; the lane
+// whose running sum crosses K finds the bin.
+template <typename SM>
+__device__ __forceinline__ void pick_digit(const int* h, int K, SM& sm) {
+    const int l = threadIdx.x & 63;
+    const int4 q = ((const int4*)h)[63 - l];   // bins 252-4l .. 255-4l
+    const int c[4] = {q.w, q.z, q.y, q.x};     // descending bin order
+    const int s = c[0] + c[1] + c[2] + c[3];
+    const int incl = wave_incl_scan_i32(s);
+    int cum = incl - s;
+    if (cum < K && incl >= K) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (cum + c[j] >= K) {
+                sm.misc[4] = 255 - 4 * l - j;
+                sm.misc[5] = cum;
+                break;
+            }
+            cum += c[j];
+        }
+    }
+}
+
 // A chunk read again by the merger (its largest fourth value reaches the
 // bound kb): the whole chunk [ce0, ce1) in one round of loads (pass 1's
-// layout), every entry >= kb that is not a window id of the chunk (bitmap
+// layout), every entry whose key (lg) is >= kb and that is not a window id
+// of the chunk (bitmap
 // sm.big.wbits, chunk-relative) appended to sm.cand after the first base0
 // entries (one LDS atomic per wave on sm.ncand).
 template <typename T, bool FAST>
 __device__ __noinline__ void reread_chunk(const T* base, const uint32_t* mrow, int ce0, int ce1, uint32_t kb,
-                                          int base0, LeanSmem& sm) {
+                                          float temp, bool divide, int base0, LeanSmem& sm) {
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NVT = kEpt / VEC;
     const int t = threadIdx.x, lane = t & 63;
@@ -299,6 +329,10 @@ __device__ __noinline__ void reread_chunk(const T* base, const uint32_t* mrow, i
 #pragma unroll
             for (int e = 0; e < VEC; ++e) f[j * VEC + e] = Elt<T>::scalar(base + min(eb + e, ce1 - 1));
         }
+    }
+    if (divide) {
+#pragma unroll
+        for (int q = 0; q < kEpt; ++q) f[q] = f[q] / temp;
     }
     uint64_t take = 0;   // bit q: entry q of this thread
 #pragma unroll
@@ -504,6 +538,15 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     return;
 #endif
 
+    // ---- the ticket, now: its round trip overlaps the window count, the
+    //      penalised entries and the publish below, and the last of the row
+    //      merges.  A chunk with an earlier ticket may still be publishing
+    //      when the merger reads; the merger reads such words again.
+    uint32_t ticket = 0;
+    if (t == 0)
+        ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+
     // ---- the history window, counted now that the ids are surely in: each
     //      window id in this chunk is counted (16 bits per id) and the
     //      position that counted it first owns it.  Pass 1 saw window ids
@@ -536,6 +579,12 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         }
         lds_sync();
     }
+    TMS_TR(19);
+
+    // Published keys are of lg = value / temperature (the quotient the tail
+    // ranks by; for greedy rows and invalid temperatures the value itself).
+    const bool cdiv = !P.greedy && P.temperature != 1.0f && P.temperature > 0.0f && P.temperature <= FLT_MAX;
+    auto lgof = [&](float x) { return cdiv ? x / P.temperature : x; };
 
     // ---- penalised window entries, from their owners
     bool my_nf = !(t1 < __builtin_huge_valf());   // +inf or NaN among this thread's entries
@@ -550,7 +599,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                 g = apply_pen(g, cnt, pn);
                 my_nf |= !(g < __builtin_huge_valf()) && g != NEG_INF;   // NaN or +inf
                 const int k = atomicAdd(&sm.npen, 1);
-                if (k < kPendCap) sm.pend[k] = ckey(g, (uint32_t)id);
+                if (k < kPendCap) sm.pend[k] = ckey(lgof(g), (uint32_t)id);
             }
         }
         const int nlate = min(sm.nlate, kLate);
@@ -564,12 +613,13 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                 g = apply_pen(g, cnt, pn);
                 my_nf |= !(g < __builtin_huge_valf()) && g != NEG_INF;
                 const int q = atomicAdd(&sm.npen, 1);
-                if (q < kPendCap) sm.pend[q] = ckey(g, (uint32_t)id);
+                if (q < kPendCap) sm.pend[q] = ckey(lgof(g), (uint32_t)id);
             }
         }
     }
+    TMS_TR(20);
     // per wave: any non-finite entry, and the largest fourth value's key
-    const uint32_t t4k = okey(t4);
+    const uint32_t t4k = okey(lgof(t4));
     const bool wnf = __any(my_nf);
     const uint32_t wt4 = wave_max_u32_dpp(t4k);
     if (lane == 0) {
@@ -585,7 +635,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     const int npen = min(npen_all, kPendCap);
     const uint64_t hdr = lean_header(flags, npen, t4max);
 
-    // ---- publish (no store waits), then the ticket.  Thread t stores its
+    // ---- publish (no store waits).  Thread t stores its
     //      three keys, thread i % kBlock penalised entry i, thread 0 the
     //      header; the same lanes zero them if this workgroup merges (one
     //      lane stores each word, so its zero lands after it).
@@ -595,9 +645,9 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         return pn.on && ((sm.big.cnt[off >> 1] >> ((off & 1) * 16)) & 0xFFFFu) != 0;
     };
     // a window entry's key is 1: never 0 (data as flag), below every bound
-    const uint64_t k1 = windowed(id1) ? 1ull : ckey(t1, id1);
-    const uint64_t k2 = windowed(id2) ? 1ull : ckey(t2, id2);
-    const uint64_t k3 = windowed(id3) ? 1ull : ckey(t3, id3);
+    const uint64_t k1 = windowed(id1) ? 1ull : ckey(lgof(t1), id1);
+    const uint64_t k2 = windowed(id2) ? 1ull : ckey(lgof(t2), id2);
+    const uint64_t k3 = windowed(id3) ? 1ull : ckey(lgof(t3), id3);
     uint64_t* row_lists = a.tlists + (int64_t)row * S * kTopkListStride;
     uint64_t* my_list = row_lists + (int64_t)c * kTopkListStride;
     st_agent(&my_list[kWordKeys + t], k1);
@@ -606,8 +656,6 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     for (int i = t; i < npen; i += kBlock) st_agent(&my_list[kWordPend + i], sm.pend[i]);
     if (t == 0) {
         st_agent(&my_list[0], hdr);
-        const uint32_t ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u,
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         sm.misc[0] = ticket == (uint32_t)(S - 1) ? 1 : 0;
     }
     TMS_TR(4);
@@ -617,6 +665,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         return;
     }
     TMS_TR(5);
+    TMS_TV(21, __builtin_amdgcn_s_memtime());
 
     // ================= merge: the last workgroup of the row =================
     // Thread t reads the three keys of thread t of every other chunk and the
@@ -655,7 +704,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         kk[2 * cc] = ld_agent(key_at(cc, 0, t));
         kk[2 * cc + 1] = ld_agent(key_at(cc, 1, t));
     }
-    uint64_t h = ld_agent(hdr_at);
+    uint64_t h = ld_agent(hdr_at);   // this workgroup's own: from hdr below (another lane stored it)
     constexpr int kPendPer = MS * kPendRead / kBlock;
     uint64_t pw[kPendPer];
 #pragma unroll
@@ -675,6 +724,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     // A word still 0 is in flight: the thread reads all of its words again
     // (a non-zero word does not change until this workgroup zeroes it), a
     // bounded number of times; spins reaching kPollCap marks the row lost.
+    h = t == c ? hdr : h;
     int spins = 0;
     bool zero = h == 0;
 #pragma unroll
@@ -687,7 +737,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
             kk[2 * cc] = ld_agent(key_at(cc, 0, tid));
             kk[2 * cc + 1] = ld_agent(key_at(cc, 1, tid));
         }
-        h = ld_agent(&row_lists[(int64_t)min(tid, S - 1) * kTopkListStride]);
+        h = tid == c ? hdr : ld_agent(&row_lists[(int64_t)min(tid, S - 1) * kTopkListStride]);
         zero = h == 0;
 #pragma unroll
         for (int i = 0; i < 2 * MS; ++i) zero |= kk[i] == 0;
@@ -710,6 +760,8 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
 #pragma unroll
     for (int cc = 0; cc < MS; ++cc) gm = max(gm, cc < S ? (uint32_t)(kk[2 * cc] >> 32) : 0u);
     sm.gkey[t] = gm;
+    sm.hist[t] = 0;
+    sm.hist2[t] = 0;
     lds_sync();
     TMS_TR(6);
     // the penalised entries read with the keys; past kPendRead (rare) below
@@ -781,38 +833,25 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     bool late_done = false;   // third keys and penalised entries waited for
     if (status == TMS_ROW_OK) {
         // ---- the bound: the K-th largest of the 256 group maxima (K groups
-        //      hold an entry >= it, so it bounds the row's K-th value from
-        //      below), bit by bit on the sixteen high bits of the order keys.
-        const uint4 g4 = ((const uint4*)sm.gkey)[lane];
-        uint32_t pre = 0;
-        for (int bit = 31; bit >= 16; --bit) {
-            const uint32_t cand = pre | (1u << bit);
-            const uint64_t m0 = __builtin_amdgcn_uicmp(g4.x, cand, 35);   // unsigned >=
-            const uint64_t m1 = __builtin_amdgcn_uicmp(g4.y, cand, 35);
-            const uint64_t m2 = __builtin_amdgcn_uicmp(g4.z, cand, 35);
-            const uint64_t m3 = __builtin_amdgcn_uicmp(g4.w, cand, 35);
-            if (__popcll(m0) + __popcll(m1) + __popcll(m2) + __popcll(m3) >= K) pre = cand;
-        }
+        //      hold an entry >= it, so it bounds the row's K-th key from
+        //      below), on the sixteen high bits of the order keys: two
+        //      rounds of an 8-bit histogram in LDS, wave 0 picking the digit.
+        atomicAdd(&sm.hist[gm >> 24], 1);
+        lds_sync();
+        if (wv == 0) pick_digit(sm.hist, K, sm);
+        lds_sync();
+        const uint32_t d1 = (uint32_t)sm.misc[4];
+        const int above1 = sm.misc[5];
+        if ((gm >> 24) == d1) atomicAdd(&sm.hist2[(gm >> 16) & 0xFFu], 1);
+        lds_sync();
+        if (wv == 0) pick_digit(sm.hist2, K - above1, sm);
+        lds_sync();
+        const uint32_t pre = (d1 << 24) | ((uint32_t)sm.misc[4] << 16);
         TMS_TR(11);
         // Keys below okey(-FLT_MAX) decode to -inf or NaN: every finite entry.
         all_finite = pre < 0x00800000u;
-        float thr = all_finite ? -FLT_MAX : okey_inv(pre);
-        // Division can merge neighbouring values: lower the bound to the
-        // smallest float with the same quotient, so every entry tying the
-        // K-th quotient is a candidate.
-        bool radix = (fo & FLAG_OVERFLOW) != 0;
-        if (divide && !all_finite) {
-            const float qt = thr / temp;
-            int it = 0;
-            for (; it < 64; ++it) {
-                const float p = float_below(thr);
-                if (p / temp == qt) thr = p;
-                else break;
-            }
-            radix |= it == 64;
-            if (thr == -__builtin_huge_valf()) thr = -FLT_MAX;
-        }
-        const uint32_t kb = okey(thr);
+        const bool radix = (fo & FLAG_OVERFLOW) != 0;
+        const uint32_t kb = all_finite ? 0x00800000u : pre;
         settle_late();
         late_done = true;
         TMS_TR(9);
@@ -911,7 +950,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                     mark(ld_agent(&row_lists[(int64_t)cc * kTopkListStride + kWordPend + i]));
             }
             lds_sync();
-            reread_chunk<T, FAST>(base, mrow, ce0, min(ce0 + a.CE, V), kb, ngath, sm);
+            reread_chunk<T, FAST>(base, mrow, ce0, min(ce0 + a.CE, V), kb, temp, divide, ngath, sm);
         }
         lds_sync();
         TMS_TR(12);
@@ -946,15 +985,9 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
             }
         }
         if (status == TMS_ROW_OK) {
-            // Divide the candidates and form their keys, then rank them by
-            // counting; the row's sorted top min(n, K) lands in srt.
-            uint64_t* keys = sm.big.m.keys;
-            for (int i = t; i < n; i += kBlock) {
-                const uint64_t rw = sm.cand[i];
-                const float f = ckey_val(rw);
-                keys[i] = ckey(divide ? f / temp : f, ckey_id(rw));
-            }
-            rank_sort(keys, n, srt, K);
+            // Rank the candidates' keys by counting; the row's sorted top
+            // min(n, K) lands in srt.
+            rank_sort(sm.cand, n, srt, K);
             // With the bound at "every finite entry" the gather holds every
             // finite entry of the row.
             N = all_finite ? n : K;
@@ -1041,6 +1074,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     if (wv == 0) {
         tail_topk(a, row, P, srt, n, K, sm.big.m.pr, (double*)sm.cand, w0, w1);
         TMS_TR(8);
+        TMS_TV(22, __builtin_amdgcn_s_memtime());
     } else {
         zero_others(t - 64, kBlock - 64);
     }
