@@ -104,13 +104,14 @@ def cpu_baseline(w, cfg):
     }
 
 
-def traffic_from_profiles(cfg):
+def traffic_from_profiles(cfg, general=False):
+    """HBM bytes per launch measured with rocprofv3 (profiles/traffic.json), or None."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(p):
         return None
     try:
         d = json.load(open(p))
-        return d.get(f"cfg{cfg}")
+        return d.get(f"cfg{cfg}" + ("_general" if general else ""))
     except Exception:
         return None
 
@@ -262,7 +263,7 @@ def main():
             "peak": PEAK_HBM / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM, 4),
-            "traffic": traffic_from_profiles(args.config),
+            "traffic": traffic_from_profiles(args.config, args.general),
         },
         "cpu_baseline": cpu,
     }

@@ -131,8 +131,10 @@ typedef struct tms_sample_args {
                                  pr / z of the same entries */
     uint32_t row_kinds;       /* TMS_ROWS_ANY, or TMS_ROWS_TOPK: the caller promises
                                  every row is greedy or has 1 <= top_k <= 128, and
-                                 the library may take its top-k kernel (a row that
-                                 breaks the promise gets TMS_ROW_UNSUPPORTED) */
+                                 the library may take its top-k kernel (it does when
+                                 batch x chunks <= 1024 workgroups); under that
+                                 kernel a row that breaks the promise gets
+                                 TMS_ROW_UNSUPPORTED, never a wrong sample */
     uint32_t reserved;        /* must be 0 */
 } tms_sample_args;
 

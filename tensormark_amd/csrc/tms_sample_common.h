@@ -45,6 +45,7 @@ constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
 constexpr int kLeanMaxChunksHost = 16;     // chunks per row of the top-k kernel (vocab <= 262,144)
 constexpr int kTopkListStride = 1280;      // u64 per (row, chunk) list of the top-k kernel
+constexpr int kTopkMaxGrid = 1024;         // workgroups of a top-k launch (2 per CU resident)
 constexpr int kRankLists = 16;             // most chunk lists the sampled merge reads in one round
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
@@ -334,6 +335,30 @@ __device__ __forceinline__ void row_uniform(const KArgs& a, int row, const tms_r
         w1 = a.draws[2 * row + 1];
     } else {
         row_words(P.seed, P.offset, 0u, w0, w1);
+    }
+}
+
+// Workgroup b of a B x S grid -> (row, chunk).  Workgroups are handed to
+// the 8 XCDs round-robin by index, so rows are kept whole on one XCD: in the
+// first 8 * floor(B / 8) rows, row r's chunks are the workgroups with
+// b % 8 == r % 8, in order.  Each XCD then merges its own rows; with
+// consecutive workgroups of a row on different XCDs, an XCD that ran a
+// little behind held the last chunk, and so the merge, of nearly every row
+// and fell further behind (B = 1024, S = 16: 501 of 515 merges on one XCD,
+// 717 us against 290 us for the others).  The mapping is a bijection
+// whatever the placement is.
+__device__ __forceinline__ void wg_row_chunk(int S, int& row, int& c) {
+    const int b = (int)blockIdx.x;
+    const int B = (int)gridDim.x / S;
+    const int whole = (B >> 3) << 3;
+    if (b < whole * S) {
+        const int s = b >> 3;
+        row = (b & 7) + 8 * (s / S);
+        c = s - (s / S) * S;
+    } else {
+        const int r = b - whole * S;
+        row = whole + r / S;
+        c = r - (r / S) * S;
     }
 }
 

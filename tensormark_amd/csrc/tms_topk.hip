@@ -375,8 +375,8 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     const int t = threadIdx.x;
     const int lane = t & 63, wv = t >> 6;
     const int S = a.S;
-    const int row = blockIdx.x / S;
-    const int c = blockIdx.x - row * S;
+    int row, c;
+    wg_row_chunk(S, row, c);
     const int V = a.V;
     const int e0 = c * a.CE;   // a multiple of 32: the chunk starts on a mask word
     const int e1 = min(e0 + a.CE, V);
