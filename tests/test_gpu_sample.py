@@ -300,6 +300,20 @@ def test_decisions_on_exact_boundaries(sampler, orc):
         check(g, want, cap)
 
 
+@pytest.mark.parametrize("B,V", [(1, 128256), (7, 70000), (13, 128256), (37, 70000)])
+def test_batch_sizes_off_the_xcd_grouping(sampler, orc, B, V):
+    """Workgroups map to (row, chunk) so that rows of the first 8 * (B // 8)
+    stay whole on one XCD and the rest follow in order: batches that are not
+    a multiple of 8 mix both parts (S = 8 and 5 chunks here).  Half the rows
+    greedy, the rest top-k 40 with the history penalties and a mask."""
+    w = workloads.cfg2(B=B, V=V, seed=40 + B, with_mask=True)
+    p = w["params"].copy()
+    p["greedy"] = (np.arange(B) % 2).astype(np.int32)
+    want = orc.sample_batch(w["logits"], p, recent=w["recent"], mask=w["mask"], topk_cap=40)
+    g = run_gpu(sampler, w["logits"], p, recent=w["recent"], mask=w["mask"], topk_cap=40)
+    check(g, want, 40)
+
+
 def test_repeated_calls_reuse_workspace(sampler, orc):
     """Back-to-back launches on one context: the arrival counters reset."""
     w = workloads.cfg2(B=16, V=40000, seed=9)
