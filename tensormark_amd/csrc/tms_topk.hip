@@ -752,7 +752,8 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     };
     if (t < kLeanMaxChunks) sm.hdr[t] = t < S ? h : 1ull;   // 1: no flags, entries or fourth value
     if (t == 0) {
-        sm.misc[3] = 0;   // a word never arrived
+        sm.misc[3] = 0;   // a key or header word never arrived
+        sm.misc[7] = 0;   // a later word never arrived (misc[3] is read for the status)
         sm.ncand = 0;
     }
     // group maxima: the largest first key of thread t over the chunks
@@ -795,7 +796,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
             z = late_zero();
         }
         if (z) spins = kPollCap;
-        if (spins >= kPollCap) sm.misc[3] = 1;
+        if (spins >= kPollCap) sm.misc[7] = 1;
     };
     if (spins >= kPollCap) sm.misc[3] = 1;
     // the headers (1 past S): flags, largest fourth values, penalised
@@ -920,7 +921,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
                     append_cand(sm, i < npc && above(v), v, ngath);
                 }
             }
-            if (spins >= kPollCap) sm.misc[3] = 1;
+            if (spins >= kPollCap) sm.misc[7] = 1;
         }
         // ---- chunks read again (rare): the whole chunk in one round of
         //      loads (pass 1's layout), every entry >= the bound that is not
@@ -956,7 +957,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         TMS_TR(12);
         n = ngath + sm.ncand;
         TMS_TV(17, n + 1);
-        if (sm.misc[3]) {
+        if (sm.misc[7]) {
             status = TMS_ROW_INTERNAL;
         } else if (radix || n > kCand) {
             // Massive ties (or too many penalised entries for the lists): the
@@ -999,7 +1000,6 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     // chunks' headers, keys and penalised entries; this workgroup's own by
     // the lanes that stored them.  Waves 1-3 zero the other chunks' words
     // while wave 0 runs a sampled row's tail.
-    const bool lost = sm.misc[3] != 0;
     auto zero_own = [&]() {
         st_agent(&my_list[kWordKeys + t], (uint64_t)0);
         st_agent(&my_list[kWordKeys + kBlock + t], (uint64_t)0);
@@ -1020,6 +1020,7 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         if (!sm.misc[3]) settle_late();
         lds_sync();
     }
+    const bool lost = sm.misc[3] != 0 || sm.misc[7] != 0;   // uniform: written before a barrier
     if (!lost && pextra && status != TMS_ROW_OK) {
         // penalised words past the first read: read (once written) before
         // they are zeroed
