@@ -518,14 +518,18 @@ __device__ void tail_topk_exact(const KArgs& a, int row, const tms_row_params& P
     }
 }
 
-// Whether the left-to-right prefix sums of the entries decide "first index
-// k < m whose prefix is >= thr" the same way as the prefixes c (lane k in
-// c0, lane k - 64 in c1) computed by a tree.  For n <= 128 non-negative
-// terms over a total >= 1, the reference's sequential prefixes (and the
-// quotients they sum) and the tree's differ by at most (2n + 24) * 2^-53
-// relative, plus a few subnormal units; the margin below is more than twice
-// that.  Returns false when some prefix up to the decision lies within the
-// margin of thr (or thr is NaN): only the sequential sums decide it.
+// Whether the reference's left-to-right prefix sums of quotients pr_j / D
+// decide "first index k < m whose prefix is >= thr" the same way as the
+// prefixes c (lane k in c0, lane k - 64 in c1) computed here as (tree
+// prefix sum of pr) / D', D' the tree's value of the divisor.  For n <= 128
+// non-negative terms: the tree prefixes carry at most 7 roundings per term
+// (a 6-step DPP scan plus one addition), the division one, the reference's
+// quotients and sequential additions 2n + 1, and the two divisors differ by
+// at most (n + 7) * 2^-53 relative, so the two differ by at most
+// (3n + 16) * 2^-53 relative (400 * 2^-53 at n = 128), plus a few subnormal
+// units; the margin below is 576 * 2^-53.  Returns false when some prefix up
+// to the decision lies within the margin of thr (or thr is NaN): only the
+// sequential sums decide it.
 __device__ __forceinline__ bool decide_first_ge(double c0, double c1, double thr, int m, int& idx) {
     const int lane = threadIdx.x & 63;
     constexpr double kRel = (4.0 * 2 * 64 + 64.0) * 0x1p-53;
@@ -563,9 +567,9 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
     const double s0 = wave_incl_scan_f64(pr0);
     const double s1 = wave_incl_scan_f64(pr1) + readlane_f64(s0, 63);
     const double z = readlane_f64(s1, 63);
-    const double q0 = pr0 / z, q1 = pr1 / z;
-    const double c0 = wave_incl_scan_f64(q0);
-    const double c1 = wave_incl_scan_f64(q1) + readlane_f64(c0, 63);
+    // cum = prefix of q = pr / z: from the prefixes of pr (decide_first_ge
+    // bounds the difference from the reference's sums of quotients)
+    const double c0 = s0 / z, c1 = s1 / z;
     int fi;
     bool ok = decide_first_ge(c0, c1, (double)P.top_p, n, fi);
     int kp = fi < n ? fi + 1 : K;
@@ -582,11 +586,8 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
     if (ok && keep >= 2) {
         const int e = keep - 1;   // the sum runs over entries 0 .. keep - 1
         const double sum = e < 64 ? readlane_f64(s0, e) : readlane_f64(s1, e - 64);
-        const double p0 = lane < keep - 1 ? pr0 / sum : 0.0;
-        const double p1 = lane + 64 < keep - 1 ? pr1 / sum : 0.0;
-        const double d0 = wave_incl_scan_f64(p0);
-        const double d1 = wave_incl_scan_f64(p1) + readlane_f64(d0, 63);
-        ok = decide_first_ge(d0, d1, u, keep - 1, tokidx);
+        // cp = prefix of p = pr / sum, likewise from the prefixes of pr
+        ok = decide_first_ge(s0 / sum, s1 / sum, u, keep - 1, tokidx);
     }
     if (!ok) {
         TMS_TV(16, 1);
