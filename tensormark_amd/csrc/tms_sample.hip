@@ -863,7 +863,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
     for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
     lds_sync();
-    if (wv == 0) tail_topp(a, row, P, srt, n, K, pr, q);
+    if (wv == 0) tail_topp_fast(a, row, P, srt, n, K, pr, q);
 }
 
 }  // namespace tms

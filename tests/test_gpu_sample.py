@@ -131,12 +131,36 @@ def test_cfg2_full_size_vs_oracle(sampler, orc, with_mask):
     check(g, want, 40)
 
 
-def test_cfg3_full_size_fp16_vs_oracle(sampler, orc):
+@pytest.mark.parametrize("cap", [64, 0])
+def test_cfg3_full_size_fp16_vs_oracle(sampler, orc, cap):
+    """cap 64 returns per-entry probabilities (the sequential top-p tail);
+    cap 0 returns tokens and keep counts only (the prefix-sum top-p tail)."""
     w = workloads.cfg3()
     x32 = w["logits"].astype(np.float32)
-    want = orc.sample_batch(x32, w["params"], mask=w["mask"], topk_cap=64)
-    g = run_gpu(sampler, w["logits"], w["params"], mask=w["mask"], topk_cap=64, dtype="f16")
-    check(g, want, 64)
+    want = orc.sample_batch(x32, w["params"], mask=w["mask"], topk_cap=cap)
+    g = run_gpu(sampler, w["logits"], w["params"], mask=w["mask"], topk_cap=cap, dtype="f16")
+    check(g, want, cap)
+
+
+@pytest.mark.parametrize("n_allowed", [70, 700, 1000])
+def test_topp_rows_many_entries(sampler, orc, n_allowed):
+    """Top-p rows (top_k = 0) holding up to 1000 entries within 40 of the
+    maximum, spread over the row's chunks: lane blocks of up to 16 entries in the prefix-sum tail, with
+    top-p, min-p and temperature varied per row and no per-entry outputs."""
+    rng = np.random.default_rng(n_allowed)
+    B, V = 64, 60000   # 4 chunks: a chunk holds at most 512 candidates
+    x = rng.normal(0.0, 1.5, (B, V)).astype(np.float32)
+    bits = np.zeros((B, ((V + 31) // 32) * 32), bool)
+    for b in range(B):
+        bits[b, rng.choice(V, size=n_allowed, replace=False)] = True
+    mask = workloads.pack_bits(bits)
+    p = params_array(B, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(B) + 5)
+    p["top_p"] = rng.choice([0.3, 0.8, 0.95, 0.999, 1.0], size=B)
+    p["min_p"] = rng.choice([0.0, 0.0, 0.01, 0.2], size=B)
+    p["temperature"] = rng.choice([0.6, 1.0, 1.7], size=B)
+    want = orc.sample_batch(x, p, mask=mask)
+    g = run_gpu(sampler, x, p, mask=mask)
+    check(g, want)
 
 
 def test_cfg5_rows_bf16_vs_oracle(sampler, orc):
@@ -268,11 +292,13 @@ def test_edge_cases(sampler, orc, name, cap):
     check(g, want, cap)
 
 
-def test_decisions_on_exact_boundaries(sampler, orc):
+@pytest.mark.parametrize("top_k", [40, 0])
+def test_decisions_on_exact_boundaries(sampler, orc, top_k):
     """Equal logits over 4 or 8 allowed ids make every prefix sum exact, so
     the top-p cut can land exactly on top_p and the uniform exactly on a
-    partial sum: the tree-sum tail must defer those decisions to the
-    sequential sums and agree with the reference's lower_bound."""
+    partial sum: the tree-sum tails (top-k rows, and top_k = 0 rows through
+    the top-p tail) must defer those decisions to the sequential sums and
+    agree with the reference's lower_bound."""
     V = 1000
     u_words = {0.0: (0, 0), 0.25: (0, 0x40000000), 0.5: (0, 0x80000000),
                0.75: (0, 0xC0000000), 0.375: (0, 0x60000000),
@@ -286,7 +312,7 @@ def test_decisions_on_exact_boundaries(sampler, orc):
     x = np.full((B, V), 2.5, np.float32)
     bits = np.zeros((B, ((V + 31) // 32) * 32), bool)
     draws = np.zeros((B, 2), np.uint32)
-    p = params_array(B, temperature=1.0, top_k=40, top_p=0.9, seed=np.arange(B))
+    p = params_array(B, temperature=1.0, top_k=top_k, top_p=0.9, seed=np.arange(B))
     rng = np.random.default_rng(11)
     for b, (na, tp, u) in enumerate(rows):
         bits[b, rng.choice(V, size=na, replace=False)] = True
@@ -294,7 +320,10 @@ def test_decisions_on_exact_boundaries(sampler, orc):
         p["top_p"][b] = tp
         assert orc.canonical(int(draws[b, 0]), int(draws[b, 1])) == u
     mask = workloads.pack_bits(bits)
-    for cap in (0, 8):
+    # A top_k = 0 row's id list holds its entries within 40 of the maximum
+    # and pads with -1 (include/tmsample_hip.h); with 4 or 8 held entries an
+    # 8-slot list would reach the padding, so those rows run without one.
+    for cap in ((0, 8) if top_k else (0,)):
         want = orc.sample_batch(x, p, mask=mask, draws=draws, topk_cap=cap)
         g = run_gpu(sampler, x, p, mask=mask, draws=draws, topk_cap=cap)
         check(g, want, cap)
