@@ -57,6 +57,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     const int e0 = c * a.CE;
     const int e1 = min(e0 + a.CE, V);
     const int nvec = (e1 - e0 + VEC - 1) / VEC;
+    TMS_TR(0);
 
     // ---- history ids first (the row's first 4 * kBlock; positions are
     //      checked against the window once the parameters are in), then the
@@ -183,6 +184,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     }
 
     __builtin_amdgcn_sched_barrier(0);
+    TMS_TR(3);
     // ---- row parameters and history window (the parameters' load was issued
     //      before pass 1 and is first waited for here).
     const bool greedy = P.greedy != 0;
@@ -268,6 +270,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
 #pragma unroll
     for (int i = 0; i < kWin; ++i) tmax = fmaxf(tmax, xo[i]);
 
+    TMS_TR(13);
     // ---- selection: the chunk's candidates, sorted, into sm.cand[0..nout).
     int flags = 0;
     int nout = 0;
@@ -499,6 +502,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         }
     }
 
+    TMS_TR(4);
     // ---- publish, then take a ticket: the row's last workgroup to publish
     //      merges, and every other list is complete by then.
     // Header and entries are stored together and complete before the
@@ -543,6 +547,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     }
     lds_sync();
     if (!sm.misc[0]) return;
+    TMS_TR(5);
 
     // ================= merge: the last workgroup of the row =================
     // Top-k rows took each list's header and first r entries (r = K where
@@ -659,6 +664,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         }
     }
     lds_sync();
+    TMS_TR(6);
     const int N = sm.misc[5];
     const int fo = sm.misc[4];
     int status = TMS_ROW_OK;
@@ -795,8 +801,10 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     // Every word the other chunks wrote this call (headers, entries) goes
     // back to zero for the next call; on a top-k row's success path waves
     // 1-3 do it while wave 0 runs the tail.
+    TMS_TR(9);
     const bool defer_zero = status == TMS_ROW_OK && mode == MODE_TOPK && !sm.misc[3];
     if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
+    TMS_TR(10);
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
         return;
@@ -832,6 +840,7 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
         lds_sync();
         n = K;
     }
+    TMS_TR(7);
     const float mx = ckey_val(srt[0]);
     if (mx == __builtin_huge_valf()) {
         if (defer_zero) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
@@ -863,7 +872,10 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
     for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
     lds_sync();
-    if (wv == 0) tail_topp_fast(a, row, P, srt, n, K, pr, q);
+    if (wv == 0) {
+        tail_topp_fast(a, row, P, srt, n, K, pr, q);
+        TMS_TR(8);
+    }
 }
 
 }  // namespace tms
