@@ -492,10 +492,35 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     //      t1.
     float t1 = NEG_INF, t2 = NEG_INF, t3 = NEG_INF, t4 = NEG_INF;
     int i1 = 0, i2 = 0, i3 = 0;
+    // The window's first kWin * kBlock positions are counted while the
+    // stream lands (after slot 1: the ids were loaded first), each count's
+    // old value kept for after pass 1 (the barrier that follows pass 1 makes
+    // every count final before it is read).
+    bool win_in[kWin];
+    uint32_t win_old[kWin];
+#pragma unroll
+    for (int i = 0; i < kWin; ++i) {
+        win_in[i] = false;
+        win_old[i] = 1u;
+    }
 #pragma unroll
     for (int j = 0; j < NVT; ++j) {
         if constexpr (FAST) {
             if (j + kLook < NVT) issue(j + kLook);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (j == 1 && pn.on) {
+#pragma unroll
+            for (int i = 0; i < kWin; ++i) {
+                const int p = t + i * kBlock;
+                const int id = (p < from || p >= nrec) ? -1 : wid[i];
+                win_in[i] = id >= e0 && id < e1;
+                if (win_in[i]) {
+                    const int off = id - e0;
+                    const uint32_t sh = (off & 1) * 16;
+                    win_old[i] = (atomicAdd(&sm.big.cnt[off >> 1], 1u << sh) >> sh) & 0xFFFFu;
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
         const int v = t + j * kBlock;
@@ -547,32 +572,28 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
         ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
 
-    // ---- the history window, counted now that the ids are surely in: each
-    //      window id in this chunk is counted (16 bits per id) and the
-    //      position that counted it first owns it.  Pass 1 saw window ids
-    //      with their raw logits; a thread leaves them out of what it
-    //      publishes (every entry it does not publish stays <= its fourth
-    //      value, so the bound test is unchanged).
+    // ---- the history window: each window id in this chunk is counted (16
+    //      bits per id) and the position that counted it first owns it (the
+    //      first kWin * kBlock positions were counted during pass 1).  Pass
+    //      1 saw window ids with their raw logits; a thread leaves them out
+    //      of what it publishes (every entry it does not publish stays <= its
+    //      fourth value, so the bound test is unchanged).
     bool first[kWin];
 #pragma unroll
-    for (int i = 0; i < kWin; ++i) first[i] = false;
+    for (int i = 0; i < kWin; ++i) first[i] = win_in[i] && win_old[i] == 0u;
     if (pn.on) {
-        for (int p0 = 0; p0 < nrec; p0 += kWin * kBlock) {
+        for (int p0 = kWin * kBlock; p0 < nrec; p0 += kWin * kBlock) {   // long windows
 #pragma unroll
             for (int i = 0; i < kWin; ++i) {
                 const int p = p0 + t + i * kBlock;
-                const int id = (p < from || p >= nrec) ? -1 : (p0 == 0 ? wid[i] : hist[p]);
+                const int id = (p < from || p >= nrec) ? -1 : hist[p];
                 if (id >= e0 && id < e1) {
                     const int off = id - e0;
                     const uint32_t sh = (off & 1) * 16;
                     const uint32_t old = atomicAdd(&sm.big.cnt[off >> 1], 1u << sh);
-                    if (((old >> sh) & 0xFFFFu) == 0) {
-                        if (p0 == 0) {
-                            first[i] = true;
-                        } else {
-                            const int k = atomicAdd(&sm.nlate, 1);   // long windows: loaded late
-                            if (k < kLate) sm.late[k] = id;
-                        }
+                    if (((old >> sh) & 0xFFFFu) == 0) {   // its logit is loaded late
+                        const int k = atomicAdd(&sm.nlate, 1);
+                        if (k < kLate) sm.late[k] = id;
                     }
                 }
             }
