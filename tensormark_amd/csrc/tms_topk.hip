@@ -496,6 +496,12 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     // stream lands (after slot 1: the ids were loaded first), each count's
     // old value kept for after pass 1 (the barrier that follows pass 1 makes
     // every count final before it is read).
+    // The ticket is taken with the last kLook slots of the stream still to
+    // come: its round trip overlaps them, the window and the publish, and
+    // the last of the row to get there merges.  A chunk with an earlier
+    // ticket may still be publishing when the merger reads; the merger reads
+    // such words again.
+    uint32_t ticket = 0;
     bool win_in[kWin];
     uint32_t win_old[kWin];
 #pragma unroll
@@ -509,6 +515,9 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
             if (j + kLook < NVT) issue(j + kLook);
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (j == NVT - kLook && t == 0)
+            ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
         if (j == 1 && pn.on) {
 #pragma unroll
             for (int i = 0; i < kWin; ++i) {
@@ -563,14 +572,6 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     return;
 #endif
 
-    // ---- the ticket, now: its round trip overlaps the window count, the
-    //      penalised entries and the publish below, and the last of the row
-    //      merges.  A chunk with an earlier ticket may still be publishing
-    //      when the merger reads; the merger reads such words again.
-    uint32_t ticket = 0;
-    if (t == 0)
-        ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
 
     // ---- the history window: each window id in this chunk is counted (16
     //      bits per id) and the position that counted it first owns it (the
