@@ -43,7 +43,7 @@
 namespace tms {
 
 template <typename T, bool FAST>
-__global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
+__global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NVT = kEpt / VEC;
     __shared__ Smem sm;
@@ -275,17 +275,18 @@ __global__ __launch_bounds__(kBlock) void sample_kernel(KArgs a) {
     int flags = 0;
     int nout = 0;
     if (mode == MODE_GREEDY) {
-        uint64_t gb = 0;
+        // The thread's best stream entry: its largest value and, among the
+        // entries equal to it (equal values share a key, -0 and +0 too), the
+        // first position, whose id is the lowest (ids grow with j, then e).
+        float smax = vmax[0];
 #pragma unroll
-        for (int j = 0; j < NVT; ++j) {
+        for (int j = 1; j < NVT; ++j) smax = fmaxf(smax, vmax[j]);
+        int q = 0;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                const float f = x[j * VEC + e];
-                const uint64_t k =
-                    f != NEG_INF ? ckey(f, (uint32_t)(e0 + (t + j * kBlock) * VEC + e)) : 0ull;
-                gb = k > gb ? k : gb;
-            }
-        }
+        for (int i = kEpt - 1; i >= 0; --i) q = x[i] == smax ? i : q;
+        uint64_t gb = smax != NEG_INF
+                          ? ckey(smax, (uint32_t)(e0 + (t + (q / VEC) * kBlock) * VEC + q % VEC))
+                          : 0ull;
 #pragma unroll
         for (int i = 0; i < kWin; ++i) {
             const uint64_t k = xo[i] != NEG_INF ? ckey(xo[i], io[i]) : 0ull;
