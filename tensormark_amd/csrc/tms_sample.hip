@@ -176,10 +176,12 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             uint32_t bits = (__float_as_uint(f[e]) & sel) | (0xFF800000u & ~sel);
             if constexpr (!FAST) bits = (eb + e < e1) ? bits : 0xFF800000u;
             const float g = __uint_as_float(bits);
-            nonfinite |= __builtin_amdgcn_class(g, 0x203);   // NaN or +inf
-            vm = fmaxf(vm, g);
+            // IEEE maximum (v_maximum3_f32) keeps a NaN, so one class test
+            // of the slot maximum finds any NaN or +inf of the slot.
+            vm = __builtin_elementwise_maximum(vm, g);
             x[j * VEC + e] = g;
         }
+        nonfinite |= __builtin_amdgcn_class(vm, 0x203);   // NaN or +inf
         vmax[j] = vm;
     }
 
