@@ -375,22 +375,68 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             constexpr int kSeg = kCand / kWaves;
             uint64_t* seg = sm.cand + wv * kSeg;
             int wcnt = 0;
+            // Stage 1: each slot whose maximum reaches thr is copied whole
+            // (VEC values, then its slot index) into the wave's staging area
+            // in sm.big (the window counts are dead now): one ballot per slot.
+            // Stage 2: the wave compacts the staged values 64 at a time.  A
+            // wave with more than kStage such slots compacts entry by entry.
+            constexpr int kStageWords = (int)(sizeof(sm.big) / 4) / kWaves;
+            constexpr int kStage = kStageWords / (VEC + 1);
+            float* stv = (float*)sm.big.cnt + wv * kStageWords;
+            int* sts = (int*)(stv + kStage * VEC);
+            int ns = 0;
 #pragma unroll
             for (int j = 0; j < NVT; ++j) {
-                if (__any(vmax[j] >= thr)) {
+                const bool sj = vmax[j] >= thr;
+                const uint64_t m = __ballot(sj);
+                if (m) {
+                    const int pos = ns + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                    if (sj && pos < kStage) {
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) {
-                        const float f = x[j * VEC + e];
-                        const bool p = f >= thr;
-                        const uint64_t m = __ballot(p);
-                        if (m) {
-                            const int pos = wcnt + __builtin_amdgcn_mbcnt_hi(
-                                                       (uint32_t)(m >> 32),
-                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-                            if (p && pos < kSeg)
-                                seg[pos] = ((uint64_t)__float_as_uint(f) << 32) |
-                                           (uint32_t)(e0 + (t + j * kBlock) * VEC + e);
-                            wcnt += __popcll(m);
+                        for (int e = 0; e < VEC; e += 4)
+                            *(float4*)(stv + pos * VEC + e) =
+                                make_float4(x[j * VEC + e], x[j * VEC + e + 1], x[j * VEC + e + 2], x[j * VEC + e + 3]);
+                        sts[pos] = t + j * kBlock;
+                    }
+                    ns += __popcll(m);
+                }
+            }
+            if (ns <= kStage) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int total = ns * VEC;
+                for (int b = 0; b < total; b += 64) {
+                    const int i = b + lane;
+                    const int ic = min(i, total - 1);
+                    const float f = i < total ? stv[ic] : NEG_INF;
+                    const uint32_t id = (uint32_t)(e0 + sts[ic / VEC] * VEC + ic % VEC);
+                    const bool p = f >= thr;
+                    const uint64_t m = __ballot(p);
+                    const int pos = wcnt + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                    if (p && pos < kSeg) seg[pos] = ((uint64_t)__float_as_uint(f) << 32) | id;
+                    wcnt += __popcll(m);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < NVT; ++j) {
+                    if (__any(vmax[j] >= thr)) {
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) {
+                            const float f = x[j * VEC + e];
+                            const bool p = f >= thr;
+                            const uint64_t m = __ballot(p);
+                            if (m) {
+                                const int pos = wcnt + __builtin_amdgcn_mbcnt_hi(
+                                                           (uint32_t)(m >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                                if (p && pos < kSeg)
+                                    seg[pos] = ((uint64_t)__float_as_uint(f) << 32) |
+                                               (uint32_t)(e0 + (t + j * kBlock) * VEC + e);
+                                wcnt += __popcll(m);
+                            }
                         }
                     }
                 }
