@@ -982,7 +982,9 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_ss = off_sp + nb * tms::kSpecParts * 2 * sizeof(uint64_t);
     const size_t off_tl = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
     const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kLeanMaxChunksHost);
-    ctx->bytes = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
+    const size_t off_zp = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
+    ctx->spec_chunks = (max_vocab + 4095) / 4096;
+    ctx->bytes = off_zp + nb * (2 * tms::kSpecMaxK + 1) * (size_t)ctx->spec_chunks * 2 * sizeof(uint64_t);
     int rc = TMS_OK;
     if (hipMalloc(&ctx->ws, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipMemset(ctx->ws, 0, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;   // lists start zeroed
@@ -1002,6 +1004,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->spec_parts = (uint64_t*)(p + off_sp);
     ctx->spec_stats = (tms_spec_stat*)(p + off_ss);
     ctx->tlists = (uint64_t*)(p + off_tl);
+    ctx->spec_zparts = (uint64_t*)(p + off_zp);
     (void)hipSetDevice(prev);
     *out = ctx;
     return TMS_OK;

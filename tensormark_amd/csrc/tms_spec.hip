@@ -37,6 +37,15 @@ __constant__ double kSpecExpTab[64] = {TMS_EXP2_64THS};
 constexpr uint64_t kPartReady = 1ull << 63;   // published partial sum is complete
 constexpr int kPartPoll = 1 << 20;            // bound on the finisher's wait per part
 
+constexpr int kSpecChunk = 4096;   // ids per chunk of the chunked statistics
+
+// One chunk's statistics: max of v / T, NaN/+inf flag, share of Z.
+struct SpecPart {
+    float m;
+    int nf;
+    int64_t z;
+};
+
 struct SArgs {
     const void* target;
     const void* draft;
@@ -52,6 +61,8 @@ struct SArgs {
     tms_spec_stat* stats;
     uint64_t* parts;
     uint32_t* tickets;
+    SpecPart* zparts;   // [B * (2k + 1)][C] chunk statistics
+    int C;              // chunks per row of the chunked statistics (0: spec_stats_kernel)
 };
 
 __device__ __forceinline__ void load_exp_table(double* tab) {
@@ -200,6 +211,129 @@ __global__ __launch_bounds__(kBlock) void spec_stats_kernel(SArgs a) {
     }
 }
 
+// Chunked statistics (16-byte aligned rows): the vocabulary in chunks of
+// kSpecChunk ids, one workgroup per (row, chunk), in two launches.  Whole
+// rows as work units left a CU in 8 with a third row while the rest idled
+// (544 rows of exp64 work on 256 CUs).
+//   spec_chunk_max_kernel: the chunk's max of v / T and NaN/+inf flag.
+//   spec_chunk_z_kernel:   the row's max and status from its chunks' parts,
+//                          then the chunk's share of Z (exact int64); chunk 0
+//                          writes the row's m and status, the chunk holding
+//                          the draft token its weight ex.
+// The resolve kernel sums a row's Z shares (exact in any order).  m, status,
+// Z and ex equal those of spec_stats_kernel.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void spec_chunk_max_kernel(SArgs a) {
+    constexpr int VEC = Elt<T>::kVec;
+    constexpr int NS = kSpecChunk / VEC / kBlock;   // vectors per thread
+    __shared__ float shf[kWaves];
+    __shared__ int shi[kWaves];
+    const int t = threadIdx.x;
+    const int g = blockIdx.x / a.C, c = blockIdx.x - g * a.C;
+    const int R = 2 * a.k + 1;
+    const int b = g / R, i = g - b * R;
+    const T* row = spec_row<T>(a, b, i);
+    const float temp = a.params[b].temperature;
+    const int nv = a.V / VEC;
+    const int v0 = c * (kSpecChunk / VEC);
+    uint4 q[NS];
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) q[sl] = *(const uint4*)(row + (int64_t)min(v0 + t + sl * kBlock, nv - 1) * VEC);
+    float mx = -__builtin_huge_valf();
+    int nf = 0;
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) {
+        const bool in = v0 + t + sl * kBlock < nv;
+        float x[VEC];
+        Elt<T>::widen(q[sl], x);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            nf |= in ? __builtin_amdgcn_class(x[e], 0x203) : 0;   // NaN or +inf
+            mx = in ? fmaxf(mx, x[e] / temp) : mx;
+        }
+    }
+    mx = block_max_f32(mx, shf);
+    nf = block_or(nf, shi);
+    if (t == 0) {
+        SpecPart pt;
+        pt.m = mx;
+        pt.nf = nf;
+        pt.z = 0;
+        a.zparts[(int64_t)g * a.C + c] = pt;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void spec_chunk_z_kernel(SArgs a) {
+    constexpr int VEC = Elt<T>::kVec;
+    constexpr int NS = kSpecChunk / VEC / kBlock;
+    __shared__ double tab[64];
+    __shared__ int64_t shl[kWaves];
+    load_exp_table(tab);
+    const int t = threadIdx.x;
+    const int g = blockIdx.x / a.C, c = blockIdx.x - g * a.C;
+    const int R = 2 * a.k + 1;
+    const int b = g / R, i = g - b * R;
+    const T* row = spec_row<T>(a, b, i);
+    const float temp = a.params[b].temperature;
+    const int nv = a.V / VEC;
+    const int v0 = c * (kSpecChunk / VEC);
+    uint4 q[NS];
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) q[sl] = *(const uint4*)(row + (int64_t)min(v0 + t + sl * kBlock, nv - 1) * VEC);
+    // The row's max and flag from its chunks (every thread reads them all).
+    const SpecPart* parts = a.zparts + (int64_t)g * a.C;
+    float mx = -__builtin_huge_valf();
+    int nf = 0;
+    for (int u = 0; u < a.C; ++u) {
+        mx = fmaxf(mx, parts[u].m);
+        nf |= parts[u].nf;
+    }
+    int st = TMS_ROW_OK;
+    if (nf) st = TMS_ROW_NONFINITE;
+    else if (mx == -__builtin_huge_valf()) st = TMS_ROW_ALL_MASKED;
+    else if (mx == __builtin_huge_valf()) st = TMS_ROW_NONFINITE;
+    const double md = (double)mx;
+    int64_t z = 0;
+    if (st == TMS_ROW_OK) {
+#pragma unroll
+        for (int sl = 0; sl < NS; ++sl) {
+            float x[VEC];
+            Elt<T>::widen(q[sl], x);
+            if (v0 + t + sl * kBlock < nv) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) z += weight(x[e], temp, md, tab);
+            }
+        }
+        z = block_sum_i64(z, shl);
+    } else {
+        __syncthreads();   // the table's LDS writes, as block_sum_i64 orders them
+    }
+    if (t == 0) {
+        a.zparts[(int64_t)g * a.C + c].z = z;
+        const int di = i < a.k ? i : (i > a.k ? i - a.k - 1 : -1);
+        const int x = di >= 0 ? a.tokens[(int64_t)b * a.k + di] : -1;
+        const bool xin = x >= 0 && x < a.V;
+        if (c == 0) {
+            a.stats[g].m = mx;
+            a.stats[g].status = st;
+            a.stats[g].Z = 0;
+            a.stats[g].pad = 0;
+        }
+        if (c == (xin ? x / kSpecChunk : 0))
+            a.stats[g].ex = (st == TMS_ROW_OK && xin) ? weight(Elt<T>::scalar(row + x), temp, md, tab) : 0;
+    }
+}
+
+// A row's statistics as the resolve kernel uses them: with chunked
+// statistics, Z is the sum of the chunks' shares, gathered into zrow (LDS)
+// at the start of the resolve kernel.
+__device__ __forceinline__ tms_spec_stat get_stat(const SArgs& a, int g, int g0, const int64_t* zrow) {
+    tms_spec_stat s = a.stats[g];
+    if (a.C > 0) s.Z = zrow[g - g0];
+    return s;
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     __shared__ double tab[64];
@@ -212,6 +346,17 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     const int b = blockIdx.x / a.P, p = blockIdx.x - b * a.P;
     const tms_row_params P = a.params[b];
     const tms_spec_stat* st = a.stats + (int64_t)b * (2 * a.k + 1);
+    const int g0 = b * (2 * a.k + 1);
+    __shared__ int64_t zrow[2 * kSpecMaxK + 1];
+    if (a.C > 0) {
+        // The sequence's Z shares, one load per thread, summed in LDS.
+        const int R = 2 * a.k + 1;
+        if (t < R) zrow[t] = 0;
+        __syncthreads();
+        for (int idx = t; idx < R * a.C; idx += kBlock)
+            atomicAdd((unsigned long long*)&zrow[idx / a.C], (unsigned long long)a.zparts[(int64_t)g0 * a.C + idx].z);
+        __syncthreads();
+    }
     const uint32_t* dw = a.draws ? a.draws + (int64_t)b * (a.k + 1) * 2 : nullptr;
 
     // ---- the accept tests, evaluated identically by every workgroup.
@@ -221,7 +366,7 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     } else {
         acc = a.k;
         for (int i = 0; i < a.k; ++i) {
-            const tms_spec_stat ts = st[i], ds = st[a.k + 1 + i];
+            const tms_spec_stat ts = get_stat(a, g0 + i, g0, zrow), ds = get_stat(a, g0 + a.k + 1 + i, g0, zrow);
             if (ts.status) { status = ts.status; break; }
             if (ds.status) { status = ds.status; break; }
             const int x = a.tokens[(int64_t)b * a.k + i];
@@ -252,8 +397,8 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     const int ti = rej < 0 ? a.k : rej;
     const T* rt = spec_row<T>(a, b, ti);
     const T* rd = spec_row<T>(a, b, rej < 0 ? ti : a.k + 1 + rej);
-    const tms_spec_stat ts = st[ti];
-    const tms_spec_stat ds = rej < 0 ? ts : st[a.k + 1 + rej];
+    const tms_spec_stat ts = get_stat(a, g0 + ti, g0, zrow);
+    const tms_spec_stat ds = rej < 0 ? ts : get_stat(a, g0 + a.k + 1 + rej, g0, zrow);
     const float temp = P.temperature;
     const double mt = (double)ts.m, md = (double)ds.m;
     __syncthreads();   // exp table in LDS
@@ -404,12 +549,23 @@ extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStre
     s.stats = ctx->spec_stats;
     s.parts = ctx->spec_parts;
     s.tickets = ctx->spec_tickets;
+    s.zparts = (tms::SpecPart*)ctx->spec_zparts;
+    s.C = s.fast ? (a->vocab + tms::kSpecChunk - 1) / tms::kSpecChunk : 0;
+    static_assert(sizeof(tms::SpecPart) == 2 * sizeof(uint64_t), "chunk statistics layout");
     const dim3 block(tms::kBlock);
     const dim3 g1((unsigned)(a->batch * (2 * a->k + 1))), g2((unsigned)(a->batch * s.P));
-#define TMS_SPEC_LAUNCH(T)                                                              \
-    do {                                                                                \
-        hipLaunchKernelGGL(tms::spec_stats_kernel<T>, g1, block, 0, stream, s);        \
-        hipLaunchKernelGGL(tms::spec_resolve_kernel<T>, g2, block, 0, stream, s);      \
+    // 16-byte aligned rows take the chunked statistics; others the per-row
+    // kernel.
+    const dim3 gc((unsigned)(a->batch * (2 * a->k + 1) * (s.C > 0 ? s.C : 1)));
+#define TMS_SPEC_LAUNCH(T)                                                                 \
+    do {                                                                                   \
+        if (s.C > 0) {                                                                     \
+            hipLaunchKernelGGL(tms::spec_chunk_max_kernel<T>, gc, block, 0, stream, s);    \
+            hipLaunchKernelGGL(tms::spec_chunk_z_kernel<T>, gc, block, 0, stream, s);      \
+        } else {                                                                           \
+            hipLaunchKernelGGL(tms::spec_stats_kernel<T>, g1, block, 0, stream, s);        \
+        }                                                                                  \
+        hipLaunchKernelGGL(tms::spec_resolve_kernel<T>, g2, block, 0, stream, s);         \
     } while (0)
     switch (a->dtype) {
         case TMS_DTYPE_F32: TMS_SPEC_LAUNCH(float); break;
