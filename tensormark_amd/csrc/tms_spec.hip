@@ -325,15 +325,6 @@ __global__ __launch_bounds__(kBlock) void spec_chunk_z_kernel(SArgs a) {
     }
 }
 
-// A row's statistics as the resolve kernel uses them: with chunked
-// statistics, Z is the sum of the chunks' shares, gathered into zrow (LDS)
-// at the start of the resolve kernel.
-__device__ __forceinline__ tms_spec_stat get_stat(const SArgs& a, int g, int g0, const int64_t* zrow) {
-    tms_spec_stat s = a.stats[g];
-    if (a.C > 0) s.Z = zrow[g - g0];
-    return s;
-}
-
 template <typename T>
 __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     __shared__ double tab[64];
@@ -345,19 +336,38 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     const int t = threadIdx.x;
     const int b = blockIdx.x / a.P, p = blockIdx.x - b * a.P;
     const tms_row_params P = a.params[b];
-    const tms_spec_stat* st = a.stats + (int64_t)b * (2 * a.k + 1);
     const int g0 = b * (2 * a.k + 1);
-    __shared__ int64_t zrow[2 * kSpecMaxK + 1];
-    if (a.C > 0) {
-        // The sequence's Z shares, one load per thread, summed in LDS.
-        const int R = 2 * a.k + 1;
-        if (t < R) zrow[t] = 0;
-        __syncthreads();
-        for (int idx = t; idx < R * a.C; idx += kBlock)
-            atomicAdd((unsigned long long*)&zrow[idx / a.C], (unsigned long long)a.zparts[(int64_t)g0 * a.C + idx].z);
-        __syncthreads();
-    }
     const uint32_t* dw = a.draws ? a.draws + (int64_t)b * (a.k + 1) * 2 : nullptr;
+    // The sequence's statistics, draft tokens and accept uniforms, staged in
+    // LDS with one load (or Philox draw) per thread, so the sequential accept
+    // loop below waits on no memory.  With chunked statistics Z is the sum
+    // of the chunks' shares, gathered the same way.
+    __shared__ tms_spec_stat srow[2 * kSpecMaxK + 1];
+    __shared__ int64_t zrow[2 * kSpecMaxK + 1];
+    __shared__ int stok[kSpecMaxK];
+    __shared__ double su[kSpecMaxK];
+    {
+        const int R = 2 * a.k + 1;
+        if (t < R) {
+            srow[t] = a.stats[g0 + t];
+            zrow[t] = 0;
+        }
+        if (t < a.k) {
+            stok[t] = a.tokens[(int64_t)b * a.k + t];
+            uint32_t w0, w1;
+            if (dw) { w0 = dw[2 * t]; w1 = dw[2 * t + 1]; }
+            else row_words(P.seed, P.offset, (uint32_t)t, w0, w1);
+            su[t] = canonical(w0, w1);
+        }
+        __syncthreads();
+        if (a.C > 0) {
+            for (int idx = t; idx < R * a.C; idx += kBlock)
+                atomicAdd((unsigned long long*)&zrow[idx / a.C], (unsigned long long)a.zparts[(int64_t)g0 * a.C + idx].z);
+            __syncthreads();
+            if (t < R) srow[t].Z = zrow[t];
+            __syncthreads();
+        }
+    }
 
     // ---- the accept tests, evaluated identically by every workgroup.
     int status = TMS_ROW_OK, acc = 0, rej = -1;   // rej < 0: all accepted, bonus draw
@@ -366,23 +376,20 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     } else {
         acc = a.k;
         for (int i = 0; i < a.k; ++i) {
-            const tms_spec_stat ts = get_stat(a, g0 + i, g0, zrow), ds = get_stat(a, g0 + a.k + 1 + i, g0, zrow);
+            const tms_spec_stat ts = srow[i], ds = srow[a.k + 1 + i];
             if (ts.status) { status = ts.status; break; }
             if (ds.status) { status = ds.status; break; }
-            const int x = a.tokens[(int64_t)b * a.k + i];
+            const int x = stok[i];
             if (x < 0 || x >= a.V) { status = TMS_ROW_BAD_PARAMS; break; }
             double r;
             if (ds.ex == 0) r = ts.ex > 0 ? 1.0 : 0.0;
             else r = ((double)ts.ex * (double)ds.Z) / ((double)ds.ex * (double)ts.Z);
-            uint32_t w0, w1;
-            if (dw) { w0 = dw[2 * i]; w1 = dw[2 * i + 1]; }
-            else row_words(P.seed, P.offset, (uint32_t)i, w0, w1);
-            if (canonical(w0, w1) < r) continue;
+            if (su[i] < r) continue;
             acc = i;
             rej = i;
             break;
         }
-        if (status == TMS_ROW_OK && rej < 0 && st[a.k].status) status = st[a.k].status;
+        if (status == TMS_ROW_OK && rej < 0 && srow[a.k].status) status = srow[a.k].status;
     }
     if (status != TMS_ROW_OK) {
         if (p == 0 && t == 0) {
@@ -397,8 +404,8 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     const int ti = rej < 0 ? a.k : rej;
     const T* rt = spec_row<T>(a, b, ti);
     const T* rd = spec_row<T>(a, b, rej < 0 ? ti : a.k + 1 + rej);
-    const tms_spec_stat ts = get_stat(a, g0 + ti, g0, zrow);
-    const tms_spec_stat ds = rej < 0 ? ts : get_stat(a, g0 + a.k + 1 + rej, g0, zrow);
+    const tms_spec_stat ts = srow[ti];
+    const tms_spec_stat ds = rej < 0 ? ts : srow[a.k + 1 + rej];
     const float temp = P.temperature;
     const double mt = (double)ts.m, md = (double)ds.m;
     __syncthreads();   // exp table in LDS
