@@ -131,8 +131,13 @@ __device__ __forceinline__ double exp64(double x, const double* tab) {
     return y * __longlong_as_double((long long)(m + 1023) << 52);
 }
 
+// y in [0, 1] (a probability): floor(y * 2^44 + 0.5) is a whole number
+// below 2^52, so adding 2^52 holds it exactly in the mantissa, and the
+// difference of the bit patterns is that integer (two operations, where a
+// general double -> int64 conversion takes several).
 __device__ __forceinline__ int64_t q44(double y) {
-    return (int64_t)floor(y * 17592186044416.0 + 0.5);
+    const double f = floor(y * 17592186044416.0 + 0.5);
+    return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
 // ------------------------------------------------------------ reductions
