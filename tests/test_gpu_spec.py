@@ -76,8 +76,11 @@ def test_spec_cfg4_full_size(orc, sampler):
 
 def test_spec_caller_draws_and_dtypes(orc, sampler):
     rng = np.random.default_rng(41)
+    # 16-byte aligned rows (V a multiple of 4 for f32, 8 for f16/bf16) take the
+    # chunked statistics (4096 ids a chunk, the last one ragged); the others
+    # the per-row kernel.
     for dtype, V, k in [("f32", 1000, 3), ("f16", 4096, 5), ("bf16", 777, 16), ("f32", 5, 1),
-                        ("f32", 50000, 2)]:
+                        ("f32", 50000, 2), ("bf16", 10000, 4), ("f16", 12296, 3)]:
         B = 6
         target = rng.normal(0, 2.0, size=(B, k + 1, V)).astype(np.float32)
         draft = (target[:, :k] + rng.normal(0, 1.0, size=(B, k, V))).astype(np.float32)
