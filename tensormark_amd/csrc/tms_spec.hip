@@ -218,8 +218,8 @@ __global__ __launch_bounds__(kBlock) void spec_stats_kernel(SArgs a) {
 //   spec_chunk_max_kernel: the chunk's max of v / T and NaN/+inf flag.
 //   spec_chunk_z_kernel:   the row's max and status from its chunks' parts,
 //                          then the chunk's share of Z (exact int64); chunk 0
-//                          writes the row's m and status, the chunk holding
-//                          the draft token its weight ex.
+//                          writes the row's record: m, status and the draft
+//                          token's weight ex.
 // The resolve kernel sums a row's Z shares (exact in any order).  m, status,
 // Z and ex equal those of spec_stats_kernel.
 template <typename T>
@@ -255,11 +255,11 @@ __global__ __launch_bounds__(kBlock) void spec_chunk_max_kernel(SArgs a) {
     mx = block_max_f32(mx, shf);
     nf = block_or(nf, shi);
     if (t == 0) {
-        SpecPart pt;
-        pt.m = mx;
-        pt.nf = nf;
-        pt.z = 0;
-        a.zparts[(int64_t)g * a.C + c] = pt;
+        // Agent-scope stores: workgroups on different XCDs write neighbouring
+        // records of one cache line, read by the next kernel.
+        uint64_t* w = (uint64_t*)(a.zparts + (int64_t)g * a.C + c);
+        st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)nf << 32));
+        st_agent(&w[1], (uint64_t)0);
     }
 }
 
@@ -286,8 +286,9 @@ __global__ __launch_bounds__(kBlock) void spec_chunk_z_kernel(SArgs a) {
     float mx = -__builtin_huge_valf();
     int nf = 0;
     for (int u = 0; u < a.C; ++u) {
-        mx = fmaxf(mx, parts[u].m);
-        nf |= parts[u].nf;
+        const uint64_t w = ld_agent((uint64_t*)(parts + u));
+        mx = fmaxf(mx, __uint_as_float((uint32_t)w));
+        nf |= (int)(w >> 32);
     }
     int st = TMS_ROW_OK;
     if (nf) st = TMS_ROW_NONFINITE;
@@ -310,18 +311,20 @@ __global__ __launch_bounds__(kBlock) void spec_chunk_z_kernel(SArgs a) {
         __syncthreads();   // the table's LDS writes, as block_sum_i64 orders them
     }
     if (t == 0) {
-        a.zparts[(int64_t)g * a.C + c].z = z;
+        st_agent((uint64_t*)(a.zparts + (int64_t)g * a.C + c) + 1, (uint64_t)z);
         const int di = i < a.k ? i : (i > a.k ? i - a.k - 1 : -1);
         const int x = di >= 0 ? a.tokens[(int64_t)b * a.k + di] : -1;
         const bool xin = x >= 0 && x < a.V;
         if (c == 0) {
-            a.stats[g].m = mx;
-            a.stats[g].status = st;
-            a.stats[g].Z = 0;
-            a.stats[g].pad = 0;
+            // The whole record from one workgroup (the token's weight by one
+            // scalar load), so no two workgroups write parts of it.
+            const int64_t ex = (st == TMS_ROW_OK && xin) ? weight(Elt<T>::scalar(row + x), temp, md, tab) : 0;
+            uint64_t* w = (uint64_t*)(a.stats + g);
+            st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)st << 32));
+            st_agent(&w[1], (uint64_t)0);
+            st_agent(&w[2], (uint64_t)ex);
+            st_agent(&w[3], (uint64_t)0);
         }
-        if (c == (xin ? x / kSpecChunk : 0))
-            a.stats[g].ex = (st == TMS_ROW_OK && xin) ? weight(Elt<T>::scalar(row + x), temp, md, tab) : 0;
     }
 }
 
@@ -349,7 +352,13 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     {
         const int R = 2 * a.k + 1;
         if (t < R) {
-            srow[t] = a.stats[g0 + t];
+            const uint64_t* w = (const uint64_t*)(a.stats + g0 + t);
+            const uint64_t w0 = ld_agent(&w[0]);
+            srow[t].m = __uint_as_float((uint32_t)w0);
+            srow[t].status = (int32_t)(w0 >> 32);
+            srow[t].Z = (int64_t)ld_agent(&w[1]);
+            srow[t].ex = (int64_t)ld_agent(&w[2]);
+            srow[t].pad = 0;
             zrow[t] = 0;
         }
         if (t < a.k) {
@@ -362,7 +371,8 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
         __syncthreads();
         if (a.C > 0) {
             for (int idx = t; idx < R * a.C; idx += kBlock)
-                atomicAdd((unsigned long long*)&zrow[idx / a.C], (unsigned long long)a.zparts[(int64_t)g0 * a.C + idx].z);
+                atomicAdd((unsigned long long*)&zrow[idx / a.C],
+                          (unsigned long long)ld_agent((const uint64_t*)(a.zparts + (int64_t)g0 * a.C + idx) + 1));
             __syncthreads();
             if (t < R) srow[t].Z = zrow[t];
             __syncthreads();
@@ -494,8 +504,33 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
         const int64_t ed = weight(Elt<T>::scalar(rd + id), temp, md, tab);
         return residual(et, ed, ts.Z, ds.Z);
     };
+    // Runs of up to kRunMax ids: every load issued at once (clamped
+    // addresses), the weights kept in registers for the scan and the search;
+    // longer runs walk the ids one by one.
+    constexpr int kRunMax = 16;
+    const bool cached = E <= kRunMax;
+    int64_t wc[kRunMax];
     int64_t mine = 0;
-    for (int id = my_lo; id < my_hi; ++id) mine += w_at(id);
+    if (cached) {
+        float xt[kRunMax], xd[kRunMax];
+#pragma unroll
+        for (int j = 0; j < kRunMax; ++j) {
+            const int id = min(my_lo + j, phi - 1);
+            xt[j] = Elt<T>::scalar(rt + id);
+            xd[j] = use_t ? 0.0f : Elt<T>::scalar(rd + id);
+        }
+#pragma unroll
+        for (int j = 0; j < kRunMax; ++j) {
+            wc[j] = 0;
+            if (my_lo + j < my_hi) {
+                const int64_t et = weight(xt[j], temp, mt, tab);
+                wc[j] = use_t ? et : residual(et, weight(xd[j], temp, md, tab), ts.Z, ds.Z);
+            }
+            mine += wc[j];
+        }
+    } else {
+        for (int id = my_lo; id < my_hi; ++id) mine += w_at(id);
+    }
     // Exclusive scan of the threads' sums.
     const int lane = t & 63, wv = t >> 6;
     const int64_t inc = wave_incl_scan_i64(mine);
@@ -507,9 +542,21 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     if (mine > 0 && pre <= thr && thr < pre + mine) {
         int64_t acc_w = pre;
         int tok = my_hi - 1;
-        for (int id = my_lo; id < my_hi; ++id) {
-            acc_w += w_at(id);
-            if (acc_w > thr) { tok = id; break; }
+        if (cached) {
+            bool found = false;
+#pragma unroll
+            for (int j = 0; j < kRunMax; ++j) {
+                acc_w += wc[j];
+                if (!found && my_lo + j < my_hi && acc_w > thr) {
+                    tok = my_lo + j;
+                    found = true;
+                }
+            }
+        } else {
+            for (int id = my_lo; id < my_hi; ++id) {
+                acc_w += w_at(id);
+                if (acc_w > thr) { tok = id; break; }
+            }
         }
         a.out_acc[b] = acc;
         a.out_tok[b] = tok;
