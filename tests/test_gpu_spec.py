@@ -157,3 +157,15 @@ def test_spec_repeated_calls(orc, sampler):
         assert np.array_equal(a[key], b[key]), key
     words = philox_words(orc, c["params"], 4)
     check_spec(orc, a, c["target"], c["draft"], c["tokens"], c["params"], words)
+
+
+def test_spec_back_to_back_different_batches(orc, sampler):
+    """Full-size calls on different batches, back to back: each call's chunk
+    statistics are written by workgroups on all XCDs and read by the next
+    kernel, so a stale record from the previous call would change an accept
+    count or a token."""
+    for seed in (21, 22, 23):
+        c = workloads.cfg4(seed=seed)
+        gpu = run_spec(sampler, c["target"], c["draft"], c["tokens"], c["params"])
+        words = philox_words(orc, c["params"], c["draft"].shape[1])
+        check_spec(orc, gpu, c["target"], c["draft"], c["tokens"], c["params"], words)
