@@ -201,13 +201,13 @@ __global__ __launch_bounds__(kBlock) void spec_stats_kernel(SArgs a) {
             const int x = a.tokens[(int64_t)b * a.k + di];
             if (x >= 0 && x < a.V) ex = weight(Elt<T>::scalar(row + x), temp, md, tab);
         }
-        tms_spec_stat s;
-        s.m = mx;
-        s.status = st;
-        s.Z = z;
-        s.ex = ex;
-        s.pad = 0;
-        a.stats[g] = s;
+        // Agent-scope stores, as the chunked statistics write theirs: rows on
+        // different XCDs share cache lines of the record array.
+        uint64_t* w = (uint64_t*)(a.stats + g);
+        st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)st << 32));
+        st_agent(&w[1], (uint64_t)z);
+        st_agent(&w[2], (uint64_t)ex);
+        st_agent(&w[3], (uint64_t)0);
     }
 }
 
