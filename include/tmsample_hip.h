@@ -62,7 +62,9 @@ enum {
     TMS_ROW_BAD_PARAMS = 1,   /* temperature <= 0 or non-finite on a sampled row */
     TMS_ROW_ALL_MASKED = 2,   /* every id is -inf after mask and penalties */
     TMS_ROW_NONFINITE = 3,    /* NaN or +inf after masking, or lg overflowed */
-    TMS_ROW_UNSUPPORTED = 4,  /* top-p-only row with too many candidates */
+    TMS_ROW_UNSUPPORTED = 4,  /* a row that breaks the TMS_ROWS_TOPK promise (top_k = 0
+                                 or > 128, not greedy) in a call that runs no whole-row
+                                 pass; never produced under TMS_ROWS_ANY */
     TMS_ROW_INTERNAL = 5      /* a chunk list never arrived (bounded wait expired) */
 };
 
@@ -132,9 +134,15 @@ typedef struct tms_sample_args {
     uint32_t row_kinds;       /* TMS_ROWS_ANY, or TMS_ROWS_TOPK: the caller promises
                                  every row is greedy or has 1 <= top_k <= 128, and
                                  the library may take its top-k kernel (it does when
-                                 batch x chunks <= 1024 workgroups); under that
-                                 kernel a row that breaks the promise gets
-                                 TMS_ROW_UNSUPPORTED, never a wrong sample */
+                                 batch x chunks <= 1024 workgroups).  TMS_ROWS_ANY
+                                 calls (and TMS_ROWS_TOPK calls with recent_stride >
+                                 512) are followed by a second launch, the whole-row
+                                 pass, that samples every row the chunked kernel
+                                 could not finish (top-p rows with more than 1024
+                                 entries within 40 of the maximum, draws past those
+                                 entries); without that pass a row that breaks the
+                                 promise gets TMS_ROW_UNSUPPORTED, never a wrong
+                                 sample */
     uint32_t reserved;        /* must be 0 */
 } tms_sample_args;
 

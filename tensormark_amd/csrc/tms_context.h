@@ -43,6 +43,10 @@ struct tms_context {
     tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]
     uint64_t* spec_zparts;     // [max_batch][2 * kSpecMaxK + 1][spec_chunks] chunk statistics, 2 words each
     int spec_chunks;           // ceil(max_vocab / 4096)
+    uint32_t* dqueue;          // whole-row pass queue: 3 counters, then [max_batch] rows
+    uint64_t* dense;           // [dense_slots][2 * max_vocab] the whole-row pass (separate allocation)
+    int dense_slots;           // min(max_batch, kDenseGridMax): one region per pass workgroup
+    size_t dense_bytes;
 };
 
 #endif  // TMS_CONTEXT_H

@@ -38,7 +38,7 @@
 
 #include <algorithm>
 
-#include "tms_sample_common.h"
+#include "tms_dense.h"
 
 namespace tms {
 
@@ -720,8 +720,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     if (sm.misc[3]) status = TMS_ROW_INTERNAL;
     else if (bad_params) status = TMS_ROW_BAD_PARAMS;
     else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
-    else if ((fo & FLAG_OVERFLOW) || (mode == MODE_TOPP && N > kToppCap)) status = TMS_ROW_UNSUPPORTED;
-    else if (N == 0) status = TMS_ROW_ALL_MASKED;
+    else if (N == 0 && !(fo & FLAG_OVERFLOW)) status = TMS_ROW_ALL_MASKED;   // an overflowed list holds 0
+    // Top-p rows whose lists overflowed, or whose top min(N, K) exceed the
+    // merge capacity, take the whole-row path (tms_dense.h).
+    const bool go_dense = status == TMS_ROW_OK && mode == MODE_TOPP &&
+                          ((fo & FLAG_OVERFLOW) || min(N, K) > kToppCap);
 
     uint64_t* srt = sm.big.m.surv;
     int n_acc = 0;
@@ -793,11 +796,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         lds_sync();
         full = sm.misc[1] != 0;
     }
-    if (status == TMS_ROW_OK && full) {
+    if (status == TMS_ROW_OK && full && !go_dense) {
         // Whole lists, in rounds: the running top list (surv[0..n_acc)) plus
         // as many chunk lists as fit in kUni, ranked by binary search against
         // each other.  Top-k rows read at most K entries a list.
-        const int keep_cap = mode == MODE_TOPP ? kToppCap : K;
+        const int keep_cap = mode == MODE_TOPP ? min(kToppCap, K) : K;
         if (t < S) sm.list_s[t] = mode == MODE_TOPP ? sm.list_n[t] : min(sm.list_n[t], K);
         n_acc = 0;
         int c_next = 0;
@@ -858,6 +861,10 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         write_row_error(a, row, status);
         return;
     }
+    if (go_dense) {
+        defer_dense(a, row);
+        return;
+    }
 
     if (mode == MODE_GREEDY) {
         const int tok = (int)ckey_id(srt[0]);
@@ -915,16 +922,23 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         if (lane == 0) sm.wave_i[wv] = sig;
         lds_sync();
         n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
+        n = min(n, K);   // tmsample::sample sums over the top K only (tmsample.h:185-191)
         lds_sync();
     }
     double* pr = (double*)sm.big.m.uni;               // staging no longer needed
     double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
     for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
     lds_sync();
+    if (t == 0) sm.nvalid = 0;
+    lds_sync();
     if (wv == 0) {
-        tail_topp_fast(a, row, P, srt, n, K, pr, q);
+        const bool lost = tail_topp_fast(a, row, P, srt, n, K, pr, q);
+        if (lane == 0) sm.nvalid = lost;
         TMS_TR(8);
     }
+    lds_sync();
+    // The answer needs the order past the held entries: the whole row.
+    if (sm.nvalid) defer_dense(a, row);
 }
 
 }  // namespace tms
@@ -984,12 +998,21 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kLeanMaxChunksHost);
     const size_t off_zp = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
     ctx->spec_chunks = (max_vocab + 4095) / 4096;
-    ctx->bytes = off_zp + nb * (2 * tms::kSpecMaxK + 1) * (size_t)ctx->spec_chunks * 2 * sizeof(uint64_t);
+    const size_t off_dq = off_zp + nb * (2 * tms::kSpecMaxK + 1) * (size_t)ctx->spec_chunks * 2 * sizeof(uint64_t);
+    ctx->bytes = off_dq + (tms::kDenseQueueHead + nb) * sizeof(uint32_t);
     int rc = TMS_OK;
     if (hipMalloc(&ctx->ws, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipMemset(ctx->ws, 0, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;   // lists start zeroed
     else if (hipMemset((char*)ctx->ws + off_ones, 0xFF, ones_words * 4) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipDeviceSynchronize() != hipSuccess) rc = TMS_ERR_HIP;
+    // The whole-row path's region: never read before it is written, so not
+    // cleared.
+    ctx->dense_slots = std::min(max_batch, tms::kDenseGridMax);
+    ctx->dense_bytes = (size_t)ctx->dense_slots * 2 * (size_t)max_vocab * sizeof(uint64_t);
+    if (rc == TMS_OK && hipMalloc(&ctx->dense, ctx->dense_bytes) != hipSuccess) {
+        ctx->dense = nullptr;
+        rc = TMS_ERR_HIP;
+    }
     if (rc != TMS_OK) {
         if (ctx->ws) (void)hipFree(ctx->ws);
         delete ctx;
@@ -1005,6 +1028,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->spec_stats = (tms_spec_stat*)(p + off_ss);
     ctx->tlists = (uint64_t*)(p + off_tl);
     ctx->spec_zparts = (uint64_t*)(p + off_zp);
+    ctx->dqueue = (uint32_t*)(p + off_dq);
     (void)hipSetDevice(prev);
     *out = ctx;
     return TMS_OK;
@@ -1015,13 +1039,16 @@ extern "C" int tms_destroy(tms_context* ctx) {
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(ctx->device);
-    const hipError_t e = hipFree(ctx->ws);
+    hipError_t e = hipFree(ctx->ws);
+    if (ctx->dense && hipFree(ctx->dense) != hipSuccess) e = hipErrorUnknown;
     (void)hipSetDevice(prev);
     delete ctx;
     return e == hipSuccess ? TMS_OK : TMS_ERR_HIP;
 }
 
-extern "C" size_t tms_workspace_bytes(const tms_context* ctx) { return ctx ? ctx->bytes : 0; }
+extern "C" size_t tms_workspace_bytes(const tms_context* ctx) {
+    return ctx ? ctx->bytes + ctx->dense_bytes : 0;
+}
 
 extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipStream_t stream) {
     if (!ctx || !a || !a->logits || !a->params || !a->out_tokens || !a->out_status)
@@ -1066,6 +1093,14 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     k.counters = ctx->counters;
     k.lists = ctx->lists;
     k.tlists = ctx->tlists;
+    // The whole-row pass follows any call without the top-k promise, and a
+    // top-k call whose windows can overflow the top-k kernel's penalised-entry
+    // lists (more than kCand window ids).
+    const bool dense_pass = a->row_kinds == TMS_ROWS_ANY || (a->recent && a->recent_stride > tms::kCand);
+    k.dense = dense_pass ? ctx->dense : nullptr;
+    k.dense_stride = ctx->max_vocab;
+    k.dqueue = ctx->dqueue;
+    const int dense_grid = std::min(a->batch, ctx->dense_slots);
 #ifdef TMS_TRACE
     k.trace = g_tms_trace_host;
 #endif
@@ -1083,7 +1118,9 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
             tms::KArgs kl = k;
             kl.CE = ce;
             kl.S = s_lean;
-            return tms_launch_topk(kl, a->dtype, fast, a->batch, stream);
+            const int rc = tms_launch_topk(kl, a->dtype, fast, a->batch, stream);
+            if (rc != TMS_OK || !dense_pass) return rc;
+            return tms_launch_dense(kl, a->dtype, dense_grid, stream);
         }
     }
     const dim3 grid((unsigned)(a->batch * k.S)), block(tms::kBlock);
@@ -1103,5 +1140,6 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
             break;
     }
 #undef TMS_LAUNCH
-    return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;
+    if (hipGetLastError() != hipSuccess) return TMS_ERR_HIP;
+    return dense_pass ? tms_launch_dense(k, a->dtype, dense_grid, stream) : TMS_OK;
 }

@@ -51,6 +51,8 @@ constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no e
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
 constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per list
 constexpr int kReadRounds = 64;            // bound on the merger's re-reads of a sample
+constexpr int kDenseQueueHead = 64;        // u32 words before the whole-row queue's rows
+constexpr int kDenseGridMax = 256;         // workgroups of the whole-row pass
 
 enum : int { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_TOPP = 2 };
 enum : int { FLAG_NONFINITE = 1, FLAG_OVERFLOW = 2 };
@@ -78,6 +80,11 @@ struct KArgs {
     uint32_t* counters;    // [B] arrival tickets, reset by the merger
     uint64_t* lists;       // [B][S][kListStride]: header, entries; headers reset by the merger
     uint64_t* tlists;      // [B][S][kTopkListStride]: the top-k kernel's lists, zeroed by the merger
+    uint64_t* dense;       // [B][2 * dense_stride]: the whole-row pass's keys and sums; null when
+                           // the call runs no whole-row pass
+    int64_t dense_stride;  // >= V
+    uint32_t* dqueue;      // [0] rows queued, [1] rows taken, [2] pass workgroups done,
+                           // [kDenseQueueHead + i] the queued rows
 #ifdef TMS_TRACE
     uint64_t* trace;
 #endif
@@ -124,7 +131,7 @@ struct Smem {
     int list_s[kMaxChunks];        // survivors of each chunk list
     int hist[256];
     int ncand;
-    int nvalid;
+    int nvalid;                    // top-p tail: the row goes to the whole-row pass
     int misc[8];
     uint64_t theta;
 };
@@ -321,6 +328,21 @@ __device__ __forceinline__ void write_row_error(const KArgs& a, int row, int sta
     for (int i = t; i < a.topk_cap; i += kBlock) {
         if (ids) ids[i] = -1;
         if (probs) probs[i] = 0.0f;
+    }
+}
+
+// Hand row `row` to the whole-row pass that follows the launch (all
+// threads of the workgroup call this; thread 0 queues the row).  Without
+// that pass the row reports TMS_ROW_UNSUPPORTED.
+__device__ __forceinline__ void defer_dense(const KArgs& a, int row) {
+    if (!a.dense) {
+        write_row_error(a, row, TMS_ROW_UNSUPPORTED);
+        return;
+    }
+    if (threadIdx.x == 0) {
+        const uint32_t slot = __hip_atomic_fetch_add(&a.dqueue[0], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        a.dqueue[kDenseQueueHead + slot] = (uint32_t)row;
     }
 }
 
@@ -606,11 +628,16 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
             a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i < n ? (int)ckey_id(srt[i]) : -1;
 }
 
-// The same tail for top-p rows (n <= kToppCap entries in LDS, exact prefix
-// only), one wave reading the entries from LDS in order.
-__device__ void tail_topp(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
+// The same tail for top-p rows (n = min(K, significant entries) <= kToppCap
+// entries in LDS), one wave reading the entries from LDS in order.  Returns
+// true, having written nothing, when the answer needs the order past the
+// held entries (the draw or a min-p threshold of at most e^-40 reaching past
+// them, or more top-k ids asked for than are held): the caller then runs
+// the whole-row path.
+__device__ bool tail_topp(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
                           int n, int K, double* pr, double* q) {
     const int lane = threadIdx.x & 63;
+    if (n < K && a.topk_cap > n && (a.out_topk_ids || a.out_topk_probs)) return true;
     double z = 0;
 #pragma unroll 8
     for (int i = 0; i < n; ++i) z += pr[i];
@@ -632,8 +659,10 @@ __device__ void tail_topp(const KArgs& a, int row, const tms_row_params& P, cons
         const double mp = (double)P.min_p;
         int m = 1;
         while (m < kp && m < n && pr[m] >= mp) ++m;
-        if (m >= n && n < K && mp <= 4.248354255291589e-18) m = K;   // exp(-40)
-        if (m < kp) kp = m;
+        // Past the held entries pr <= e^-40 (4.2484e-18): below a larger
+        // min_p; a smaller one needs the entries themselves.
+        if (m == n && m < kp && !(mp > 4.3e-18)) return true;
+        kp = m;
     }
     const int keep = kp;
     const int lim = keep < n ? keep : n;
@@ -659,12 +688,12 @@ __device__ void tail_topp(const KArgs& a, int row, const tms_row_params& P, cons
             }
         }
     }
-    // tokidx >= n: the draw fell past the last entry that moves the sums, so
-    // the reference would return its K-th entry, which this row does not hold.
-    const bool lost = tokidx >= n;
+    // tokidx >= n: the draw fell past the last entry that moves the sums; the
+    // reference returns its entry at that rank, which this row does not hold.
+    if (tokidx >= n) return true;
     if (lane == 0) {
-        a.out_tokens[row] = lost ? -1 : (int)ckey_id(srt[tokidx]);
-        a.out_status[row] = lost ? TMS_ROW_UNSUPPORTED : TMS_ROW_OK;
+        a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
+        a.out_status[row] = TMS_ROW_OK;
         if (a.out_keep) a.out_keep[row] = keep;
     }
     int32_t* ids = a.out_topk_ids ? a.out_topk_ids + (int64_t)row * a.topk_cap : nullptr;
@@ -674,6 +703,7 @@ __device__ void tail_topp(const KArgs& a, int row, const tms_row_params& P, cons
         if (ids) ids[i] = have ? (int)ckey_id(srt[i]) : -1;
         if (probs) probs[i] = have ? (float)(pr[i] / z) : 0.0f;
     }
+    return false;
 }
 
 // Minimum of non-negative ints across the wave (DPP steps towards lane 63;
@@ -704,13 +734,11 @@ __device__ __forceinline__ int wave_min_nonneg(int v) {
 // its threshold, and any call that returns per-entry probabilities, takes
 // the sequential tail_topp.  The min-p cut compares the same pr values, so
 // it is exact here.
-__device__ void tail_topp_fast(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
+__device__ bool tail_topp_fast(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
                                int n, int K, double* pr, double* q) {
     static_assert(kToppCap <= 64 * 16, "lane blocks of at most 16 entries");
-    if (a.topk_cap && a.out_topk_probs) {
-        tail_topp(a, row, P, srt, n, K, pr, q);
-        return;
-    }
+    if (a.topk_cap && a.out_topk_probs) return tail_topp(a, row, P, srt, n, K, pr, q);
+    if (n < K && a.topk_cap > n && a.out_topk_ids) return true;
     const int lane = threadIdx.x & 63;
     const int per = (n + 63) >> 6;
     const int b0 = lane * per;
@@ -763,8 +791,8 @@ __device__ void tail_topp_fast(const KArgs& a, int row, const tms_row_params& P,
             if (j < per && i >= 1 && i < n && pr[i] < mp) fl = i;
         }
         fl = wave_min_nonneg(fl);
-        int m = min(fl, min(kp, n));
-        if (m >= n && n < K && mp <= 4.248354255291589e-18) m = K;   // exp(-40)
+        if (fl >= n && n < kp && !(mp > 4.3e-18)) return true;   // as in tail_topp
+        const int m = min(fl, min(kp, n));
         if (m < kp) kp = m;
     }
     const int keep = kp;
@@ -789,22 +817,24 @@ __device__ void tail_topp_fast(const KArgs& a, int row, const tms_row_params& P,
     }
     if (!ok) {
         TMS_TV(16, 1);
-        tail_topp(a, row, P, srt, n, K, pr, q);
-        return;
+        return tail_topp(a, row, P, srt, n, K, pr, q);
     }
     // tokidx >= n: the draw fell past the last entry that moves the sums
-    const bool lost = tokidx >= n;
+    if (tokidx >= n) return true;
     if (lane == 0) {
-        a.out_tokens[row] = lost ? -1 : (int)ckey_id(srt[tokidx]);
-        a.out_status[row] = lost ? TMS_ROW_UNSUPPORTED : TMS_ROW_OK;
+        a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
+        a.out_status[row] = TMS_ROW_OK;
         if (a.out_keep) a.out_keep[row] = keep;
     }
     if (a.topk_cap && a.out_topk_ids)
         for (int i = lane; i < a.topk_cap; i += 64)
             a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i < n ? (int)ckey_id(srt[i]) : -1;
+    return false;
 }
 
 }  // namespace tms
 
 // Launches the top-k kernel (tms_topk.hip) over `batch` rows.
 int tms_launch_topk(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
+// Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.
+int tms_launch_dense(const tms::KArgs& k, int dtype, int workgroups, hipStream_t stream);

@@ -28,7 +28,8 @@
 //              no store waits.
 //   merge      bound (bisection on order keys), gather from registers, rank
 //              by counting, tail on wave 0.
-// A row that is not greedy and not top-k <= 128 breaks the hint and reports
+// A row that is not greedy and not top-k <= 128 breaks the hint: it goes to
+// the whole-row pass (tms_dense.hip) when the call runs one, else it reports
 // TMS_ROW_UNSUPPORTED.
 
 #include "tms_sample_common.h"
@@ -844,9 +845,9 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     TMS_TR(10);
     int status = TMS_ROW_OK;
     if (sm.misc[3]) status = TMS_ROW_INTERNAL;
-    else if (unsupported) status = TMS_ROW_UNSUPPORTED;
     else if (bad_params) status = TMS_ROW_BAD_PARAMS;
     else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
+    else if (unsupported) status = TMS_ROW_UNSUPPORTED;   // the whole-row path below
 
     uint64_t* srt = sm.big.m.srt;
     int n = 0;        // candidates gathered, then the sorted top-K kept
@@ -1059,6 +1060,14 @@ __global__ __launch_bounds__(kBlock, 2) void topk_kernel(KArgs a) {
     if (!lost) zero_own();
     const bool sampled_ok = status == TMS_ROW_OK && !greedy;
     if (!lost && !sampled_ok) zero_others(t, kBlock);
+    if (status == TMS_ROW_UNSUPPORTED) {
+        // A row outside this kernel's kinds (top_k = 0 or > 128), or more
+        // window ids than the lists stage: the exact whole-row path.
+        if (a.dense) defer_dense(a, row);
+        else write_row_error(a, row, TMS_ROW_UNSUPPORTED);
+        TK_TRACE_FLUSH();
+        return;
+    }
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
         TK_TRACE_FLUSH();

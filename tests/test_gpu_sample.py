@@ -320,10 +320,9 @@ def test_decisions_on_exact_boundaries(sampler, orc, top_k):
         p["top_p"][b] = tp
         assert orc.canonical(int(draws[b, 0]), int(draws[b, 1])) == u
     mask = workloads.pack_bits(bits)
-    # A top_k = 0 row's id list holds its entries within 40 of the maximum
-    # and pads with -1 (include/tmsample_hip.h); with 4 or 8 held entries an
-    # 8-slot list would reach the padding, so those rows run without one.
-    for cap in ((0, 8) if top_k else (0,)):
+    # With 4 or 8 finite entries an 8-slot id list of a top_k = 0 row runs
+    # into the masked ids (-inf, in id order): the whole-row pass lists them.
+    for cap in (0, 8):
         want = orc.sample_batch(x, p, mask=mask, draws=draws, topk_cap=cap)
         g = run_gpu(sampler, x, p, mask=mask, draws=draws, topk_cap=cap)
         check(g, want, cap)
@@ -352,15 +351,79 @@ def test_repeated_calls_reuse_workspace(sampler, orc):
         check(g, want, 40)
 
 
-@pytest.mark.xfail(reason="dense rows without top-k need a full-row sort path; the kernel "
-                          "reports TMS_ROW_UNSUPPORTED for them", strict=True)
 def test_dense_row_without_topk(sampler, orc):
+    """top_k = 0 over a row whose every entry lies within 40 of the maximum:
+    the whole-row pass (full sort) samples it."""
     rng = np.random.default_rng(12)
     x = rng.normal(0, 2, (2, 20000)).astype(np.float32)
     p = params_array(2, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(2))
     want = orc.sample_batch(x, p, topk_cap=16)
     g = run_gpu(sampler, x, p, topk_cap=16)
     check(g, want, 16)
+
+
+def _large_k_rows(kind, K, B, V, rng):
+    """Rows for 128 < top_k < V.  "dense": every entry within 40 of the
+    maximum (n > K).  "spiked": 50 ids 60 above the rest, so the entries that
+    move the sums are fewer than K and the rest of the top K lies past them.
+    "masked": K // 2 allowed ids, so fewer than K finite entries."""
+    x = rng.normal(0.0, 1.5, (B, V)).astype(np.float32)
+    mask = None
+    if kind == "spiked":
+        for b in range(B):
+            x[b, rng.choice(V, 50, replace=False)] += 60.0
+    elif kind == "masked":
+        bits = np.zeros((B, ((V + 31) // 32) * 32), bool)
+        for b in range(B):
+            bits[b, rng.choice(V, K // 2, replace=False)] = True
+        mask = workloads.pack_bits(bits)
+    p = params_array(B, temperature=1.0, top_k=K, top_p=0.95, seed=np.arange(B) + 3 * K)
+    p["top_p"] = rng.choice([0.5, 0.9, 0.999, 1.0], size=B)
+    p["min_p"] = rng.choice([0.0, 0.0, 1e-3], size=B)
+    p["temperature"] = rng.choice([0.7, 1.0, 1.6], size=B)
+    return x, p, mask
+
+
+@pytest.mark.parametrize("cap", [0, 16])
+@pytest.mark.parametrize("kind", ["dense", "spiked", "masked"])
+@pytest.mark.parametrize("K", [129, 200, 1000])
+def test_large_top_k_rows(sampler, orc, K, kind, cap):
+    """128 < top_k < V: tmsample::sample normalises and draws over the top K
+    only (tmsample.h:180-199), with the survivors both above and below K."""
+    rng = np.random.default_rng(1000 * K + len(kind))
+    x, p, mask = _large_k_rows(kind, K, 16, 60000, rng)
+    want = orc.sample_batch(x, p, mask=mask, topk_cap=cap)
+    g = run_gpu(sampler, x, p, mask=mask, topk_cap=cap)
+    check(g, want, cap)
+
+
+@pytest.mark.parametrize("cap", [0, 64, 2000])
+def test_dense_rows_whole_row_pass(sampler, orc, cap):
+    """Rows only the whole-row pass can finish: top_k = 0 over flat rows
+    (tens of thousands of entries within 40 of the maximum) at V = 128256,
+    with penalties and a mask; a row whose draw lands past the entries that
+    move the sums (u just below 1 with top_p = 1); a min-p threshold below
+    e^-40; id lists longer than the held entries."""
+    rng = np.random.default_rng(77 + cap)
+    B, V = 8, 128256
+    x = rng.normal(0.0, 1.0, (B, V)).astype(np.float32)
+    x[4:6, :40] += 60.0           # rows 4, 5: 40 entries move the sums
+    recent = rng.integers(0, V, (B, 256)).astype(np.int32)
+    p = params_array(B, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(B) + 11,
+                     repeat_penalty=1.1, repeat_last_n=256, frequency_penalty=0.2,
+                     presence_penalty=0.1)
+    p["top_k"] = [0, 0, 50000, 0, 1000, 0, 0, 300]
+    p["top_p"] = [0.9, 0.5, 0.95, 1.0, 1.0, 1.0, 0.99, 0.8]
+    p["temperature"] = [1.0, 0.6, 1.3, 1.0, 1.0, 1.0, 2.0, 1.0]
+    p["min_p"] = [0.0, 0.0, 0.0, 0.0, 0.0, 1e-30, 0.01, 0.0]
+    draws = rng.integers(0, 2**32, (B, 2), dtype=np.uint64).astype(np.uint32)
+    draws[3] = draws[4] = [0xFFFFFFFF, 0xFFFFFFFF]   # u = 1 - 2^-53
+    bits = np.ones((B, ((V + 31) // 32) * 32), bool)
+    bits[1, ::3] = False
+    mask = workloads.pack_bits(bits)
+    want = orc.sample_batch(x, p, recent=recent, mask=mask, draws=draws, topk_cap=cap)
+    g = run_gpu(sampler, x, p, recent=recent, mask=mask, draws=draws, topk_cap=cap)
+    check(g, want, cap)
 
 
 def test_topk_kernel_error_rows(sampler, orc):
