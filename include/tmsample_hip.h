@@ -197,6 +197,23 @@ size_t tms_workspace_bytes(const tms_context* ctx);
 int tms_sample_batch(tms_context* ctx, const tms_sample_args* args, hipStream_t stream);
 
 /*
+ * tms_sample_batch without a context and without any allocation, for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  Same arguments, semantics and results as tms_sample_batch;
+ * the workspace is a fixed 18.9 MB device array inside the library (one
+ * copy per device, held until the process ends), so batch <= 64 rows and
+ * vocab <= 262144 ids, else TMS_ERR_CAPACITY.  Runs on the current device
+ * (the stream's device must be current).  The first call on each device
+ * looks the array's address up (hipGetSymbolAddress): make one call before
+ * capturing a graph.  Every call on a device shares that device's array:
+ * calls that overlap on one device (two streams, or two threads) race and
+ * must be serialised by the caller.  Whole-row-pass rows of one call are
+ * sampled one after another.
+ */
+int tms_sample_batch_noalloc(const tms_sample_args* args, hipStream_t stream);
+
+/*
  * Speculative verify: for each sequence, accept draft i while
  * u_i < p_t(x_i) / p_d(x_i); at the first rejection draw from
  * normalize(max(p_t - p_d, 0)); if all k are accepted draw a bonus token

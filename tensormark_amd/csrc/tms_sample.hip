@@ -37,6 +37,7 @@
 // wait for the headers is bounded.
 
 #include <algorithm>
+#include <mutex>
 
 #include "tms_dense.h"
 
@@ -1050,11 +1051,25 @@ extern "C" size_t tms_workspace_bytes(const tms_context* ctx) {
     return ctx ? ctx->bytes + ctx->dense_bytes : 0;
 }
 
-extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipStream_t stream) {
-    if (!ctx || !a || !a->logits || !a->params || !a->out_tokens || !a->out_status)
+// The workspace regions one sampling call uses, and their capacities.
+struct SampleWs {
+    int max_batch, max_vocab;
+    uint32_t* counters;
+    uint32_t* ones;
+    uint64_t* lists;
+    uint64_t* tlists;
+    uint32_t* dqueue;
+    uint64_t* dense;
+    int dense_slots;
+};
+
+// tms_sample_batch over workspace w (a context's, or the allocation-free
+// entry point's static one).
+static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_t stream) {
+    if (!a || !a->logits || !a->params || !a->out_tokens || !a->out_status)
         return TMS_ERR_INVALID_ARG;
     if (a->batch <= 0 || a->vocab <= 0 || a->row_stride < a->vocab) return TMS_ERR_INVALID_ARG;
-    if (a->batch > ctx->max_batch || a->vocab > ctx->max_vocab) return TMS_ERR_CAPACITY;
+    if (a->batch > w.max_batch || a->vocab > w.max_vocab) return TMS_ERR_CAPACITY;
     if (a->mask && a->mask_stride < (a->vocab + 31) / 32) return TMS_ERR_INVALID_ARG;
     // Window counts are 16-bit per id in LDS.
     if (a->recent && (a->recent_stride <= 0 || a->recent_stride > 65535)) return TMS_ERR_INVALID_ARG;
@@ -1081,7 +1096,7 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     k.recent = a->recent;
     k.n_recent = a->n_recent;
     k.recent_stride = a->recent_stride;
-    k.mask = a->mask ? a->mask : ctx->ones;
+    k.mask = a->mask ? a->mask : w.ones;
     k.mask_stride = a->mask ? a->mask_stride : 0;
     k.draws = a->draws;
     k.out_tokens = a->out_tokens;
@@ -1090,17 +1105,17 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     k.out_topk_ids = a->out_topk_ids;
     k.out_topk_probs = a->out_topk_probs;
     k.topk_cap = (a->out_topk_ids || a->out_topk_probs) ? a->topk_cap : 0;
-    k.counters = ctx->counters;
-    k.lists = ctx->lists;
-    k.tlists = ctx->tlists;
+    k.counters = w.counters;
+    k.lists = w.lists;
+    k.tlists = w.tlists;
     // The whole-row pass follows any call without the top-k promise, and a
     // top-k call whose windows can overflow the top-k kernel's penalised-entry
     // lists (more than kCand window ids).
     const bool dense_pass = a->row_kinds == TMS_ROWS_ANY || (a->recent && a->recent_stride > tms::kCand);
-    k.dense = dense_pass ? ctx->dense : nullptr;
-    k.dense_stride = ctx->max_vocab;
-    k.dqueue = ctx->dqueue;
-    const int dense_grid = std::min(a->batch, ctx->dense_slots);
+    k.dense = dense_pass ? w.dense : nullptr;
+    k.dense_stride = w.max_vocab;
+    k.dqueue = w.dqueue;
+    const int dense_grid = std::min(a->batch, w.dense_slots);
 #ifdef TMS_TRACE
     k.trace = g_tms_trace_host;
 #endif
@@ -1142,4 +1157,88 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
 #undef TMS_LAUNCH
     if (hipGetLastError() != hipSuccess) return TMS_ERR_HIP;
     return dense_pass ? tms_launch_dense(k, a->dtype, dense_grid, stream) : TMS_OK;
+}
+
+extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipStream_t stream) {
+    if (!ctx) return TMS_ERR_INVALID_ARG;
+    SampleWs w;
+    w.max_batch = ctx->max_batch;
+    w.max_vocab = ctx->max_vocab;
+    w.counters = ctx->counters;
+    w.ones = ctx->ones;
+    w.lists = ctx->lists;
+    w.tlists = ctx->tlists;
+    w.dqueue = ctx->dqueue;
+    w.dense = ctx->dense;
+    w.dense_slots = ctx->dense_slots;
+    return sample_launch(w, a, stream);
+}
+
+// ============================================= allocation-free entry point
+//
+// tms_sample_batch_noalloc runs the same kernels over `scratch`, a
+// file-scope device array of fixed size, instead of a context's workspace:
+// batches of up to kNoAllocRows rows of up to kNoAllocVocab ids, and one
+// region for the whole-row pass (its rows are taken one after another).
+// The array starts zeroed when the code object loads, and every launch
+// leaves its counters, lists and queue at zero again, as a context's
+// workspace does.  The all-ones mask row (for calls without a mask) is set
+// once per device.  In host code `scratch` names a host-side stand-in, so
+// its device address is looked up once per device (hipGetSymbolAddress,
+// with that device current) and only that address reaches the kernels and
+// the memset.
+
+namespace {
+constexpr int kNoAllocRows = 64;
+constexpr int kNoAllocVocab = 262144;
+constexpr size_t kNoAllocChunks = kNoAllocVocab / tms::kChunk;   // 16
+constexpr size_t align32(size_t words) { return (words + 31) / 32 * 32; }   // u64 words: 256 bytes
+constexpr size_t kNaCounters = 0;
+constexpr size_t kNaLists = kNaCounters + align32((size_t)kNoAllocRows * tms::kCounterStride / 2);
+constexpr size_t kNaTlists = kNaLists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kListStride);
+constexpr size_t kNaQueue = kNaTlists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kTopkListStride);
+constexpr size_t kNaOnes = kNaQueue + align32((tms::kDenseQueueHead + kNoAllocRows + 1) / 2);
+constexpr size_t kNaDense = kNaOnes + align32(kNoAllocVocab / 64);
+constexpr size_t kNaWords = kNaDense + 2 * (size_t)kNoAllocVocab;   // 18.9 MB
+}  // namespace
+
+static __device__ __align__(256) uint64_t scratch[kNaWords];
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint64_t* g_noalloc_scratch[kNoAllocMaxDevices];   // device address of `scratch`, per device
+}  // namespace
+
+extern "C" int tms_sample_batch_noalloc(const tms_sample_args* a, hipStream_t stream) {
+    if (!a) return TMS_ERR_INVALID_ARG;
+    if (a->batch > kNoAllocRows || a->vocab > kNoAllocVocab) return TMS_ERR_CAPACITY;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return TMS_ERR_NO_DEVICE;
+    if (dev < 0 || dev >= kNoAllocMaxDevices) return TMS_ERR_NO_DEVICE;
+    uint64_t* base;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        if (!g_noalloc_scratch[dev]) {
+            void* p = nullptr;
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TMS_ERR_HIP;
+            uint64_t* q = (uint64_t*)p;
+            // the all-ones row, once (synchronous: before any launch uses it)
+            if (hipMemset(q + kNaOnes, 0xFF, kNoAllocVocab / 8) != hipSuccess) return TMS_ERR_HIP;
+            if (hipDeviceSynchronize() != hipSuccess) return TMS_ERR_HIP;
+            g_noalloc_scratch[dev] = q;
+        }
+        base = g_noalloc_scratch[dev];
+    }
+    SampleWs w;
+    w.max_batch = kNoAllocRows;
+    w.max_vocab = kNoAllocVocab;
+    w.counters = (uint32_t*)(base + kNaCounters);
+    w.ones = (uint32_t*)(base + kNaOnes);
+    w.lists = base + kNaLists;
+    w.tlists = base + kNaTlists;
+    w.dqueue = (uint32_t*)(base + kNaQueue);
+    w.dense = base + kNaDense;
+    w.dense_slots = 1;
+    return sample_launch(w, a, stream);
 }

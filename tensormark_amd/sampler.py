@@ -35,6 +35,7 @@ EXPORTS = (
     "tms_destroy",
     "tms_workspace_bytes",
     "tms_sample_batch",
+    "tms_sample_batch_noalloc",
     "tms_spec_verify",
     "tms_debug_philox",
     "tms_debug_exp",
@@ -165,6 +166,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         lib.tms_destroy.argtypes = [C.c_void_p]
         lib.tms_workspace_bytes.argtypes = [C.c_void_p]
         lib.tms_sample_batch.argtypes = [C.c_void_p, C.POINTER(SampleArgs), C.c_void_p]
+        lib.tms_sample_batch_noalloc.argtypes = [C.POINTER(SampleArgs), C.c_void_p]
         lib.tms_spec_verify.argtypes = [C.c_void_p, C.POINTER(SpecArgs), C.c_void_p]
         lib.tms_debug_philox.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
         lib.tms_debug_exp.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
@@ -266,14 +268,16 @@ class Sampler:
         return self.torch.from_numpy(raw.copy()).to(f"cuda:{self.device}")
 
     def sample(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
-               topk_cap: int = 0, out=None, stream=None, row_kinds=None):
+               topk_cap: int = 0, out=None, stream=None, row_kinds=None, noalloc=False):
         """Sample one token per row of ``logits`` ([B, V] fp32/fp16/bf16, cuda).
 
         ``params`` is a device uint8 tensor from params_tensor() (or a numpy
         ROW_DTYPE array, uploaded here).  ``row_kinds`` is the hint of
         tms_sample_args (ROWS_ANY / ROWS_TOPK); by default it is derived from
         numpy params (ROWS_ANY for device params), and a Sampler created with
-        kernel="general" always passes ROWS_ANY.  Returns a dict of device
+        kernel="general" always passes ROWS_ANY.  ``noalloc`` takes the
+        context-free entry point tms_sample_batch_noalloc (its static
+        workspace) instead of this context's.  Returns a dict of device
         tensors: tokens, status, keep, and topk_ids/topk_probs when
         topk_cap > 0.
         """
@@ -298,8 +302,12 @@ class Sampler:
         a = self.make_args(logits, params, recent=recent, n_recent=n_recent, mask=mask,
                            draws=draws, topk_cap=topk_cap, out=out, row_kinds=row_kinds)
         s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
-        _check(self.lib.tms_sample_batch(self.handle, C.byref(a), C.c_void_p(s)),
-               "tms_sample_batch")
+        if noalloc:
+            _check(self.lib.tms_sample_batch_noalloc(C.byref(a), C.c_void_p(s)),
+                   "tms_sample_batch_noalloc")
+        else:
+            _check(self.lib.tms_sample_batch(self.handle, C.byref(a), C.c_void_p(s)),
+                   "tms_sample_batch")
         return out
 
     def make_args(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
