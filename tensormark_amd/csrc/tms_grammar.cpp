@@ -97,11 +97,11 @@ uint32_t decode_source(std::string_view s, size_t& i) {
     if ((c0 & 0xE0) == 0xC0) { need = 1; v = c0 & 0x1Fu; }
     else if ((c0 & 0xF0) == 0xE0) { need = 2; v = c0 & 0x0Fu; }
     else if ((c0 & 0xF8) == 0xF0) { need = 3; v = c0 & 0x07u; }
-    else throw std::runtime_error("gbnf: invalid UTF-8 in grammar");
+    else throw std::runtime_error("gbnf: lexer error at byte " + std::to_string(i) + ": not a UTF-8 lead byte");
     ++i;
     for (int k = 0; k < need; ++k, ++i) {
         if (i >= s.size() || ((unsigned char)s[i] & 0xC0) != 0x80)
-            throw std::runtime_error("gbnf: truncated UTF-8 in grammar");
+            throw std::runtime_error("gbnf: lexer error at byte " + std::to_string(i) + ": UTF-8 sequence cut short");
         v = (v << 6) | ((unsigned char)s[i] & 0x3Fu);
     }
     return v;
@@ -144,185 +144,255 @@ struct RuleDef {
     std::vector<Seq> alts;
 };
 
-class Reader {
-public:
-    explicit Reader(std::string_view src) : s_(src) {}
+// ------------------------------------------------------------------ front end
+//
+// Two stages.  The lexer turns the source into a flat token list (literal
+// and class contents already decoded to codepoints), so every question the
+// parser asks is a look at the next one or two tokens.  The parser is a
+// loop over that list with an explicit stack of open groups: each frame
+// holds the alternatives finished so far and the sequence being built; `(`
+// pushes a frame, `)` pops one into a synthetic rule, `|` closes a
+// sequence, and a rule name followed by `::=` at depth 0 starts the next
+// rule.  Errors are "gbnf: <stage> error at byte N: <what>".
 
-    // rules in source order, then the groups in creation order
-    std::vector<RuleDef> read_all() {
-        std::vector<RuleDef> out;
+enum class Tk : uint8_t { Name, Define, Literal, Class, Dot, Open, Close, Bar, Star, Plus, Quest, Count, End };
+
+struct Token {
+    Tk kind;
+    size_t at;                   // byte offset in the source
+    std::string text;            // Name: the name; Literal: UTF-8 of the decoded codepoints
+    std::vector<Span> spans;     // Class
+    bool negate = false;         // Class
+};
+
+[[noreturn]] void syntax_fail(const char* stage, size_t at, const std::string& what) {
+    throw std::runtime_error(std::string("gbnf: ") + stage + " error at byte " + std::to_string(at) + ": " + what);
+}
+
+class Lexer {
+public:
+    explicit Lexer(std::string_view src) : src_(src) {}
+
+    std::vector<Token> run() {
+        std::vector<Token> out;
         for (;;) {
-            blank();
-            if (i_ >= s_.size()) break;
-            RuleDef r;
-            r.name = name();
-            owner_ = r.name;
-            blank();
-            if (s_.compare(i_, 3, "::=") != 0) error("expected '::='");
-            i_ += 3;
-            r.alts = choice();
-            out.push_back(std::move(r));
+            skip_layout();
+            if (pos_ >= src_.size()) break;
+            out.push_back(next());
         }
-        for (auto& g : groups_) out.push_back(std::move(g));
+        out.push_back(Token{Tk::End, src_.size(), {}, {}, false});
         return out;
     }
 
 private:
-    [[noreturn]] void error(const std::string& m) const {
-        throw std::runtime_error("gbnf: " + m + " at offset " + std::to_string(i_));
-    }
-    char cur() const { return i_ < s_.size() ? s_[i_] : '\0'; }
-    void blank() {
-        while (i_ < s_.size()) {
-            if (std::isspace((unsigned char)s_[i_])) { ++i_; continue; }
-            if (s_[i_] == '#') {
-                while (i_ < s_.size() && s_[i_] != '\n') ++i_;
-                continue;
+    static bool is_name_head(char c) { return (c >= 'a' && c <= 'z') || (c >= 'A' && c <= 'Z') || c == '_'; }
+    static bool is_name_body(char c) { return is_name_head(c) || (c >= '0' && c <= '9') || c == '-'; }
+
+    void skip_layout() {   // whitespace and # comments
+        while (pos_ < src_.size()) {
+            const char c = src_[pos_];
+            if (c == '#') {
+                const size_t nl = src_.find('\n', pos_);
+                pos_ = nl == std::string_view::npos ? src_.size() : nl;
+            } else if (std::isspace((unsigned char)c)) {
+                ++pos_;
+            } else {
+                return;
             }
-            break;
         }
-    }
-    static bool name_start(char c) { return std::isalpha((unsigned char)c) || c == '_'; }
-    static bool name_char(char c) { return std::isalnum((unsigned char)c) || c == '_' || c == '-'; }
-    std::string name() {
-        blank();
-        if (i_ >= s_.size() || !name_start(s_[i_])) error("expected a rule name");
-        const size_t b = i_;
-        while (i_ < s_.size() && name_char(s_[i_])) ++i_;
-        return std::string(s_.substr(b, i_ - b));
-    }
-    // `name ::=` ahead (nothing consumed)
-    bool rule_ahead() {
-        const size_t keep = i_;
-        blank();
-        bool yes = false;
-        if (i_ < s_.size() && name_start(s_[i_])) {
-            while (i_ < s_.size() && name_char(s_[i_])) ++i_;
-            blank();
-            yes = s_.compare(i_, 3, "::=") == 0;
-        }
-        i_ = keep;
-        return yes;
-    }
-    uint32_t escaped() {
-        const char c = s_[i_++];
-        switch (c) {
-            case 'n': return '\n';
-            case 'r': return '\r';
-            case 't': return '\t';
-            case '0': return 0;
-            case 'x':
-            case 'u': {
-                const int digits = c == 'x' ? 2 : 4;
-                if (i_ + (size_t)digits > s_.size()) error("short hex escape");
-                uint32_t v = 0;
-                for (int k = 0; k < digits; ++k) {
-                    const char h = s_[i_++];
-                    int d;
-                    if (h >= '0' && h <= '9') d = h - '0';
-                    else if (h >= 'a' && h <= 'f') d = h - 'a' + 10;
-                    else if (h >= 'A' && h <= 'F') d = h - 'A' + 10;
-                    else error("bad hex digit");
-                    v = v * 16 + (uint32_t)d;
-                }
-                return v;
-            }
-            default: return (uint32_t)(unsigned char)c;   // \\ \" \' \[ \] and any other
-        }
-    }
-    uint32_t one_char() {
-        if (s_[i_] == '\\') {
-            ++i_;
-            return escaped();
-        }
-        return decode_source(s_, i_);
-    }
-    std::vector<Seq> choice() {
-        std::vector<Seq> alts;
-        alts.push_back(sequence());
-        for (;;) {
-            blank();
-            if (cur() != '|') break;
-            ++i_;
-            alts.push_back(sequence());
-        }
-        return alts;
-    }
-    Seq sequence() {
-        Seq seq;
-        for (;;) {
-            blank();
-            const char c = cur();
-            if (c == '\0' || c == '|' || c == ')' || rule_ahead()) break;
-            Term t = primary();
-            blank();
-            const char r = cur();
-            if (r == '*' || r == '+' || r == '?') {
-                t.rep = r;
-                ++i_;
-            } else if (r == '{') {
-                error("counted repetition {m,n} is not supported");
-            }
-            seq.push_back(std::move(t));
-        }
-        return seq;
-    }
-    Term primary() {
-        blank();
-        Term t;
-        const char c = cur();
-        if (c == '"') {
-            ++i_;
-            t.kind = Term::Lit;
-            while (i_ < s_.size() && s_[i_] != '"') encode_utf8(one_char(), t.text);
-            if (i_ >= s_.size()) error("unterminated literal");
-            ++i_;
-        } else if (c == '[') {
-            ++i_;
-            t.kind = Term::Set;
-            if (cur() == '^') {
-                t.negate = true;
-                ++i_;
-            }
-            while (i_ < s_.size() && s_[i_] != ']') {
-                const uint32_t lo = one_char();
-                uint32_t hi = lo;
-                if (cur() == '-' && i_ + 1 < s_.size() && s_[i_ + 1] != ']') {
-                    ++i_;
-                    hi = one_char();
-                }
-                if (hi < lo) error("inverted range in character class");
-                t.spans.push_back(Span{lo, hi});
-            }
-            if (i_ >= s_.size()) error("unterminated character class");
-            ++i_;
-        } else if (c == '(') {
-            ++i_;
-            RuleDef g;
-            g.name = "group:" + owner_ + ":" + std::to_string(n_groups_++);
-            g.alts = choice();
-            blank();
-            if (cur() != ')') error("expected ')'");
-            ++i_;
-            t.kind = Term::Rule;
-            t.name = g.name;
-            groups_.push_back(std::move(g));
-        } else if (c == '.') {
-            ++i_;
-            t.kind = Term::Any;
-        } else {
-            t.kind = Term::Rule;
-            t.name = name();
-        }
-        return t;
     }
 
-    std::string_view s_;
-    size_t i_ = 0;
-    std::string owner_;
-    int n_groups_ = 0;
-    std::vector<RuleDef> groups_;
+    static int hex_value(char h) {
+        if (h >= '0' && h <= '9') return h - '0';
+        const char l = (char)(h | 0x20);
+        return (l >= 'a' && l <= 'f') ? l - 'a' + 10 : -1;
+    }
+
+    // One codepoint of a literal or class body: an escape or a UTF-8 sequence.
+    uint32_t body_codepoint() {
+        if (src_[pos_] != '\\') return decode_source(src_, pos_);
+        const size_t esc = pos_++;
+        if (pos_ >= src_.size()) syntax_fail("lexer", esc, "backslash at the end of the grammar");
+        const char c = src_[pos_++];
+        static const struct { char key; uint32_t cp; } simple[] = {{'n', '\n'}, {'r', '\r'}, {'t', '\t'}, {'0', 0}};
+        for (const auto& e : simple)
+            if (e.key == c) return e.cp;
+        if (c != 'x' && c != 'u') return (uint32_t)(unsigned char)c;   // \\ \" \' \[ \] and the rest: the character
+        const size_t width = c == 'x' ? 2 : 4;
+        if (src_.size() - pos_ < width) syntax_fail("lexer", esc, "hex escape cut short");
+        uint32_t cp = 0;
+        for (size_t k = 0; k < width; ++k) {
+            const int d = hex_value(src_[pos_ + k]);
+            if (d < 0) syntax_fail("lexer", pos_ + k, "not a hex digit in an escape");
+            cp = cp * 16 + (uint32_t)d;
+        }
+        pos_ += width;
+        return cp;
+    }
+
+    Token next() {
+        const size_t at = pos_;
+        const char c = src_[pos_];
+        Token t{Tk::End, at, {}, {}, false};
+        static const struct { char ch; Tk kind; } single[] = {
+            {'.', Tk::Dot}, {'(', Tk::Open}, {')', Tk::Close}, {'|', Tk::Bar},
+            {'*', Tk::Star}, {'+', Tk::Plus}, {'?', Tk::Quest}};
+        for (const auto& e : single)
+            if (e.ch == c) {
+                ++pos_;
+                t.kind = e.kind;
+                return t;
+            }
+        if (c == '{') {   // {m,n}: one token, which the parser rejects
+            const size_t close = src_.find('}', pos_);
+            pos_ = close == std::string_view::npos ? src_.size() : close + 1;
+            t.kind = Tk::Count;
+            return t;
+        }
+        if (src_.compare(pos_, 3, "::=") == 0) {
+            pos_ += 3;
+            t.kind = Tk::Define;
+            return t;
+        }
+        if (is_name_head(c)) {
+            while (pos_ < src_.size() && is_name_body(src_[pos_])) ++pos_;
+            t.kind = Tk::Name;
+            t.text.assign(src_.substr(at, pos_ - at));
+            return t;
+        }
+        if (c == '"') {
+            ++pos_;
+            t.kind = Tk::Literal;
+            while (pos_ < src_.size() && src_[pos_] != '"') encode_utf8(body_codepoint(), t.text);
+            if (pos_ >= src_.size()) syntax_fail("lexer", at, "string literal never closed");
+            ++pos_;
+            return t;
+        }
+        if (c == '[') {
+            ++pos_;
+            t.kind = Tk::Class;
+            if (pos_ < src_.size() && src_[pos_] == '^') {
+                t.negate = true;
+                ++pos_;
+            }
+            while (pos_ < src_.size() && src_[pos_] != ']') {
+                const size_t item = pos_;
+                Span sp;
+                sp.lo = sp.hi = body_codepoint();
+                // `a-z` is a range unless the '-' is the class's last character
+                if (pos_ + 1 < src_.size() && src_[pos_] == '-' && src_[pos_ + 1] != ']') {
+                    ++pos_;
+                    sp.hi = body_codepoint();
+                }
+                if (sp.hi < sp.lo) syntax_fail("lexer", item, "character range runs backwards");
+                t.spans.push_back(sp);
+            }
+            if (pos_ >= src_.size()) syntax_fail("lexer", at, "character class never closed");
+            ++pos_;
+            return t;
+        }
+        syntax_fail("lexer", at, std::string("unexpected character '") + c + "'");
+    }
+
+    std::string_view src_;
+    size_t pos_ = 0;
 };
+
+// Rules in source order, then the synthetic group rules in the order their
+// ')' closed them.
+std::vector<RuleDef> parse_grammar(std::string_view src) {
+    const std::vector<Token> toks = Lexer(src).run();
+    struct Frame {
+        std::vector<Seq> alts;
+        Seq seq;
+        size_t opened_at;
+    };
+    std::vector<RuleDef> rules, groups;
+    std::vector<Frame> open;   // open[0]: the rule body; open[d]: group at depth d
+    std::vector<int> group_serial;   // per rule: groups named so far
+    auto starts_rule = [&](size_t i) { return toks[i].kind == Tk::Name && toks[i + 1].kind == Tk::Define; };
+    auto finish_rule = [&]() {
+        Frame& f = open.back();
+        f.alts.push_back(std::move(f.seq));
+        rules.back().alts = std::move(f.alts);
+        open.clear();
+    };
+    size_t i = 0;
+    for (;;) {
+        const Token& tk = toks[i];
+        if (tk.kind == Tk::End || starts_rule(i)) {
+            if (open.size() > 1) syntax_fail("parser", open.back().opened_at, "'(' is never closed");
+            if (!open.empty()) finish_rule();
+            if (tk.kind == Tk::End) break;
+            RuleDef r;
+            r.name = tk.text;
+            rules.push_back(std::move(r));
+            group_serial.push_back(0);
+            open.push_back(Frame{{}, {}, tk.at});
+            i += 2;
+            continue;
+        }
+        if (open.empty()) syntax_fail("parser", tk.at, "expected a rule: a name followed by '::='");
+        Frame& f = open.back();
+        switch (tk.kind) {
+            case Tk::Bar:
+                f.alts.push_back(std::move(f.seq));
+                f.seq.clear();
+                break;
+            case Tk::Open:
+                open.push_back(Frame{{}, {}, tk.at});
+                break;
+            case Tk::Close: {
+                if (open.size() == 1) syntax_fail("parser", tk.at, "')' without a matching '('");
+                RuleDef g;
+                g.name = "(" + rules.back().name + ")#" + std::to_string(group_serial.back()++);
+                f.alts.push_back(std::move(f.seq));
+                g.alts = std::move(f.alts);
+                open.pop_back();
+                Term ref;
+                ref.kind = Term::Rule;
+                ref.name = g.name;
+                open.back().seq.push_back(std::move(ref));
+                groups.push_back(std::move(g));
+                break;
+            }
+            case Tk::Star:
+            case Tk::Plus:
+            case Tk::Quest: {
+                if (f.seq.empty()) syntax_fail("parser", tk.at, "repetition operator with nothing before it");
+                Term& last = f.seq.back();
+                if (last.rep) syntax_fail("parser", tk.at, "two repetition operators in a row");
+                last.rep = tk.kind == Tk::Star ? '*' : (tk.kind == Tk::Plus ? '+' : '?');
+                break;
+            }
+            case Tk::Count:
+                syntax_fail("parser", tk.at, "counted repetition {m,n} is not part of this grammar language");
+            case Tk::Define:
+                syntax_fail("parser", tk.at, "'::=' without a rule name before it");
+            default: {   // an atom
+                Term t;
+                if (tk.kind == Tk::Literal) {
+                    t.kind = Term::Lit;
+                    t.text = tk.text;
+                } else if (tk.kind == Tk::Class) {
+                    t.kind = Term::Set;
+                    t.spans = tk.spans;
+                    t.negate = tk.negate;
+                } else if (tk.kind == Tk::Dot) {
+                    t.kind = Term::Any;
+                } else {
+                    t.kind = Term::Rule;
+                    t.name = tk.text;
+                }
+                f.seq.push_back(std::move(t));
+                break;
+            }
+        }
+        ++i;
+    }
+    for (RuleDef& g : groups) rules.push_back(std::move(g));
+    return rules;
+}
 
 // ------------------------------------------------------------------ automaton
 
@@ -396,15 +466,14 @@ struct StateHash {
 class Machine {
 public:
     explicit Machine(std::string_view src) {
-        Reader rd(src);
-        rules_ = rd.read_all();
+        rules_ = parse_grammar(src);
         std::unordered_map<std::string, int> index;
         for (size_t r = 0; r < rules_.size(); ++r) {
             if (!index.emplace(rules_[r].name, (int)r).second)
-                throw std::runtime_error("gbnf: duplicate rule '" + rules_[r].name + "'");
+                throw std::runtime_error("gbnf: rule error: '" + rules_[r].name + "' is defined twice");
         }
         auto root = index.find("root");
-        if (root == index.end()) throw std::runtime_error("gbnf: no 'root' rule");
+        if (root == index.end()) throw std::runtime_error("gbnf: rule error: the grammar defines no 'root' rule");
         root_ = root->second;
         for (RuleDef& r : rules_)
             for (Seq& a : r.alts)
@@ -412,7 +481,7 @@ public:
                     if (t.kind == Term::Rule) {
                         auto it = index.find(t.name);
                         if (it == index.end())
-                            throw std::runtime_error("gbnf: unknown rule '" + t.name + "'");
+                            throw std::runtime_error("gbnf: rule error: '" + t.name + "' is used but never defined");
                         t.rule = it->second;
                     }
         assemble();

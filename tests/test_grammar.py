@@ -78,7 +78,9 @@ def test_byte_at_a_time_utf8():
 
 @pytest.mark.parametrize("text", [
     'thing ::= "a"', "root ::= missing", 'root ::= "a"\nroot ::= "b"', "root ::= [0-9]{4}",
-    'root ::= "unterminated', "root ::= [abc"])
+    'root ::= "unterminated', "root ::= [abc", 'root ::= ("a"', 'root ::= "a")', "root ::= *",
+    'root ::= "a"**', '::= "a"', "root ::= [z-a]", 'root ::= "\\x4"', "root ::= @",
+    'root ::= ( "a" x ::= "b" )'])
 def test_parse_errors(text):
     with pytest.raises(GrammarError, match="gbnf:"):
         Grammar.parse(text)
