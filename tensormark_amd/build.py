@@ -5,6 +5,7 @@ Usage: python -m tensormark_amd.build   (or tensormark_amd.build.build())
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -13,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtmsample_hip.so")
-SOURCES = ["tms_sample.hip", "tms_topk.hip", "tms_dense.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp"]
+SOURCES = ["tms_sample.hip", "tms_topk.hip", "tms_wide.hip", "tms_dense.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp"]
 
 # -ffp-contract=off keeps every a*b+c as two rounded operations, so the
 # device arithmetic matches the host checker bit for bit.  Packed-FP32 ops
@@ -31,12 +32,13 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
 ]
 
-# Per-file flags.  The top-k kernel takes its row ticket as soon as its
-# stream is in and uses the result only after publishing; the atomic
+# Per-file flags.  The top-k kernels take their row ticket as soon as the
+# stream is in and use the result only after publishing; the atomic
 # optimizer would rewrite that single-lane atomic into a wave-wide one whose
 # result is broadcast at once, waiting out the round trip there.
 FILE_FLAGS = {
     "tms_topk.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+    "tms_wide.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 
 BUILD_DIR = os.path.join(HERE, "_build")
@@ -47,13 +49,28 @@ def hipcc() -> str:
     return os.path.join(rocm, "bin", "hipcc")
 
 
-def _run(cmd: list, verbose: bool) -> None:
+def _run(cmd: list, verbose: bool) -> str:
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("hipcc failed building libtmsample_hip.so: " + " ".join(cmd))
+    return r.stderr
+
+
+# Files whose kernels must not use scratch memory: they run at two
+# 1024-thread workgroups per CU (64 VGPRs), and a build of the wide kernel
+# that spilled to scratch under that limit sampled wrong tokens on the GPU.
+NO_SCRATCH = ("tms_wide.hip",)
+
+
+def _check_no_scratch(src: str, remarks: str) -> None:
+    sizes = re.findall(r"ScratchSize \[bytes/lane\]: (\d+)", remarks)
+    if not sizes:
+        raise RuntimeError(f"{src}: no kernel resource report from hipcc")
+    if any(int(x) for x in sizes):
+        raise RuntimeError(f"{src}: a kernel uses scratch memory ({sizes}); it must fit its register limit")
 
 
 def build(verbose: bool = False) -> str:
@@ -63,12 +80,16 @@ def build(verbose: bool = False) -> str:
     jobs = []
     for src in SOURCES:
         obj = os.path.join(BUILD_DIR, src + ".o")
-        jobs.append((obj, [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), *inc, "-c", "-o", obj,
-                           os.path.join(CSRC, src)]))
+        extra = ["-Rpass-analysis=kernel-resource-usage"] if src in NO_SCRATCH else []
+        jobs.append((src, obj, [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), *inc, *extra, "-c", "-o",
+                                obj, os.path.join(CSRC, src)]))
     workers = min(len(jobs), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with ThreadPoolExecutor(max_workers=workers) as ex:
-        list(ex.map(lambda j: _run(j[1], verbose), jobs))
-    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB + ".tmp", *[j[0] for j in jobs]], verbose)
+        remarks = list(ex.map(lambda j: _run(j[2], verbose), jobs))
+    for (src, _, _), rem in zip(jobs, remarks):
+        if src in NO_SCRATCH:
+            _check_no_scratch(src, rem)
+    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB + ".tmp", *[j[1] for j in jobs]], verbose)
     os.replace(LIB + ".tmp", LIB)
     return LIB
 

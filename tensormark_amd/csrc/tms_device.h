@@ -374,6 +374,7 @@ struct Elt;
 template <>
 struct Elt<float> {
     static constexpr int kVec = 4;
+    static constexpr uint32_t kNegInfWord = 0xFF800000u;   // -inf in each element of a word
     __device__ static void widen(const uint4& q, float (&f)[4]) {
         f[0] = __uint_as_float(q.x);
         f[1] = __uint_as_float(q.y);
@@ -385,6 +386,7 @@ struct Elt<float> {
 template <>
 struct Elt<_Float16> {
     static constexpr int kVec = 8;
+    static constexpr uint32_t kNegInfWord = 0xFC00FC00u;
     __device__ static float h2f(uint32_t h) {
         _Float16 v;
         const uint16_t b = (uint16_t)h;
@@ -404,6 +406,7 @@ struct Elt<_Float16> {
 template <>
 struct Elt<Bf16> {
     static constexpr int kVec = 8;
+    static constexpr uint32_t kNegInfWord = 0xFF80FF80u;
     __device__ static void widen(const uint4& q, float (&f)[8]) {
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll

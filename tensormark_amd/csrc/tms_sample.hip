@@ -37,6 +37,7 @@
 // wait for the headers is bounded.
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "tms_dense.h"
@@ -1051,6 +1052,20 @@ extern "C" size_t tms_workspace_bytes(const tms_context* ctx) {
     return ctx ? ctx->bytes + ctx->dense_bytes : 0;
 }
 
+// Compute units of the current device (looked up once per device).
+static int device_cus() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cus[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 // The workspace regions one sampling call uses, and their capacities.
 struct SampleWs {
     int max_batch, max_vocab;
@@ -1119,6 +1134,26 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
 #ifdef TMS_TRACE
     k.trace = g_tms_trace_host;
 #endif
+    if (a->row_kinds == TMS_ROWS_TOPK && (!a->recent || a->recent_stride <= tms::kWideMaxWindow)) {
+        // Every row greedy or top-k <= 128 (the caller's promise): the wide
+        // top-k kernel, S chunks of at most 4096 16-byte vectors, CE a
+        // multiple of 32 so each chunk starts on a mask word, when the grid
+        // is resident at once (two 1024-thread workgroups per CU).  A grid
+        // that runs in several rounds keeps each workgroup (16 waves) through
+        // its serial tail; there the general kernel is faster (B = 1024,
+        // V = 256000 bf16: 336 us against 234 us).
+        const int cap = tms::kWideChunkVecs * vec;
+        const int s_w = (a->vocab + cap - 1) / cap;
+        const int per_w = (a->vocab + s_w - 1) / s_w;
+        const int ce = (per_w + 31) / 32 * 32;
+        if (s_w <= tms::kWideMaxChunksHost && ce <= cap && a->batch * s_w <= 2 * device_cus()) {
+            tms::KArgs kw = k;
+            kw.CE = ce;
+            kw.S = (a->vocab + ce - 1) / ce;
+            kw.dense = nullptr;   // rows that break the promise report TMS_ROW_UNSUPPORTED
+            return tms_launch_wide(kw, a->dtype, fast, a->batch, stream);
+        }
+    }
     if (a->row_kinds == TMS_ROWS_TOPK) {
         // Every row greedy or top-k <= 128 (the caller's promise): the top-k
         // kernel, with chunks of CE ids, CE a multiple of 32 so each chunk

@@ -44,6 +44,9 @@ constexpr int kUni = 2048;                 // merge staging (u64)
 constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
 constexpr int kLeanMaxChunksHost = 16;     // chunks per row of the top-k kernel (vocab <= 262,144)
+constexpr int kWideMaxChunksHost = 16;     // chunks per row of the wide top-k kernel
+constexpr int kWideChunkVecs = 4096;       // 16-byte vectors per chunk of the wide kernel
+constexpr int kWideMaxWindow = 1024;       // history positions the wide kernel holds (one per thread)
 constexpr int kTopkListStride = 1280;      // u64 per (row, chunk) list of the top-k kernel
 constexpr int kTopkMaxGrid = 1024;         // workgroups of a top-k launch (2 per CU resident)
 constexpr int kRankLists = 16;             // most chunk lists the sampled merge reads in one round
@@ -418,11 +421,13 @@ __device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, int r, co
     }
 }
 
-// Sixteen doubles from LDS (16-byte reads; v + i 16-byte aligned).
-__device__ __forceinline__ void ld16(const double* v, int i, double (&c)[16]) {
+// Eight doubles from LDS (16-byte reads; v + i 16-byte aligned).  Blocks of
+// eight keep the sequential sums within the register budget of kernels that
+// run two 1024-thread workgroups per CU.
+__device__ __forceinline__ void ld8(const double* v, int i, double (&c)[8]) {
     const double2* v2 = (const double2*)(v + i);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 4; ++u) {
         const double2 d = v2[u];
         c[2 * u] = d.x;
         c[2 * u + 1] = d.y;
@@ -435,18 +440,18 @@ __device__ __forceinline__ void ld16(const double* v, int i, double (&c)[16]) {
 // returns the total.
 __device__ __forceinline__ double seq_prefix_sums(const double* v, int n, double* pre) {
     double s = 0.0;
-    for (int i = 0; i < n; i += 16) {
-        double c[16];
-        ld16(v, i, c);
+    for (int i = 0; i < n; i += 8) {
+        double c[8];
+        ld8(v, i, c);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
+        for (int e = 0; e < 8; ++e) {
             s += c[e];
             c[e] = s;
         }
         if ((threadIdx.x & 63) == 0) {
             double2* p2 = (double2*)(pre + i);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) p2[u] = make_double2(c[2 * u], c[2 * u + 1]);
+            for (int u = 0; u < 4; ++u) p2[u] = make_double2(c[2 * u], c[2 * u + 1]);
         }
     }
     return s;
@@ -454,22 +459,22 @@ __device__ __forceinline__ double seq_prefix_sums(const double* v, int n, double
 
 // First i in [0, n) whose left-to-right prefix sum v[0] + ... + v[i] is >=
 // thr, or n (v >= 0 and zero-padded as above, so the prefixes never
-// decrease).  Sixteen prefixes at a time stay in registers; the chain stops
+// decrease).  Eight prefixes at a time stay in registers; the chain stops
 // at the block that crosses.
 __device__ __forceinline__ int first_prefix_ge(const double* v, int n, double thr) {
     double s = 0.0;
-    for (int i = 0; i < n; i += 16) {
-        double c[16];
-        ld16(v, i, c);
+    for (int i = 0; i < n; i += 8) {
+        double c[8];
+        ld8(v, i, c);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
+        for (int e = 0; e < 8; ++e) {
             s += c[e];
             c[e] = s;
         }
         if (s >= thr) {
             int below = 0;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) below += c[e] < thr ? 1 : 0;
+            for (int e = 0; e < 8; ++e) below += c[e] < thr ? 1 : 0;
             return i + below;
         }
     }
@@ -836,5 +841,7 @@ __device__ bool tail_topp_fast(const KArgs& a, int row, const tms_row_params& P,
 
 // Launches the top-k kernel (tms_topk.hip) over `batch` rows.
 int tms_launch_topk(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
+// Launches the wide top-k kernel (tms_wide.hip) over `batch` rows.
+int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
 // Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.
 int tms_launch_dense(const tms::KArgs& k, int dtype, int workgroups, hipStream_t stream);

@@ -1,0 +1,953 @@
+// tms_wide.hip -- the sampler kernel for batches whose rows are all greedy or
+// top-k with k <= 128 (the host picks it from the caller's row-kind hint),
+// with 1024-thread workgroups.
+//
+// One launch per call.  Row b is cut into S <= 16 chunks; workgroup (b, c)
+// streams chunk c once: 1024 threads x 4 nontemporal 16-byte loads each, so a
+// CU holds two workgroups (32 waves) and keeps enough bytes in flight to run
+// the stream near the HBM rate (a bare stream of 33 MB measured 8.7 us with
+// 512 x 256-thread workgroups and 5.9 us with 512 x 1024).
+//
+//   window    while the stream is in flight: the row's history ids that fall
+//             in the chunk are set in an LDS bitmap and listed; the first
+//             position holding an id owns it, counts its occurrences and
+//             loads its logit and mask bit (tmsample.h:52-63 compounding,
+//             then frequency/presence).  The stream leaves those ids out; the
+//             owners bring them back penalised.
+//   pass 1    per 16-byte slot: mask bit (and not a window id) -> value,
+//             else -inf; the thread's maximum; NaN / +inf flagged.
+//   bound     each wave takes its 8 (or fewer) largest thread maxima; the
+//             K-th largest of those 16 lists bounds the chunk's K-th value
+//             from below (K thread maxima, each a distinct entry, reach it).
+//   select    every entry whose v / T can reach the bound's quotient is a
+//             candidate (the division runs on candidates only); candidates
+//             are ranked by counting, and the chunk's sorted top min(n, K)
+//             keys (v / T, then lowest id) are published.  A chunk with more
+//             than 1024 candidates (massive ties) takes an exact radix select
+//             over the keys instead.
+//   merge     the last chunk of the row to take a ticket reads the other
+//             lists (a word still in flight reads 0 and is read again; the
+//             merger returns every word it read to 0), ranks each key by its
+//             position in its own list plus binary searches in the others,
+//             and runs the fp64 tail of tmsample::sample
+//             (tensormark/tmsample.h:184-199) on one wave.
+#include "tms_sample_common.h"
+
+namespace tms {
+namespace wide {
+
+constexpr int kT = 1024;            // threads per workgroup
+constexpr int kW = kT / 64;         // waves per workgroup
+constexpr int kSlots = 4;           // 16-byte slots per thread
+constexpr int kMaxS = kWideMaxChunksHost;
+constexpr int kKMax = kTopkFast;    // largest K
+constexpr int kLStride = 136;       // u64 per (row, chunk) list: header + kKMax keys, padded
+constexpr int kHash = 2048;         // window table slots (at most 1024 ids: half full)
+constexpr int kCntBits = 11;        // occurrence count bits of a table word (<= 1024)
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+constexpr int kHot = 8;             // lanes a wave examines from LDS (more: every entry in place)
+constexpr int kCap = 1024;          // chunk candidates held in LDS
+constexpr int kPad = 256;           // zero keys after a ranked list (rank_place reads past it)
+static_assert(kMaxS <= kW, "the merger reads one list per wave");
+static_assert(kLStride >= 1 + kKMax, "list layout");
+
+// Header word: ready bit, flags (bits 48-55), list length (bits 32-47).
+__device__ __forceinline__ uint64_t header(int flags, int n) {
+    return kReady | ((uint64_t)(flags & 0xFF) << 48) | ((uint64_t)(n & 0xFFFF) << 32);
+}
+__device__ __forceinline__ int hdr_n(uint64_t h) { return (int)((h >> 32) & 0xFFFF); }
+__device__ __forceinline__ int hdr_flags(uint64_t h) { return (int)((h >> 48) & 0xFF); }
+
+// First table slot of a chunk offset (multiplicative hash, 11 bits).
+__device__ __forceinline__ int hash_slot(uint32_t off) { return (int)((off * 0x9E3779B1u) >> 21); }
+
+// Read in place of the caller's draws and history when there are none
+// (never written), so those loads need no branch.
+__device__ uint32_t kNoDraws[2] = {0u, 0u};
+__device__ int32_t kNoHistory[1] = {-1};
+
+struct Smem {
+    uint32_t wbits[kT];             // window ids of the chunk, one bit per id (<= 32768 ids)
+    uint32_t wtab[kHash];           // window ids: chunk offset << kCntBits | occurrences, or kEmpty
+    float wval[kHash];              // each window id's masked value
+    alignas(16) union {
+        struct {
+            uint64_t cand[kCap + kPad];     // the chunk's candidates: value bits << 32 | id, then keys
+        } c;
+        uint64_t surv[kMaxS * kKMax + kPad];   // merge: the keys that can place
+        struct {
+            double pr[4 * kKMax];   // fp64 tail: pr, then the prefixes of z at +256
+            double q[kKMax];
+        } tail;
+    } u;
+    alignas(16) uint64_t slist[kKMax + 8];    // this chunk's sorted top keys
+    alignas(16) uint64_t srt[kKMax + 8];      // the row's sorted top-K
+    alignas(16) uint32_t gmax[kT / 8];        // order keys of the 8-lane group maxima
+    alignas(16) uint4 hot[kW * kHot * kSlots];   // per wave: the words of its hot lanes
+    int hotlane[kW * kHot];                   // per wave: the lane of each hot slot
+    uint32_t tkey;                            // the chunk's bound (order key)
+    float vlo;                                // the least value that can be a candidate
+    alignas(16) uint32_t wnf[kW];             // per wave: a NaN or +inf seen
+    alignas(16) int hist[256];
+    alignas(16) uint64_t mk[kMaxS]; // merge: each list's rm-th key (0 if shorter)
+    alignas(16) int mn[kMaxS];      // merge: list lengths
+    alignas(16) int mf[kMaxS];      // merge: list flags
+    alignas(16) int scnt[kMaxS];    // merge: keys of each list that can place
+    int ncand, lost, onf;
+    uint32_t ticket;
+    uint32_t draw[2];               // the merger's draw words
+    int flags;
+    int misc[4];
+};
+
+#ifdef TMS_WIDE_STOP
+// Timing builds: the kernel ends after phase n, storing a value that depends
+// on that phase's work so none of it is optimised away.
+#define WSTOP(n, val)                                                                   \
+    do {                                                                                \
+        if (TMS_WIDE_STOP == (n)) {                                                     \
+            if ((val) == 12345.678f) a.out_tokens[row] = 1;                             \
+            return;                                                                     \
+        }                                                                               \
+    } while (0)
+#else
+#define WSTOP(n, val) ((void)0)
+#endif
+
+#ifdef TMS_TRACE
+// Trace builds: lane 0 of every wave stamps the 100 MHz real-time counter at
+// phase boundaries, 16 slots per wave.
+#define WTR(i)                                                                          \
+    do {                                                                                \
+        if ((threadIdx.x & 63) == 0 && a.trace)                                         \
+            a.trace[(blockIdx.x * kW + (threadIdx.x >> 6)) * 16 + (i)] =                \
+                __builtin_amdgcn_s_memrealtime();                                       \
+    } while (0)
+#define WTV(i, val)                                                                     \
+    do {                                                                                \
+        if ((threadIdx.x & 63) == 0 && a.trace)                                         \
+            a.trace[(blockIdx.x * kW + (threadIdx.x >> 6)) * 16 + (i)] = (uint64_t)(val); \
+    } while (0)
+#else
+#define WTR(i) ((void)0)
+#define WTV(i, val) ((void)0)
+#endif
+
+// 16-byte nontemporal load: the logits are read exactly once per call.
+__device__ __forceinline__ uint4 ld_nt(const void* p) {
+    typedef unsigned u4v __attribute__((ext_vector_type(4)));
+    const u4v q = __builtin_nontemporal_load((const u4v*)p);
+    return make_uint4(q.x, q.y, q.z, q.w);
+}
+
+// Element e of a 16-byte slot, widened exactly to fp32.
+template <typename T>
+__device__ __forceinline__ float elt(const uint4& q, int e) {
+    if constexpr (sizeof(T) == 4) {
+        return __uint_as_float(e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w);
+    } else {
+        const uint32_t w = (e >> 1) == 0 ? q.x : (e >> 1) == 1 ? q.y : (e >> 1) == 2 ? q.z : q.w;
+        const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+        if constexpr (__is_same(T, Bf16)) return __uint_as_float(h << 16);
+        else return Elt<_Float16>::h2f(h);
+    }
+}
+
+// Reductions over the 64 lanes of a wave by DPP (no LDS round trips):
+// butterflies within 16-lane rows (quad_perm, half-row and row mirrors),
+// then across rows (row_bcast:15 and :31 towards lane 63, read there).
+template <int CTRL, int RM = 0xF>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, RM, 0xF, false);
+}
+constexpr int kQxor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kQxor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kHalfMirror = 0x141;
+constexpr int kMirror = 0x140;
+__device__ __forceinline__ int wave_or_i32(int v) {
+    uint32_t u = (uint32_t)v;
+    u |= dpp_mov<kQxor1>(u);
+    u |= dpp_mov<kQxor2>(u);
+    u |= dpp_mov<kHalfMirror>(u);
+    u |= dpp_mov<kMirror>(u);
+    u |= dpp_u32<0x142, 0xA, false>(0u, u);   // row_bcast:15
+    u |= dpp_u32<0x143, 0xC, false>(0u, u);   // row_bcast:31
+    return __builtin_amdgcn_readlane((int)u, 63);
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+#define TMS_MINSTEP(MOVE)                                                                 \
+    {                                                                                     \
+        const uint64_t w = ((uint64_t)MOVE((uint32_t)(v >> 32)) << 32) | MOVE((uint32_t)v); \
+        v = w < v ? w : v;                                                                \
+    }
+    TMS_MINSTEP(dpp_mov<kQxor1>)
+    TMS_MINSTEP(dpp_mov<kQxor2>)
+    TMS_MINSTEP(dpp_mov<kHalfMirror>)
+    TMS_MINSTEP(dpp_mov<kMirror>)
+#undef TMS_MINSTEP
+    // rows: lanes outside the broadcast keep their own value (old = v)
+    {
+        const uint32_t lo = dpp_u32<0x142, 0xA, false>((uint32_t)v, (uint32_t)v);
+        const uint32_t hi = dpp_u32<0x142, 0xA, false>((uint32_t)(v >> 32), (uint32_t)(v >> 32));
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        v = w < v ? w : v;
+    }
+    {
+        const uint32_t lo = dpp_u32<0x143, 0xC, false>((uint32_t)v, (uint32_t)v);
+        const uint32_t hi = dpp_u32<0x143, 0xC, false>((uint32_t)(v >> 32), (uint32_t)(v >> 32));
+        const uint64_t w = ((uint64_t)hi << 32) | lo;
+        v = w < v ? w : v;
+    }
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+}
+// Sum over each aligned group of P lanes (P a power of two <= 16), every
+// lane of the group receiving it.
+__device__ __forceinline__ int group_sum(int v, int P) {
+    uint32_t u = (uint32_t)v;
+    if (P >= 2) u += dpp_mov<kQxor1>(u);
+    if (P >= 4) u += dpp_mov<kQxor2>(u);
+    if (P >= 8) u += dpp_mov<kHalfMirror>(u);
+    if (P >= 16) u += dpp_mov<kMirror>(u);
+    return (int)u;
+}
+
+// The digit of the 64-bit key radix select: wave 0 finds, among the 256
+// bins of hist (digit values), the one holding the `remaining`-th largest key
+// and how many keys lie in higher bins.
+__device__ __forceinline__ void pick_digit(const int* hist, int remaining, int* out) {
+    const int lane = threadIdx.x & 63;
+    int h[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[i] = hist[255 - (4 * lane + i)];   // lane 0 holds the top bins
+        s += h[i];
+    }
+    int above = wave_incl_scan_i32(s) - s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (above < remaining && above + h[i] >= remaining) {
+            out[0] = 255 - (4 * lane + i);
+            out[1] = above;
+        }
+        above += h[i];
+    }
+}
+
+// Every thread of the workgroup: the keys keys[0..n) (distinct, 16-byte
+// aligned, followed by kPad zero words) whose rank (the number of larger
+// keys) is below K land at out[rank].  P neighbouring lanes share a key,
+// each counting the larger keys in its share of the list, and their counts
+// are summed across the P lanes (DPP): P = kT / n rounded down to a power of
+// two (at most 16), so a short list is ranked in a few steps by every wave
+// instead of n steps by a few.
+__device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, uint64_t* out) {
+    const int t = threadIdx.x;
+    int P = 16;
+    while (P > 1 && P * n > kT) P >>= 1;
+    // lane `part` of a key's P counts the keys [part * L, part * L + L), L
+    // even, in 16-byte reads; P * L <= n + 3P <= n + kPad, and the keys are
+    // zero (below every key) from n on.
+    const int L = ((n + P - 1) / P + 1) & ~1;
+    const int per_pass = kT / P;
+    for (int base = 0; base < n; base += per_pass) {
+        const int i = base + t / P, part = t & (P - 1);
+        const uint64_t k = i < n ? keys[i] : ~0ull;
+        const ulonglong2* c2 = (const ulonglong2*)(keys + part * L);
+        int cnt = 0;
+#pragma unroll 2
+        for (int q = 0; q < (L >> 1); ++q) {
+            const ulonglong2 y = c2[q];
+            cnt += (y.x > k ? 1 : 0) + (y.y > k ? 1 : 0);
+        }
+        cnt = group_sum(cnt, P);
+        if (part == 0 && i < n && cnt < K) out[cnt] = k;
+    }
+}
+
+// One wave: the keys keys[0..n) (distinct, 16-byte aligned, followed by a
+// zero word) whose rank (the number of larger keys) is below K land at
+// out[rank] (and at gout[rank] in memory, with agent-scope stores, when gout
+// is given).  Each lane ranks one key a pass, reading the list in 16-byte
+// broadcast reads.
+__device__ __forceinline__ void rank_wave(const uint64_t* keys, int n, int K, uint64_t* out,
+                                          uint64_t* gout) {
+    const int lane = threadIdx.x & 63;
+    const ulonglong2* c2 = (const ulonglong2*)keys;
+    for (int base = 0; base < n; base += 64) {
+        const int i = base + lane;
+        const uint64_t k = i < n ? keys[i] : ~0ull;
+        int cnt = 0;
+#pragma unroll 2
+        for (int q = 0; q < (n + 1) >> 1; ++q) {
+            const ulonglong2 y = c2[q];
+            cnt += (y.x > k ? 1 : 0) + (y.y > k ? 1 : 0);
+        }
+        if (i < n && cnt < K) {
+            out[cnt] = k;
+            if (gout) st_agent(&gout[cnt], k);
+        }
+    }
+}
+
+// The exact top-K keys of a chunk whose bound admits more than kCap
+// candidates (massive ties): a radix select over the 64-bit keys (v / T,
+// then lowest id), 8 bits a pass, with the chunk read again from memory
+// (mask bit, window ids left to their owners, whose values come in as
+// arguments).  Writes the K keys, unsorted, to sm.u.c.cand and returns K
+// (the chunk holds more than kCap >= K finite entries).  Reading the chunk
+// again, rather than from the registers of the stream, keeps the kernel's
+// registers at what two workgroups per CU allow.
+template <typename T>
+__device__ __forceinline__ int radix_chunk(const T* base, const uint32_t* mrow, int e0, int e1, int K,
+                                        float temp, bool divide, bool win, bool owner, float own_v,
+                                        uint32_t own_id, Smem& sm) {
+    const int t = threadIdx.x;
+    const float NEG_INF = -__builtin_huge_valf();
+    auto key_at = [&](int id, uint64_t& k) {
+        if (!((mrow[id >> 5] >> (id & 31)) & 1u)) return false;
+        const int off = id - e0;
+        if (win && ((sm.wbits[off >> 5] >> (off & 31)) & 1u)) return false;
+        const float v = Elt<T>::scalar(base + id);
+        if (!(v > NEG_INF)) return false;
+        k = ckey(divide ? v / temp : v, (uint32_t)id);
+        return true;
+    };
+    const bool own = owner && own_v > NEG_INF;
+    const uint64_t own_key = own ? ckey(divide ? own_v / temp : own_v, own_id) : 0ull;
+    uint64_t prefix = 0, pmask = 0;
+    int remaining = K;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        if (t < 256) sm.hist[t] = 0;
+        lds_sync();
+        for (int id = e0 + t; id < e1; id += kT) {
+            uint64_t k;
+            if (key_at(id, k) && (k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 0xFF], 1);
+        }
+        if (own && (own_key & pmask) == prefix) atomicAdd(&sm.hist[(own_key >> shift) & 0xFF], 1);
+        lds_sync();
+        if (t < 64) pick_digit(sm.hist, remaining, sm.misc);
+        lds_sync();
+        remaining -= sm.misc[1];
+        prefix |= (uint64_t)sm.misc[0] << shift;
+        pmask |= 0xFFull << shift;
+        lds_sync();
+    }
+    // prefix is the K-th largest key (keys are distinct): the K keys >= it
+    if (t == 0) sm.ncand = 0;
+    lds_sync();
+    for (int id = e0 + t; id < e1; id += kT) {
+        uint64_t k;
+        if (key_at(id, k) && k >= prefix) {
+            const int p = atomicAdd(&sm.ncand, 1);
+            if (p < K) sm.u.c.cand[p] = k;
+        }
+    }
+    if (own && own_key >= prefix) {
+        const int p = atomicAdd(&sm.ncand, 1);
+        if (p < K) sm.u.c.cand[p] = own_key;
+    }
+    lds_sync();
+    return min(sm.ncand, K);
+}
+
+// The entries of a 16-byte slot whose bit in `bits` is clear become the
+// -inf pattern of their type (two instructions a 32-bit word).
+template <typename T>
+__device__ __forceinline__ uint4 fold_bits(const uint4& q, uint32_t bits) {
+    constexpr int VEC = Elt<T>::kVec;
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t keep;
+        if constexpr (VEC == 4) {
+            keep = (uint32_t)__builtin_amdgcn_sbfe((int)bits, i, 1);
+        } else {
+            keep = ((uint32_t)__builtin_amdgcn_sbfe((int)bits, 2 * i, 1) & 0xFFFFu) |
+                   ((uint32_t)__builtin_amdgcn_sbfe((int)bits, 2 * i + 1, 1) << 16);
+        }
+        w[i] = (w[i] & keep) | (Elt<T>::kNegInfWord & ~keep);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// The window ids of a slot (bits wb, chunk offsets off + e): each value, as
+// folded by the mask, goes to its table entry, and the entry becomes -inf in
+// the slot.
+template <typename T>
+__device__ void window_out(uint4& q, uint32_t wb, int off, Smem& sm) {
+    constexpr int VEC = Elt<T>::kVec;
+    for (uint32_t b = wb; b; b &= b - 1u) {
+        const int e = __builtin_ctz(b);
+        const uint32_t oe = (uint32_t)(off + e);
+        int sl = hash_slot(oe);
+        for (int probe = 0; probe < kHash && (sm.wtab[sl] >> kCntBits) != oe; ++probe)
+            sl = (sl + 1) & (kHash - 1);
+        sm.wval[sl] = elt<T>(q, e);
+    }
+    q = fold_bits<T>(q, ~wb & ((1u << VEC) - 1u));
+}
+
+template <typename T, bool FAST>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void topk_wide_kernel(KArgs a) {
+    constexpr int VEC = Elt<T>::kVec;
+    constexpr int NV = kSlots * VEC;         // stream values per thread
+    constexpr int kChunkIds = kT * NV;       // ids a chunk can hold
+    static_assert(kChunkIds / 32 <= kT, "window bitmap");
+    __shared__ Smem sm;
+    const float NEG_INF = -__builtin_huge_valf();
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int S = a.S, V = a.V;
+    int row, c;
+    wg_row_chunk(S, row, c);
+    const int e0 = c * a.CE;   // a multiple of 32: the chunk starts on a mask word
+    const int e1 = min(e0 + a.CE, V);
+    const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
+    const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
+
+    // ---- loads in the order they are needed: history position t, then the
+    //      mask words and the stream; the row's parameters and draw words
+    //      come through the scalar path meanwhile.
+    const int rs = a.recent ? (int)a.recent_stride : 1;
+    const int32_t* hrow = a.recent ? a.recent + (int64_t)row * a.recent_stride : kNoHistory;
+    const int wid_raw = hrow[min(t, rs - 1)];
+    uint32_t mw[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int off = VEC * (j * kT + t);
+        mw[j] = mrow[(e0 + min(off, e1 - e0 - 1)) >> 5];
+    }
+    // Slot j holds the VEC entries from e0 + off in one 16-byte word group:
+    // one nontemporal load when the row is 16-byte aligned, else VEC element
+    // loads packed the same way.
+    uint4 raw[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int off = VEC * (j * kT + t);
+        if constexpr (FAST) {
+            raw[j] = ld_nt(base + e0 + min(off, e1 - e0 - VEC));
+        } else {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (VEC == 4) {
+                    w[i] = ((const uint32_t*)base)[min(e0 + off + i, e1 - 1)];
+                } else {
+                    const uint16_t* h = (const uint16_t*)base;
+                    w[i] = (uint32_t)h[min(e0 + off + 2 * i, e1 - 1)] |
+                           ((uint32_t)h[min(e0 + off + 2 * i + 1, e1 - 1)] << 16);
+                }
+            }
+            raw[j] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+    WTR(0);
+    const tms_row_params P = a.params[row];
+    const uint32_t* dp = a.draws ? a.draws + 2 * row : kNoDraws;
+    const uint32_t dw0 = dp[0], dw1 = dp[1];
+    int nrec = 0;
+    if (a.recent) {
+        nrec = a.n_recent ? a.n_recent[row] : rs;
+        nrec = min(max(nrec, 0), rs);
+    }
+
+    const bool greedy = P.greedy != 0;
+    const int K = greedy ? 1 : min(P.top_k, V);
+    const bool unsupported = !greedy && !(P.top_k >= 1 && P.top_k <= kKMax);
+    const float temp = P.temperature;
+    const bool bad_params = !greedy && !(temp > 0.0f && temp <= FLT_MAX);
+    const bool divide = !greedy && temp != 1.0f;
+    const bool skip = unsupported || bad_params;   // the row needs no selection
+
+    Pen pn;
+    pn.rep_on = !(P.repeat_penalty <= 1.0f);
+    pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
+    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
+    pn.rep = P.repeat_penalty;
+    pn.freq = P.frequency_penalty;
+    pn.pres = P.presence_penalty;
+    const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
+
+    // ---- window, while the stream is in flight: the row's history ids in
+    //      this chunk go into an LDS bitmap and a hash table keyed by chunk
+    //      offset that counts their occurrences.  The entry that inserts a
+    //      key owns the id.  The thread that streams the id writes its
+    //      (masked) value into the table in pass 1, and after the bound the
+    //      owner forms the penalised value (tmsample.h:58-61 once per
+    //      occurrence, then frequency/presence) and offers it as a candidate.
+    //      No load beyond the stream.
+    if (pn.on) {
+        for (int i = t; i < kChunkIds / 32; i += kT) sm.wbits[i] = 0u;
+        for (int i = t; i < kHash; i += kT) sm.wtab[i] = kEmpty;
+    }
+    if (t == 0) {
+        sm.lost = 0;
+        sm.onf = 0;
+        sm.ncand = 0;
+    }
+    lds_sync();
+    const bool in_chunk = pn.on && t >= from && t < nrec && wid_raw >= e0 && wid_raw < e1;
+    bool owner = false;
+    int wslot = 0;
+    if (in_chunk) {
+        const uint32_t off = (uint32_t)(wid_raw - e0);
+        atomicOr(&sm.wbits[off >> 5], 1u << (off & 31));
+        int sl = hash_slot(off);
+        for (int probe = 0; probe < kHash; ++probe) {   // 2048 slots for at most 1024 ids
+            const uint32_t old = atomicCAS(&sm.wtab[sl], kEmpty, off << kCntBits);
+            if (old == kEmpty) {
+                owner = true;
+                break;
+            }
+            if ((old >> kCntBits) == off) break;
+            sl = (sl + 1) & (kHash - 1);
+        }
+        atomicAdd(&sm.wtab[sl], 1u);
+        wslot = sl;
+    }
+    WTR(1);
+
+    // ---- pass 1, per slot as it lands: the mask folded into the words (an
+    //      entry the mask leaves out becomes the -inf pattern of its type in
+    //      place), and the thread's IEEE maximum, which keeps a NaN, so one
+    //      test of it finds any NaN or +inf.  Two to three instructions an
+    //      entry: at two workgroups per CU every per-entry instruction costs
+    //      the CU 32 K lane slots.  Pass 1 reads no LDS, so it does not wait
+    //      for the window table.
+    float m = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const int off = VEC * (j * kT + t);
+        const int lim = e1 - e0 - off;   // ids of this slot inside the chunk
+        const uint32_t vmask = lim > 0 ? (1u << min(lim, VEC)) - 1u : 0u;
+        raw[j] = fold_bits<T>(raw[j], (mw[j] >> (off & 31)) & vmask);
+#pragma unroll
+        for (int e = 0; e < VEC; e += 2)
+            m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(elt<T>(raw[j], e), elt<T>(raw[j], e + 1)));
+    }
+    lds_sync();   // the window table is complete
+    // ---- window ids out of the stream: the (masked) value of each goes to
+    //      its table entry and the entry becomes -inf in place; the few
+    //      threads holding one form their maximum again.
+    if (pn.on) {
+        bool again = false;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j) {
+            const int off = VEC * (j * kT + t);
+            const int lim = e1 - e0 - off;
+            const uint32_t vmask = lim > 0 ? (1u << min(lim, VEC)) - 1u : 0u;
+            const uint32_t wb = (sm.wbits[off >> 5] >> (off & 31)) & vmask;
+            if (wb) {   // rare
+                again = true;
+                window_out<T>(raw[j], wb, off, sm);
+            }
+        }
+        if (again) {
+            m = NEG_INF;
+#pragma unroll
+            for (int j = 0; j < kSlots; ++j)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) m = __builtin_elementwise_maximum(m, elt<T>(raw[j], e));
+        }
+    }
+    const bool nf = !(m < __builtin_huge_valf()) && m != NEG_INF;   // NaN or +inf
+    // The row's ticket, now that the chunk's data is in: its round trip
+    // overlaps the selection.  The last chunk of the row to get here merges;
+    // a chunk with an earlier ticket may still be publishing when the merger
+    // reads, and the merger reads such words again.
+    uint32_t ticket = 0;
+    if (S > 1 && t == 0)
+        ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    WTR(2);
+    WSTOP(1, m);
+    // The widened values are formed again from the raw words where they are
+    // used next: holding 32 widened 16-bit values across the bound would
+    // take twice the registers of the words.
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j)
+        asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
+
+    // ---- bound: the maxima of the 128 groups of 8 lanes (DPP, on order
+    //      keys), then the K-th largest of those (wave 0, a bisection with
+    //      ballot counts).  K groups, each with a distinct entry at or above
+    //      it, bound the chunk's K-th value from below.  Per wave this costs
+    //      a few instructions: at two workgroups per CU every instruction all
+    //      waves execute costs about 13 ns.
+    const uint32_t mkey = nf ? 0u : okey(m);
+    {
+        uint32_t g = mkey;
+        g = max(g, dpp_u32<0x111, 0xF, true>(0u, g));   // row_shr:1
+        g = max(g, dpp_u32<0x112, 0xF, true>(0u, g));   // row_shr:2
+        g = max(g, dpp_u32<0x114, 0xF, true>(0u, g));   // row_shr:4
+        if ((lane & 7) == 7) sm.gmax[wv * 8 + (lane >> 3)] = g;   // lane 8q + 7: lanes 8q .. 8q + 7
+    }
+    const uint64_t nfw = __ballot(nf);
+    if (lane == 0) sm.wnf[wv] = nfw ? 1 : 0;
+    WSTOP(11, m);
+    lds_sync();
+    int flags = 0;
+    {
+        const uint4* f4 = (const uint4*)sm.wnf;
+#pragma unroll
+        for (int i = 0; i < kW / 4; ++i) {
+            const uint4 q = f4[i];
+            flags |= (q.x | q.y | q.z | q.w) ? FLAG_NONFINITE : 0;
+        }
+    }
+    if (!skip && wv == 0) {
+        const uint32_t g0 = sm.gmax[lane], g1 = sm.gmax[lane + 64];
+        uint32_t th = 0;
+        // the top 20 key bits: the bound rounds down to a multiple of 2^12
+        // (at most 2^-11 relative below the exact K-th group maximum), which
+        // keeps it a lower bound
+        for (int bit = 31; bit >= 12; --bit) {
+            const uint32_t cand = th | (1u << bit);
+            if (__popcll(__ballot(g0 >= cand)) + __popcll(__ballot(g1 >= cand)) >= K) th = cand;
+        }
+        if (lane == 0) sm.tkey = th;
+    }
+    lds_sync();
+    const uint32_t tkey = sm.tkey;
+    // the owners' penalised values (the table is complete: pass 1 came
+    // before the barrier); they are left out of the bound, which K other
+    // entries already meet
+    float own_v = NEG_INF;
+    if (owner) {
+        own_v = apply_pen(sm.wval[wslot], sm.wtab[wslot] & ((1u << kCntBits) - 1u), pn);
+        if (!(own_v < __builtin_huge_valf()) && own_v != NEG_INF) atomicOr(&sm.onf, 1);
+    }
+    WTR(3);
+    WSTOP(2, okey_inv(tkey));
+
+    // ---- select: candidates are the entries at or above vlo, whose
+    //      quotient can reach the bound's.
+    //      v < vlo implies fl(v / T) < fl(tau / T) (a relative gap of
+    //      2^-19 exceeds two roundings; the absolute term covers subnormal
+    //      quotients), so every entry below it has a key below K entries at
+    //      or above tau.  -inf entries are never candidates (vlo >= -FLT_MAX).
+    const bool select = !skip && !(flags & FLAG_NONFINITE);
+    const float tau = okey_inv(tkey);
+    float vlo = tau;
+    if (divide && tau != NEG_INF) {
+        const double lo = (double)tau - (fabs((double)tau) * 0x1p-19 + (double)temp * 0x1p-140);
+        float f = (float)lo;
+        if ((double)f > lo) f = float_below(f);
+        vlo = f;
+    }
+    vlo = fmaxf(vlo, -FLT_MAX);
+    auto key_of = [&](float v, uint32_t id) { return ckey(divide ? v / temp : v, id); };
+    // Candidates are appended as (value bits, id) to one LDS array: one
+    // ballot and one LDS atomic per wave and pass.
+    auto append = [&](bool tk, float x, uint32_t id) {
+        const uint64_t b = __ballot(tk);
+        if (b) {
+            int base = 0;
+            if (lane == 0) base = atomicAdd(&sm.ncand, __popcll(b));
+            base = __builtin_amdgcn_readfirstlane(base);
+            const int p = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            if (tk && p < kCap) sm.u.c.cand[p] = ((uint64_t)__float_as_uint(x) << 32) | id;
+        }
+    };
+    if (select) {
+        // A lane holds candidates only if its maximum reaches vlo ("hot").
+        const bool hot = m >= vlo;
+        const uint64_t hb = __ballot(hot);
+        const int nh = __popcll(hb);
+        // The hot lanes' words go to LDS, kHot lanes a round, and the wave
+        // examines only those entries, 64 a pass.
+        const int hs = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(hb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)hb, 0u));
+        uint4* hw = sm.hot + (wv * kHot) * kSlots;
+        const T* hv = (const T*)hw;   // hot slot s, entry q: hv[s * NV + q] with q = j * VEC + e
+        for (int g0 = 0; g0 < nh; g0 += kHot) {
+            const int ng = min(nh - g0, kHot);
+            if (hot && hs >= g0 && hs < g0 + kHot) {
+#pragma unroll
+                for (int j = 0; j < kSlots; ++j) hw[(hs - g0) * kSlots + j] = raw[j];
+                sm.hotlane[wv * kHot + hs - g0] = lane;
+            }
+            wave_lds_sync();
+            for (int p = 0; p < ng * NV; p += 64) {
+                const int q = p + lane, sidx = q / NV, qi = q % NV;
+                float x = NEG_INF;
+                int id = 0;
+                if (sidx < ng) {
+                    x = Elt<T>::scalar(hv + q);
+                    id = e0 + VEC * ((qi / VEC) * kT + wv * 64 + sm.hotlane[wv * kHot + sidx]) + qi % VEC;
+                }
+                append(x >= vlo, x, (uint32_t)id);
+            }
+            wave_lds_sync();   // the next round writes over these slots
+        }
+        append(owner && own_v >= vlo, own_v, (uint32_t)wid_raw);
+    }
+    if (t == 0) sm.ticket = ticket;
+    lds_sync();
+    int ncand = select ? sm.ncand : 0;
+    const bool merger = S == 1 || (int)sm.ticket == S - 1;   // the last chunk of the row to arrive
+    WSTOP(22, (float)ncand);
+    const bool radixed = ncand > kCap;
+    if (radixed) {
+        // ---- exact radix select (every wave): the chunk's K keys
+        ncand = radix_chunk<T>(base, mrow, e0, e1, K, temp, divide, pn.on, owner, own_v,
+                               (uint32_t)wid_raw, sm);
+    }
+    WTV(15, ncand);
+    const int nlist = min(ncand, K);
+    uint64_t* rl = a.tlists + (int64_t)row * S * kLStride;   // this row's lists
+    uint64_t* my = rl + (int64_t)c * kLStride;
+    // The merge bound uses each list's rm-th key, rm = ceil(K / S).
+    const int rm = (K + S - 1) / S;
+    // Merger waves 1 .. S - 1 hold the other lists (wave w: entry i in key0
+    // of lane i, entry 64 + i in key1); wave 0 holds this chunk's own.
+    uint64_t key0 = 0, key1 = 0;
+    int ncc = 0;
+    if (wv == 0) {
+        // ---- wave 0 alone (the other waves wait at a barrier or have
+        //      ended): the keys (the division, one per lane), the rank, and
+        //      the publish straight from the rank (every word is non-zero;
+        //      the merger reads a word again while it reads 0)
+        if (select && !radixed) {
+            for (int i = lane; i < ncand; i += 64) {
+                const uint64_t rv = sm.u.c.cand[i];
+                sm.u.c.cand[i] = key_of(__uint_as_float((uint32_t)(rv >> 32)), (uint32_t)rv);
+            }
+        }
+        if (lane == 0) sm.u.c.cand[ncand] = 0ull;   // rank_wave reads keys in pairs
+        wave_lds_sync();
+        if (sm.onf) flags |= FLAG_NONFINITE;      // a penalised window value
+        // (the merger's own list stays in LDS)
+        if (select) rank_wave(sm.u.c.cand, ncand, K, sm.slist, merger ? nullptr : my + 1);
+        if (!merger && lane == 0) st_agent(&my[0], header(flags, nlist));
+        if (merger) {
+            wave_lds_sync();
+            key0 = lane < nlist ? sm.slist[lane] : 0ull;
+            key1 = lane + 64 < nlist ? sm.slist[lane + 64] : 0ull;
+            ncc = nlist;
+            if (lane == 0) sm.mf[0] = flags;
+        }
+    } else if (!merger) {
+        return;
+    } else if (wv == kW - 1 && S < kW) {
+        // an idle merger wave: the row's draw words meanwhile
+        uint32_t w0 = dw0, w1 = dw1;
+        if (!a.draws && !greedy) row_words(P.seed, P.offset, 0u, w0, w1);
+        if (lane == 0) {
+            sm.draw[0] = w0;
+            sm.draw[1] = w1;
+        }
+    } else if (wv < S) {
+        // other list number wv - 1 (skipping this chunk's own)
+        const int cc = wv - 1 < c ? wv - 1 : wv;
+        uint64_t* L = rl + (int64_t)cc * kLStride;
+        // header and keys at once; a word still in flight reads 0
+        uint64_t h = ld_agent(&L[0]);
+        uint64_t k0 = ld_agent(&L[1 + lane]);
+        uint64_t k1 = K > 64 ? ld_agent(&L[65 + lane]) : 0ull;
+        int spins = 0;
+        while (!(h & kReady) && spins < kPollCap) {
+            h = ld_agent(&L[0]);
+            ++spins;
+        }
+        const int n = (h & kReady) ? hdr_n(h) : 0;
+        while (lane < n && k0 == 0 && spins < kPollCap) {
+            k0 = ld_agent(&L[1 + lane]);
+            ++spins;
+        }
+        while (lane + 64 < n && k1 == 0 && spins < kPollCap) {
+            k1 = ld_agent(&L[65 + lane]);
+            ++spins;
+        }
+        const bool lost = !(h & kReady) || (lane < n && k0 == 0) || (lane + 64 < n && k1 == 0);
+        if (__ballot(lost) && lane == 0) sm.lost = 1;
+        key0 = lane < n ? k0 : 0ull;
+        key1 = lane + 64 < n ? k1 : 0ull;
+        ncc = n;
+        if (lane == 0) sm.mf[wv] = hdr_flags(h);
+        // every word read goes back to zero for the next call
+        if (!lost) {
+            if (lane < n) st_agent(&L[1 + lane], (uint64_t)0);
+            if (lane + 64 < n) st_agent(&L[65 + lane], (uint64_t)0);
+            if (lane == 0) st_agent(&L[0], (uint64_t)0);
+        }
+    }
+    WTR(5);
+    WSTOP(3, (float)(key0 + key1));
+    if (!merger) return;   // wave 0 of a chunk that does not merge
+
+    // ================= merge (the last chunk of the row)
+    WTR(6);
+    WSTOP(4, (float)nlist);
+    if (t == 0 && S > 1) st_agent(&a.counters[row * kCounterStride], 0u);
+    if (wv < S) {
+        // the list's rm-th key (0 when it holds fewer)
+        uint64_t kr = 0;
+        if (ncc >= rm) {
+            const uint64_t src = rm <= 64 ? key0 : key1;
+            const int l = (rm - 1) & 63;
+            kr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(src >> 32), l) << 32) |
+                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)src, l);
+        }
+        if (lane == 0) {
+            sm.mn[wv] = ncc;
+            sm.mk[wv] = kr;
+        }
+    }
+    lds_sync();
+
+    WTR(7);
+    WSTOP(5, (float)(key0 + key1));
+    // the lists' flags, lengths and rm-th keys: lane l reads list l, and
+    // wave reductions give each wave the totals
+    int fo, ntot, nlong;
+    uint64_t tm;
+    {
+        const bool in = lane < S;
+        const int f = in ? sm.mf[lane] : 0, n = in ? sm.mn[lane] : 0;
+        const bool lg = in && n >= rm;
+        uint64_t k = lg ? sm.mk[lane] : ~0ull;
+        fo = wave_or_i32(f);
+        ntot = wave_sum_dpp(n);
+        nlong = __popcll(__ballot(lg));
+        tm = wave_min_u64(k);
+    }
+    int status = TMS_ROW_OK;
+    if (sm.lost) status = TMS_ROW_INTERNAL;
+    else if (bad_params) status = TMS_ROW_BAD_PARAMS;
+    else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
+    else if (unsupported) status = TMS_ROW_UNSUPPORTED;
+    else if (ntot == 0) status = TMS_ROW_ALL_MASKED;
+    if (status == TMS_ROW_UNSUPPORTED) {
+        defer_dense(a, row);   // the whole-row pass, or TMS_ROW_UNSUPPORTED without one
+        return;
+    }
+    if (status != TMS_ROW_OK) {
+        if (t == 0) {
+            a.out_tokens[row] = -1;
+            a.out_status[row] = status;
+            if (a.out_keep) a.out_keep[row] = 0;
+        }
+        for (int i = t; i < a.topk_cap; i += kT) {
+            if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = -1;
+            if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = 0.0f;
+        }
+        return;
+    }
+
+    // ---- rank merge.  When the lists holding rm keys number at least
+    //      K / rm, the least of their rm-th keys bounds the row's K-th key
+    //      from below (they hold K keys at or above it); only keys at or
+    //      above it can place.  They are compacted and ranked among
+    //      themselves (the set is closed upward, so the ranks are the row's).
+    {
+        const uint64_t tg = nlong * rm >= K ? tm : 0ull;
+        const int lim = min(ncc, K);
+        const bool s0 = wv < S && lane < lim && key0 >= tg;
+        const bool s1 = wv < S && lane + 64 < lim && key1 >= tg;
+        const uint64_t b0 = __ballot(s0), b1 = __ballot(s1);
+        if (wv < S && lane == 0) sm.scnt[wv] = __popcll(b0) + __popcll(b1);
+        WSTOP(51, (float)(b0 + b1));
+        lds_sync();
+        // this wave's offset and the total, from lane l's count of list l
+        const int q = lane < S ? sm.scnt[lane] : 0;
+        const int qi = wave_incl_scan_i32(q);
+        const int nsurv = __builtin_amdgcn_readlane(qi, 63);
+        const int off = wv < S ? __builtin_amdgcn_readlane(qi - q, wv) : 0;
+        const int r0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
+        const int r1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
+        if (s0) sm.u.surv[off + r0] = key0;
+        if (s1) sm.u.surv[off + __popcll(b0) + r1] = key1;
+        if (t < kPad) sm.u.surv[nsurv + t] = 0ull;
+        lds_sync();
+        WTV(14, nsurv);
+        WSTOP(52, (float)nsurv);
+        rank_place(sm.u.surv, nsurv, K, sm.srt);
+    }
+    lds_sync();
+    WTR(8);
+    WSTOP(6, (float)sm.srt[0]);
+    const int N = min(ntot, K);
+
+    if (greedy) {
+        const int tok = (int)ckey_id(sm.srt[0]);
+        if (t == 0) {
+            a.out_tokens[row] = tok;
+            a.out_status[row] = TMS_ROW_OK;
+            if (a.out_keep) a.out_keep[row] = 0;
+        }
+        for (int i = t; i < a.topk_cap; i += kT) {
+            if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
+            if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
+        }
+        return;
+    }
+    if (wv != 0) return;
+    // ---- one wave from here: fewer than K finite ids -> the top-K goes on
+    //      with -inf entries in ascending id order (the ids in [0, K + N)
+    //      missing from the finite set).
+    if (N < K) {
+        int filled = 0;
+        for (int q0 = 0; q0 < K + N && filled < K - N; q0 += 64) {
+            const int q = q0 + lane;
+            bool member = false;
+            for (int i = 0; i < N; ++i) member |= (int)ckey_id(sm.srt[i]) == q;
+            const bool gap = q < K + N && q < V && !member;
+            const uint64_t b = __ballot(gap);
+            const int p = filled + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            if (gap && p < K - N) sm.srt[N + p] = ckey(NEG_INF, (uint32_t)q);
+            filled += __popcll(b);
+        }
+        wave_lds_sync();
+    }
+    if (ckey_val(sm.srt[0]) == __builtin_huge_valf()) {   // v / T overflowed
+        if (lane == 0) {
+            a.out_tokens[row] = -1;
+            a.out_status[row] = TMS_ROW_NONFINITE;
+            if (a.out_keep) a.out_keep[row] = 0;
+        }
+        for (int i = lane; i < a.topk_cap; i += 64) {
+            if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = -1;
+            if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = 0.0f;
+        }
+        return;
+    }
+    uint32_t w0 = dw0, w1 = dw1;
+    if (S < kW) {   // formed by the idle merger wave (the barriers since order its store)
+        w0 = sm.draw[0];
+        w1 = sm.draw[1];
+    } else if (!a.draws) {
+        row_words(P.seed, P.offset, 0u, w0, w1);
+    }
+    tail_topk(a, row, P, sm.srt, K, K, sm.u.tail.pr, sm.u.tail.q, w0, w1);
+    WTR(9);
+}
+
+}  // namespace wide
+}  // namespace tms
+
+// Launch of the wide top-k kernel for tms_sample_batch (declared in
+// tms_sample_common.h): same argument block as the general kernel, with
+// k.S <= kWideMaxChunksHost chunks of k.CE ids (a multiple of 32, at most
+// 4096 * the vector width).
+int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream) {
+    const dim3 grid((unsigned)(batch * k.S)), block(tms::wide::kT);
+#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::wide::topk_wide_kernel<T, F>), grid, block, 0, stream, k)
+    switch (dtype) {
+        case TMS_DTYPE_F32:
+            if (fast) TMS_LAUNCH(float, true);
+            else TMS_LAUNCH(float, false);
+            break;
+        case TMS_DTYPE_F16:
+            if (fast) TMS_LAUNCH(_Float16, true);
+            else TMS_LAUNCH(_Float16, false);
+            break;
+        default:
+            if (fast) TMS_LAUNCH(tms::Bf16, true);
+            else TMS_LAUNCH(tms::Bf16, false);
+            break;
+    }
+#undef TMS_LAUNCH
+    return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;
+}
