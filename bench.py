@@ -13,7 +13,16 @@ launches, so the bench keeps enough copies of the batch to stream at least
 768 MB and rotates through them, launch by launch: every launch reads its
 batch from HBM, not from the cache (--no-rotate times the cache-resident case).
 
-    python bench.py [--steps K] [--warmup W] [--config 2|3|4|5] [--no-cpu] [--no-rotate]
+roofline.traffic is the sampler's HBM bytes per launch measured in the same
+run: before this process touches the GPU it runs itself twice under
+rocprofv3 (--pmc FETCH_SIZE, then --pmc WRITE_SIZE, 22 eager launches each),
+and scales each counter by what it reads for a 256 MiB device copy of known
+size (--no-traffic skips this).  The CPU baseline is the reference's own
+tmsample.h (oracle/_ref) on the host's threads, median pass, with a one-thread
+figure beside it.
+
+    python bench.py [--steps K] [--warmup W] [--config 2|3|4|5] [--no-cpu] [--no-traffic]
+                    [--no-rotate]
 """
 from __future__ import annotations
 
@@ -29,7 +38,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8.0e12
-METRIC = "sampled rows/sec and HBM GB/s (% of peak) at B=64, V=128256, fp32 logits"
+# BASELINE.json's metric is quoted on config 2; the other configs are named the
+# same way for their own shapes.
+METRICS = {
+    2: "sampled rows/sec and HBM GB/s (% of peak) at B=64, V=128256, fp32 logits",
+    3: "sampled rows/sec and HBM GB/s (% of peak) at B=128, V=151936, fp16 logits",
+    4: "verified sequences/sec and HBM GB/s (% of peak) at B=32, k=8, V=32000, fp32 logits",
+    5: "sampled rows/sec and HBM GB/s (% of peak) at B=1024, V=256000, bf16 logits",
+}
 
 
 def parse():
@@ -44,6 +60,8 @@ def parse():
     ap.add_argument("--eager", action="store_true", help="time eager launches, no graph")
     ap.add_argument("--general", action="store_true",
                     help="pass no row-kind hint (the general kernel for every batch)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the in-run HBM traffic measurement (two rocprofv3 counter passes)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 plain device copies of MIB MiB (a known-size kernel that "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -75,45 +93,108 @@ def workload(cfg):
     return w, "bf16", bytes_, "cfg5: B=1024 V=256000 bf16, 50% greedy, top-k 100 + top-p 0.98"
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, cfg):
-    """The reference's own tmsample.h (oracle/_ref), timed on this host."""
+    """The reference's own tmsample.h (oracle/_ref), timed on this host: rows
+    dealt to a thread pool, median pass of about 10 s of work, and a
+    one-thread figure beside it."""
     import oracle
 
     ref = oracle.reference()
     if ref is None or cfg != 2:
         return None
     x = w["logits"]
-    threads = max(1, min(16, os.cpu_count() or 1))
+    nproc = os.cpu_count() or 1
+    # the GPU box's CPU share is 16 threads (OMP_NUM_THREADS there), whatever nproc shows
+    threads = max(1, min(nproc, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16))
+    kw = dict(recent=w["recent"], window=256, penalty=1.1, mask=w["mask"])
     t0 = time.perf_counter()
-    dt, _ = ref.bench(x, 0.7, 40, 0.95, recent=w["recent"], window=256, penalty=1.1,
-                      mask=w["mask"], threads=threads, reps=1)
-    reps = max(1, min(5000, int(10.0 / max(dt, 1e-4))))   # about 10 s of host work
-    dt, _ = ref.bench(x, 0.7, 40, 0.95, recent=w["recent"], window=256, penalty=1.1,
-                      mask=w["mask"], threads=threads, reps=reps)
-    wall = time.perf_counter() - t0
+    dt, _ = ref.bench(x, 0.7, 40, 0.95, threads=threads, reps=1, **kw)
+    reps = max(3, min(5000, int(10.0 / max(dt, 1e-4))))   # about 10 s of host work
+    dt, _ = ref.bench(x, 0.7, 40, 0.95, threads=threads, reps=reps, **kw)
     B = x.shape[0]
+    rows1 = x[:8]   # one thread: 8 rows, median of 5 passes
+    dt1, _ = ref.bench(rows1, 0.7, 40, 0.95, recent=w["recent"][:8], window=256, penalty=1.1,
+                       mask=w["mask"][:8], threads=1, reps=5)
+    wall = time.perf_counter() - t0
     return {
         "value": round(B / dt, 1),
         "unit": "rows/s",
         "cores": threads,
         "kind": "reference",
-        "sample": (f"the reference tmsample.h (mask -> apply_repeat_penalty 1.1/256 -> "
-                   f"sample T=0.7 k=40 p=0.95) over the same {B} x {x.shape[1]} fp32 rows, "
-                   f"best of {reps} passes, {threads} threads, {wall:.1f} s wall; "
+        "one_core": round(8 / dt1, 1),
+        "cpu": cpu_model(),
+        "nproc": nproc,
+        "sample": (f"the reference tmsample.h compiled -O3 (mask -> apply_repeat_penalty 1.1/256 -> "
+                   f"sample T=0.7 k=40 p=0.95) over the same {B} x {x.shape[1]} fp32 rows, rows dealt "
+                   f"to {threads} threads (the GPU box's CPU share; nproc {nproc}), median of {reps} "
+                   f"passes; one_core: 8 rows on 1 thread, median of 5; {wall:.1f} s wall in all; "
                    f"frequency/presence/min-p are absent from the reference"),
     }
 
 
-def traffic_from_profiles(cfg, general=False):
-    """HBM bytes per launch measured with rocprofv3 (profiles/traffic.json), or None."""
-    p = os.path.join(ROOT, "profiles", "traffic.json")
-    if not os.path.exists(p):
-        return None
-    try:
-        d = json.load(open(p))
-        return d.get(f"cfg{cfg}" + ("_general" if general else ""))
-    except Exception:
-        return None
+def measure_traffic(args):
+    """HBM bytes per launch of the sampler, measured in this run: two child
+    runs of this script under rocprofv3 (FETCH_SIZE, then WRITE_SIZE; one
+    counter pass each), each with a device copy of 256 MiB first whose
+    counters calibrate the bytes.  Returns (bytes, note) or (None, reason)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, "rocprofv3 not found"
+    steps, warm, mib = 20, 2, 256
+    vals = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="tms_traffic_", dir="/tmp")
+        cmd = [prof, "--pmc", ctr, "--output-format", "csv", "-d", out, "-o", "p", "--",
+               sys.executable, os.path.abspath(__file__), "--config", str(args.config),
+               "--steps", str(steps), "--warmup", str(warm), "--no-cpu", "--eager",
+               "--no-traffic", "--calib-copy", str(mib)] + (["--general"] if args.general else [])
+        env = dict(os.environ, TMPDIR="/tmp")
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=300)
+        except subprocess.TimeoutExpired:
+            return None, f"rocprofv3 {ctr} pass timed out"
+        files = [os.path.join(d, f) for d, _, fs in os.walk(out) for f in fs
+                 if f.endswith("counter_collection.csv")]
+        if r.returncode != 0 or not files:
+            return None, f"rocprofv3 {ctr} pass failed (rc {r.returncode})"
+        copy, tms = [], []
+        for row in csv.DictReader(open(files[0])):
+            if row.get("Counter_Name") != ctr:
+                continue
+            v = float(row["Counter_Value"])
+            name = row["Kernel_Name"]
+            if "copyBuffer" in name:
+                copy.append(v)
+            elif "tms::" in name:
+                tms.append(v)
+        shutil.rmtree(out, ignore_errors=True)
+        if not copy or not tms:
+            return None, f"rocprofv3 {ctr} pass: no copy or sampler dispatches"
+        known_kib = mib * 1024.0   # the copy reads mib MiB and writes mib MiB
+        factor = known_kib / max(copy)
+        vals[ctr] = (sum(tms) / (steps + warm), factor)
+    fetch, ff = vals["FETCH_SIZE"]
+    write, fw = vals["WRITE_SIZE"]
+    nbytes = int(round((fetch * ff + write * fw) * 1024.0))
+    note = (f"rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE in this run ({steps + warm} eager launches "
+            f"each): {fetch:.1f} KiB x {ff:.3f} read + {write:.1f} KiB x {fw:.3f} written per launch, "
+            f"factors from a {mib} MiB device copy")
+    return nbytes, note
 
 
 def main():
@@ -123,6 +204,9 @@ def main():
               f"(rows are independent; a batch split across GPUs needs no exchange)",
               file=sys.stderr)
         sys.exit(2)
+    # The traffic passes run as child processes before this one touches the GPU.
+    traffic, traffic_note = (None, "not measured (--no-traffic)") if args.no_traffic \
+        else measure_traffic(args)
     import torch
 
     from tensormark_amd import Sampler
@@ -241,9 +325,9 @@ def main():
     achieved = algo_bytes / (ms * 1e-3)
     cpu = None if args.no_cpu else cpu_baseline(w, args.config)
     line = {
-        "metric": METRIC,
+        "metric": METRICS[args.config],
         "value": round(rows_per_s, 1),
-        "unit": "rows/s",
+        "unit": "sequences/s" if args.config == 4 else "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -251,7 +335,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": dt_name,
         "data": "synthetic (seeded numpy; no model)",
         "config": {"workload": name, "batch": B, "vocab": V, "launch": "graph" if graph else "eager",
                    "input_sets": n_sets, "hbm_resident_bytes": n_sets * algo_bytes,
@@ -263,7 +347,8 @@ def main():
             "peak": PEAK_HBM / 1e9,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM, 4),
-            "traffic": traffic_from_profiles(args.config, args.general),
+            "traffic": traffic,
+            "traffic_source": traffic_note,
         },
         "cpu_baseline": cpu,
     }

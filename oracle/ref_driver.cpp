@@ -12,6 +12,7 @@
 
 #include "tmsample.h"
 
+#include <algorithm>
 #include <chrono>
 #include <cstdint>
 #include <cstring>
@@ -98,14 +99,15 @@ int ref_sample(const float* logits, int V, float T, int top_k, float top_p, int 
 }
 
 // CPU baseline: sample B rows with `threads` workers, `reps` times; returns
-// the best wall time of one pass in seconds.  Rows are independent, so they
+// the median wall time of one pass in seconds.  Rows are independent, so they
 // are dealt round-robin to the workers.
 double ref_bench(const float* logits, int B, int V, float T, int top_k, float top_p,
                  const std::int32_t* recent, int recent_stride, int window, float penalty,
                  const std::uint32_t* mask, int mask_stride, int threads, int reps,
                  std::int32_t* tokens) {
     if (threads < 1) threads = 1;
-    double best = 1e30;
+    if (reps < 1) reps = 1;
+    std::vector<double> times;
     for (int r = 0; r < reps; ++r) {
         const auto t0 = std::chrono::steady_clock::now();
         std::vector<std::thread> pool;
@@ -122,11 +124,11 @@ double ref_bench(const float* logits, int B, int V, float T, int top_k, float to
                                              : nullptr);
             });
         for (auto& t : pool) t.join();
-        const double dt =
-            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-        if (dt < best) best = dt;
+        times.push_back(std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
     }
-    return best;
+    // the median pass (the lower middle one for an even count)
+    std::nth_element(times.begin(), times.begin() + (reps - 1) / 2, times.end());
+    return times[(reps - 1) / 2];
 }
 
 // The reference's no-repeat n-gram ban and DRY on a row, in place

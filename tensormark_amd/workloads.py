@@ -18,6 +18,9 @@ library and the CPU checker.  Shapes and distributions:
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 from .sampler import make_params, Opts
@@ -93,9 +96,39 @@ def cfg3(seed=3, B=128, V=151936):
     return dict(logits=x, recent=None, params=params, mask=mask)
 
 
+def _blocks(n, size):
+    return [(i, min(i + size, n)) for i in range(0, n, size)]
+
+
+def _pool():
+    return ThreadPoolExecutor(max_workers=max(1, min(16, os.cpu_count() or 1)))
+
+
 def cfg5(seed=5, B=1024, V=256000):
-    rng = np.random.default_rng(seed)
-    x = (rng.standard_t(3, size=(B, V)) * 2.0).astype(np.float32)
+    """Student-t (nu 3) * 2 as z / sqrt(g / 1.5), z ~ N(0, 1), g ~ Gamma(1.5)
+    (chi-square with 3 degrees is 2 * Gamma(1.5)), drawn in float32 per block
+    of 64 rows from the block's own child seed on a thread pool: the values
+    depend on the seed and the block, not on the number of threads."""
+    ss = np.random.SeedSequence(seed)
+    main, blocks = ss.spawn(2)
+    rng = np.random.default_rng(main)
+    spans = _blocks(B, 64)
+    seeds = blocks.spawn(len(spans))
+    x = np.empty((B, V), np.float32)
+
+    def fill(i):
+        lo, hi = spans[i]
+        r = np.random.default_rng(seeds[i])
+        z = r.standard_normal((hi - lo, V), dtype=np.float32)
+        g = r.standard_gamma(1.5, (hi - lo, V), dtype=np.float32)
+        g /= np.float32(1.5)
+        np.sqrt(g, out=g)
+        z /= g
+        z *= np.float32(2.0)
+        x[lo:hi] = z
+
+    with _pool() as ex:
+        list(ex.map(fill, range(len(spans))))
     recent = rng.integers(0, V, size=(B, 512)).astype(np.int32)
     greedy = rng.random(B) < 0.5
     params = make_params(B, Opts(1.2, 100, 0.98), repeat_penalty=1.05, repeat_last_n=512,
@@ -104,10 +137,26 @@ def cfg5(seed=5, B=1024, V=256000):
 
 
 def to_bf16_bits(x: np.ndarray) -> np.ndarray:
-    """fp32 -> bf16 (round to nearest even) as uint16 bits."""
-    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    return r
+    """fp32 -> bf16 (round to nearest even) as uint16 bits; a NaN stays a NaN
+    (quiet bit set).  32-bit arithmetic, 64 rows a block on a thread pool."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    out = np.empty(u.shape, np.uint16)
+    flat_u = u.reshape(-1, u.shape[-1]) if u.ndim > 1 else u.reshape(1, -1)
+    flat_o = out.reshape(flat_u.shape)
+
+    def conv(span):
+        lo, hi = span
+        w = flat_u[lo:hi]
+        r = w + np.uint32(0x7FFF)      # no wrap: only NaN patterns exceed 0xFFFF8000
+        r += (w >> 16) & np.uint32(1)
+        r >>= 16
+        nan = (w & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+        r[nan] = (w[nan] >> 16) | np.uint32(0x40)
+        flat_o[lo:hi] = r.astype(np.uint16)
+
+    with _pool() as ex:
+        list(ex.map(conv, _blocks(flat_u.shape[0], 64)))
+    return out
 
 
 def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:

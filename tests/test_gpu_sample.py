@@ -172,6 +172,29 @@ def test_cfg5_rows_bf16_vs_oracle(sampler, orc):
     check(g, want, 100)
 
 
+@pytest.fixture(scope="module")
+def cfg5_full(orc):
+    """Config 5 at its benchmark size (B = 1024, V = 256000 bf16) and the
+    oracle's answer for every row, made once for both kernel choices."""
+    w = workloads.cfg5()
+    bits = workloads.to_bf16_bits(w["logits"])
+    del w["logits"]
+    x32 = workloads.bf16_bits_to_f32(bits)
+    want = orc.sample_batch(x32, w["params"], recent=w["recent"], topk_cap=100)
+    del x32
+    return bits, w, want
+
+
+def test_cfg5_full_workload_vs_oracle(sampler, cfg5_full):
+    """Every row of the benchmark workload: tokens, keep counts and the
+    top-100 ids and probabilities of the sampled half, the argmax of the
+    greedy half (16,384 workgroups, many rounds of residency)."""
+    bits, w, want = cfg5_full
+    g = run_gpu(sampler, bits, w["params"], recent=w["recent"], topk_cap=100, dtype="bf16")
+    assert (want["status"] == 0).all()
+    check(g, want, 100)
+
+
 def test_many_draws_same_row(sampler, orc):
     """One row, 256 batch copies with different uniforms: every draw matches."""
     rng = np.random.default_rng(3)
