@@ -186,6 +186,19 @@ int tms_destroy(tms_context* ctx);
 size_t tms_workspace_bytes(const tms_context* ctx);
 
 /*
+ * Zero the words of the workspace that the calls' cross-workgroup protocols
+ * expect at zero between calls (arrival counters and tickets, list and part
+ * words, the whole-row queue), stream-ordered.  The calls leave them at zero
+ * themselves; a row that reports TMS_ROW_INTERNAL (a bounded wait ran out)
+ * may leave late words behind, so a caller that sees that status calls this
+ * before the next call on the context.  ctx == NULL resets the current
+ * device's tms_sample_batch_noalloc scratch.  Uses hipMemsetAsync: not for
+ * graph capture.  No counterpart in the reference (its sampler is host
+ * code).
+ */
+int tms_workspace_reset(tms_context* ctx, hipStream_t stream);
+
+/*
  * Batched mask -> penalties -> temperature -> top-k -> softmax -> top-p /
  * min-p -> draw, one launch, stream-ordered, no host synchronisation.
  * Replaces sample_token (tensormark/llama_chat.cpp:146-153) with the grammar
@@ -295,6 +308,14 @@ void tms_vocab_clear_cache(tms_vocab* v);
  * library's own exp used by tms_spec_verify).
  */
 int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipStream_t stream);
+/* Checks of the device ordering the cross-workgroup protocols rely on
+ * (synchronous; allocates; `trials` of each): counts[0] stale reads of a
+ * line written by another XCD in the previous kernel, counts[1] words lost
+ * when two XCDs write halves of one line in one kernel, counts[2] kernels
+ * started before their predecessor on the stream finished, counts[3]
+ * workgroups w of a 64-workgroup grid not on XCD w mod n, counts[4] the XCD
+ * count n. */
+int tms_debug_ordering(int trials, int32_t* counts);
 int tms_debug_exp(const double* in, double* out, int n, int which, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -34,6 +34,7 @@ struct tms_context {
     int max_chunks;
     size_t bytes;
     void* ws;
+    size_t ones_begin, ones_end;   // byte range of the all-ones mask row in ws
     uint32_t* counters;        // [max_batch][kCounterStride] sampler arrival counters (word 0)
     uint32_t* ones;            // all-ones mask row, for calls without a grammar mask
     uint64_t* lists;           // [max_batch][max_chunks][kListStride] chunk candidate lists

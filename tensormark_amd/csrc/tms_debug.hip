@@ -1,8 +1,12 @@
 // tms_debug.hip -- test hooks: run the device Philox and the device double
-// exp on caller inputs so the tests can pin them against the host checker.
+// exp on caller inputs so the tests can pin them against the host checker,
+// and check the ordering properties of the device that the library's
+// cross-workgroup protocols rely on.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 
 #include "../../include/tmsample_hip.h"
 #include "tms_device.h"
@@ -28,7 +32,138 @@ __global__ void exp_kernel(const double* in, double* out, int n, int which) {
     out[i] = which ? exp64(in[i], tab) : exp(in[i]);
 }
 
+// ---- ordering checks (tms_debug_ordering)
+
+// The XCD (XCC) this wave runs on: hardware register XCC_ID, bits 3:0.
+__device__ __forceinline__ int xcc_id() {
+    return __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 0xF;
+}
+
+// The first workgroup of the grid found running on XCD `who` claims the role.
+__device__ __forceinline__ bool claims(int who, int* claim) {
+    return xcc_id() == who && atomicCAS(&claim[who], 0, 1) == 0;
+}
+
+// One line of 16 words: the claimant on XCD `who` sums it (plain loads).
+__global__ void line_read(const uint64_t* p, int who, int* claim, uint64_t* out) {
+    if (threadIdx.x != 0 || !claims(who, claim)) return;
+    uint64_t s = 0;
+    for (int i = 0; i < 16; ++i) s += p[i];
+    out[0] = s;
+}
+
+// XCD `a` writes the even words, XCD `b` the odd words of the line (plain
+// stores), in one kernel; with a == b XCD a writes every word.
+__global__ void line_write(uint64_t* p, uint64_t v, int a, int b, int* claim) {
+    if (threadIdx.x != 0) return;
+    int off = -1, step = a == b ? 1 : 2;
+    if (claims(a, claim)) off = 0;
+    else if (a != b && claims(b, claim)) off = 1;
+    if (off < 0) return;
+    for (int i = off; i < 16; i += step) p[i] = v;
+}
+
+// Back to back on one stream: every workgroup of the first kernel counts
+// itself after a short bounded pause; the second reads the count at once.
+__global__ void count_in(unsigned* ctr, int pause) {
+    if (threadIdx.x != 0) return;
+    for (int i = 0; i < pause; ++i) __builtin_amdgcn_s_sleep(10);
+    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__global__ void count_seen(unsigned* ctr, unsigned want, int* bad) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != want) atomicAdd(bad, 1);
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void xcc_of(int* ids) {
+    if (threadIdx.x == 0) ids[blockIdx.x] = xcc_id();
+}
+
 }  // namespace tms
+
+// counts[0]: reads on XCD 1 that missed a line written on XCD 0 by the
+//            previous kernel, after XCD 1 had read (cached) the line;
+// counts[1]: lines written half by XCD 0 and half by XCD 1 in one kernel
+//            that the next kernel (XCD 2) read with a word lost;
+// counts[2]: kernels that started before the previous kernel on the stream
+//            had finished;
+// counts[3]: workgroups w of a 64-workgroup grid not on XCD w mod (XCD
+//            count), the placement the sampler's row mapping assumes;
+// counts[4]: the XCD count seen.  Synchronous; `trials` of each.
+extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
+    if (!counts || trials <= 0) return TMS_ERR_INVALID_ARG;
+    constexpr int kGrid = 64;
+    uint64_t* line = nullptr;
+    uint64_t* out = nullptr;
+    int* claim = nullptr;
+    int* ids = nullptr;
+    int* bad = nullptr;
+    unsigned* ctr = nullptr;
+    int rc = TMS_OK;
+    hipStream_t s = nullptr;
+    if (hipMalloc(&line, 128) != hipSuccess || hipMalloc(&out, 8) != hipSuccess ||
+        hipMalloc(&claim, 16 * sizeof(int)) != hipSuccess || hipMalloc(&ids, kGrid * sizeof(int)) != hipSuccess ||
+        hipMalloc(&bad, sizeof(int)) != hipSuccess || hipMalloc(&ctr, sizeof(unsigned)) != hipSuccess ||
+        hipStreamCreate(&s) != hipSuccess)
+        rc = TMS_ERR_HIP;
+    int hid[kGrid] = {0};
+    int nx = 1;
+    if (rc == TMS_OK) {
+        hipLaunchKernelGGL(tms::xcc_of, dim3(kGrid), dim3(64), 0, s, ids);
+        if (hipMemcpyAsync(hid, ids, sizeof(hid), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            rc = TMS_ERR_HIP;
+        for (int i = 0; i < kGrid; ++i) nx = std::max(nx, hid[i] + 1);
+    }
+    int stale = 0, lost = 0, overlap = 0, placed = 0;
+    if (rc == TMS_OK) {
+        for (int i = 0; i < kGrid; ++i) placed += hid[i] != i % nx;
+        const int b = nx > 1 ? 1 : 0, c2 = nx > 2 ? 2 : 0;
+        for (int it = 1; it <= trials && rc == TMS_OK; ++it) {
+            uint64_t sum = 0;
+            // (a) XCD b caches the line; XCD 0 writes it; XCD b reads it again
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            hipLaunchKernelGGL(tms::line_read, dim3(kGrid), dim3(64), 0, s, line, b, claim, out);
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            hipLaunchKernelGGL(tms::line_write, dim3(kGrid), dim3(64), 0, s, line, (uint64_t)it, 0, 0, claim);
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            hipLaunchKernelGGL(tms::line_read, dim3(kGrid), dim3(64), 0, s, line, b, claim, out);
+            if (hipMemcpyAsync(&sum, out, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
+            stale += sum != 16ull * (uint64_t)it;
+            // (b) XCDs 0 and b write alternate words in one kernel; XCD c2 reads
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            hipLaunchKernelGGL(tms::line_write, dim3(kGrid), dim3(64), 0, s, line, (uint64_t)it + 1000000, 0, b, claim);
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            hipLaunchKernelGGL(tms::line_read, dim3(kGrid), dim3(64), 0, s, line, c2, claim, out);
+            if (hipMemcpyAsync(&sum, out, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
+            lost += sum != 16ull * ((uint64_t)it + 1000000);
+        }
+        // (c) back-to-back kernels
+        if (rc == TMS_OK) {
+            (void)hipMemsetAsync(ctr, 0, sizeof(unsigned), s);
+            (void)hipMemsetAsync(bad, 0, sizeof(int), s);
+            for (int it = 0; it < trials; ++it) {
+                hipLaunchKernelGGL(tms::count_in, dim3(1024), dim3(64), 0, s, ctr, 1 + (it % 7) * 20);
+                hipLaunchKernelGGL(tms::count_seen, dim3(8), dim3(64), 0, s, ctr, 1024u, bad);
+            }
+            if (hipMemcpyAsync(&overlap, bad, sizeof(int), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
+        }
+    }
+    if (hipGetLastError() != hipSuccess) rc = TMS_ERR_HIP;
+    counts[0] = stale;
+    counts[1] = lost;
+    counts[2] = overlap;
+    counts[3] = placed;
+    counts[4] = nx;
+    if (s) (void)hipStreamDestroy(s);
+    for (void* q : {(void*)line, (void*)out, (void*)claim, (void*)ids, (void*)bad, (void*)ctr})
+        if (q) (void)hipFree(q);
+    return rc;
+}
 
 extern "C" int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipStream_t stream) {
     if (!in6 || !out4 || n < 0) return TMS_ERR_INVALID_ARG;

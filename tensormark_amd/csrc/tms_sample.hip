@@ -1031,6 +1031,8 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->tlists = (uint64_t*)(p + off_tl);
     ctx->spec_zparts = (uint64_t*)(p + off_zp);
     ctx->dqueue = (uint32_t*)(p + off_dq);
+    ctx->ones_begin = off_ones;
+    ctx->ones_end = off_l;
     (void)hipSetDevice(prev);
     *out = ctx;
     return TMS_OK;
@@ -1050,6 +1052,16 @@ extern "C" int tms_destroy(tms_context* ctx) {
 
 extern "C" size_t tms_workspace_bytes(const tms_context* ctx) {
     return ctx ? ctx->bytes + ctx->dense_bytes : 0;
+}
+
+// Zero every workspace word the cross-workgroup protocols expect at zero
+// (counters, tickets, list and part words, the queue), keeping the all-ones
+// mask row.  For recovery after a TMS_ROW_INTERNAL row, whose late words
+// may otherwise be taken as the next call's.
+static int reset_regions(void* ws, size_t ones_begin, size_t ones_end, size_t bytes, hipStream_t stream) {
+    if (hipMemsetAsync(ws, 0, ones_begin, stream) != hipSuccess) return TMS_ERR_HIP;
+    if (hipMemsetAsync((char*)ws + ones_end, 0, bytes - ones_end, stream) != hipSuccess) return TMS_ERR_HIP;
+    return TMS_OK;
 }
 
 // Compute units of the current device (looked up once per device).
@@ -1244,6 +1256,25 @@ constexpr int kNoAllocMaxDevices = 64;
 std::mutex g_noalloc_mu;
 uint64_t* g_noalloc_scratch[kNoAllocMaxDevices];   // device address of `scratch`, per device
 }  // namespace
+
+extern "C" int tms_workspace_reset(tms_context* ctx, hipStream_t stream) {
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return TMS_ERR_NO_DEVICE;
+    if (!ctx) {
+        // the allocation-free entry point's scratch on the current device
+        uint64_t* base = nullptr;
+        {
+            std::lock_guard<std::mutex> lock(g_noalloc_mu);
+            if (prev >= 0 && prev < kNoAllocMaxDevices) base = g_noalloc_scratch[prev];
+        }
+        if (!base) return TMS_OK;   // never used on this device: still zero
+        return reset_regions(base, kNaOnes * 8, kNaDense * 8, kNaDense * 8, stream);
+    }
+    if (hipSetDevice(ctx->device) != hipSuccess) return TMS_ERR_HIP;
+    const int rc = reset_regions(ctx->ws, ctx->ones_begin, ctx->ones_end, ctx->bytes, stream);
+    (void)hipSetDevice(prev);
+    return rc;
+}
 
 extern "C" int tms_sample_batch_noalloc(const tms_sample_args* a, hipStream_t stream) {
     if (!a) return TMS_ERR_INVALID_ARG;

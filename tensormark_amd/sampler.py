@@ -37,6 +37,8 @@ EXPORTS = (
     "tms_sample_batch",
     "tms_sample_batch_noalloc",
     "tms_spec_verify",
+    "tms_workspace_reset",
+    "tms_debug_ordering",
     "tms_debug_philox",
     "tms_debug_exp",
     "tms_host_repeat_penalty",
@@ -169,6 +171,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         lib.tms_sample_batch_noalloc.argtypes = [C.POINTER(SampleArgs), C.c_void_p]
         lib.tms_spec_verify.argtypes = [C.c_void_p, C.POINTER(SpecArgs), C.c_void_p]
         lib.tms_debug_philox.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+        lib.tms_debug_ordering.argtypes = [C.c_int, C.POINTER(C.c_int32)]
+        lib.tms_workspace_reset.argtypes = [C.c_void_p, C.c_void_p]
         lib.tms_debug_exp.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p]
         fp, ip = C.POINTER(C.c_float), C.POINTER(C.c_int32)
         lib.tms_host_repeat_penalty.argtypes = [fp, C.c_int, ip, C.c_int, C.c_int, C.c_float]
@@ -258,6 +262,14 @@ class Sampler:
             self.close()
         except Exception:
             pass
+
+    def reset_workspace(self, stream=None) -> None:
+        """Return the workspace to its creation state (zeroed counters and
+        lists, all-ones mask row) on ``stream``.  Recovery after a call that
+        reported TMS_ROW_INTERNAL; not for use inside graph capture."""
+        import torch
+        s = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
+        _check(self.lib.tms_workspace_reset(self.handle, C.c_void_p(s)), "tms_workspace_reset")
 
     @property
     def workspace_bytes(self) -> int:
