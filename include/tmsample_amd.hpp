@@ -106,6 +106,7 @@ public:
         hip(hipMalloc(&d_recent_, sizeof(int32_t) * kMaxHistory), "hipMalloc");
         hip(hipMalloc(&d_mask_, sizeof(uint32_t) * words), "hipMalloc");
         hip(hipMalloc(&d_small_, 256), "hipMalloc");
+        hip(hipMalloc(&d_breaker_, static_cast<size_t>(max_vocab)), "hipMalloc");
         hip(hipStreamCreate(&stream_), "hipStreamCreate");
         (void)hipSetDevice(prev);
         max_vocab_ = max_vocab;
@@ -115,7 +116,7 @@ public:
         (void)hipGetDevice(&prev);
         (void)hipSetDevice(device_);
         if (stream_) (void)hipStreamDestroy(stream_);
-        for (void* p : {d_logits_, d_recent_, d_mask_, d_small_})
+        for (void* p : {d_logits_, d_recent_, d_mask_, d_small_, d_breaker_})
             if (p) (void)hipFree(p);
         (void)hipSetDevice(prev);
         if (ctx_) (void)tms_destroy(ctx_);
@@ -137,25 +138,29 @@ public:
     }
 
     // sample_token (tensormark/llama_chat.cpp:146-153): repetition penalty,
-    // n-gram ban, DRY, then sample.  With the ban and DRY off, the penalty
-    // runs on the GPU from the uploaded window; otherwise all three run here
-    // in the reference's order and the GPU samples the result.  `mask`
-    // (nullable, ceil(V / 32) words, bit id & 31 of word id >> 5) restricts
-    // the row first, as GrammarFilter::restrict does (llama_chat.cpp:184-209).
+    // n-gram ban, DRY, then sample, all on the GPU.  `mask` (nullable,
+    // ceil(V / 32) words, bit id & 31 of word id >> 5) restricts the row
+    // first, as GrammarFilter::restrict does (llama_chat.cpp:184-209).  With
+    // the ban and DRY off only the repetition window is uploaded; otherwise
+    // the whole history (its last 65535 ids) and the breaker table go up and
+    // the library's history pre-pass runs.  Unlike the reference, `logits`
+    // is left as it was.
     [[nodiscard]] int sample_token(std::vector<float>& logits, int V, const ChatOpts& o,
                                    bool greedy, std::mt19937& rng, const int* recent,
                                    int n_recent, const uint32_t* mask = nullptr) {
         tms_row_params p = row_params(o.temperature, o.top_k, o.top_p, greedy);
-        const bool host_chain = o.no_repeat_ngram >= 2 || o.dry.multiplier > 0.0f;
-        if (host_chain) {
-            if (mask) apply_mask(logits, mask);
-            apply_repeat_penalty(logits, recent, n_recent, o.repeat_last_n, o.repeat_penalty);
-            apply_no_repeat_ngram(logits, recent, n_recent, o.no_repeat_ngram);
-            apply_dry(logits, recent, n_recent, o.dry, o.dry_breaker);
-            return run_row(logits.data(), V, p, nullptr, 0, nullptr, greedy, rng);
-        }
         p.repeat_penalty = o.repeat_penalty;
         p.repeat_last_n = o.repeat_last_n;
+        if (o.no_repeat_ngram >= 2 || o.dry.multiplier > 0.0f) {
+            tms_history_params h{};
+            h.no_repeat_ngram = o.no_repeat_ngram;
+            h.dry_multiplier = o.dry.multiplier;
+            h.dry_base = o.dry.base;
+            h.dry_allowed_length = o.dry.allowed_length;
+            h.dry_penalty_last_n = o.dry.penalty_last_n;
+            return run_row(logits.data(), V, p, recent, n_recent, mask, greedy, rng, &h,
+                           o.dry_breaker);
+        }
         // Only the window reaches the device.
         const int from = std::max(0, n_recent - std::max(0, o.repeat_last_n));
         return run_row(logits.data(), V, p, recent + from, n_recent - from, mask, greedy, rng);
@@ -194,7 +199,8 @@ private:
     }
 
     int run_row(const float* logits, int V, const tms_row_params& p, const int* recent, int n_recent,
-                const uint32_t* mask, bool greedy, std::mt19937& rng) {
+                const uint32_t* mask, bool greedy, std::mt19937& rng,
+                const tms_history_params* hist = nullptr, const unsigned char* breaker = nullptr) {
         if (V <= 0 || V > max_vocab_) throw Error("row wider than the sampler's vocabulary", TMS_ERR_CAPACITY);
         if (n_recent > kMaxHistory) {
             recent += n_recent - kMaxHistory;
@@ -213,9 +219,12 @@ private:
         }
         struct Small {
             tms_row_params params;
+            tms_history_params hist;
             uint32_t draws[2];
             int32_t n_recent, token, status, keep;
         } h{};
+        static_assert(sizeof(Small) <= 256, "d_small_ holds 256 bytes");
+        if (hist) h.hist = *hist;
         h.params = p;
         h.draws[0] = words[0];
         h.draws[1] = words[1];
@@ -229,6 +238,9 @@ private:
         if (mask)
             hip(hipMemcpyAsync(d_mask_, mask, sizeof(uint32_t) * ((static_cast<size_t>(V) + 31) / 32),
                                hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+        if (hist && breaker)
+            hip(hipMemcpyAsync(d_breaker_, breaker, static_cast<size_t>(V), hipMemcpyHostToDevice, stream_),
+                "hipMemcpyAsync");
         hip(hipMemcpyAsync(d, &h, sizeof(h), hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
         tms_sample_args a{};
         a.logits = d_logits_;
@@ -246,6 +258,8 @@ private:
         a.out_tokens = &d->token;
         a.out_status = &d->status;
         a.out_keep = &d->keep;
+        a.history = hist ? &d->hist : nullptr;
+        a.dry_breaker = (hist && breaker) ? static_cast<const uint8_t*>(d_breaker_) : nullptr;
         // The row is known here: a greedy or top-k <= 128 row may take the
         // library's top-k kernel.
         a.row_kinds = (h.params.greedy != 0 || (h.params.top_k >= 1 && h.params.top_k <= 128))
@@ -276,6 +290,7 @@ private:
     void* d_recent_ = nullptr;
     void* d_mask_ = nullptr;
     void* d_small_ = nullptr;
+    void* d_breaker_ = nullptr;
     hipStream_t stream_ = nullptr;
 };
 

@@ -23,6 +23,17 @@
  *   2. repetition penalty over the last repeat_last_n ids of the row's
  *      history, compounding once per occurrence (v > 0 ? v / p : v * p);
  *   3. frequency/presence penalty: v -= (float)count * freq + presence;
+ *   3a. (with `history`) no-repeat n-gram ban, tensormark/tmsample.h:81-114:
+ *      every id that followed an earlier occurrence of the row's last
+ *      ngram - 1 ids becomes -inf, unless that leaves no value above -inf
+ *      (then the banned ids keep their step-3 values);
+ *   3b. (with `history`) DRY, tensormark/tmsample.h:148-170: for each
+ *      earlier position of the last penalty_last_n ids whose run agrees with
+ *      the tail for L >= allowed_length ids (never across a breaker id), the
+ *      id that followed it loses multiplier * base^(L - allowed_length), in
+ *      position order (base^k by binary powering in double and one rounding
+ *      to float; glibc's powf, which the reference calls, differs from it by
+ *      1 ulp for about 0.1% of (base, k) pairs);
  *   4. greedy: the first maximum (lowest id) of the penalised row;
  *   5. otherwise lg = v / temperature (fp32 division), top-k by
  *      (lg descending, id ascending), pr = exp((double)lg - (double)lg_max)
@@ -45,7 +56,7 @@
 extern "C" {
 #endif
 
-#define TMS_ABI_VERSION 2
+#define TMS_ABI_VERSION 3
 
 /* Return codes of the entry points. */
 enum {
@@ -64,7 +75,8 @@ enum {
     TMS_ROW_NONFINITE = 3,    /* NaN or +inf after masking, or lg overflowed */
     TMS_ROW_UNSUPPORTED = 4,  /* a row that breaks the TMS_ROWS_TOPK promise (top_k = 0
                                  or > 128, not greedy) in a call that runs no whole-row
-                                 pass; never produced under TMS_ROWS_ANY */
+                                 pass; or, with `history`, a row whose history touches
+                                 more than TMS_HISTORY_MAX_IDS distinct ids */
     TMS_ROW_INTERNAL = 5      /* a chunk list never arrived (bounded wait expired) */
 };
 
@@ -103,6 +115,26 @@ typedef struct tms_row_params {
     uint64_t seed;            /* Philox4x32-10 key */
     uint64_t offset;          /* Philox4x32-10 counter words 0 and 1 */
 } tms_row_params;
+
+/* Most distinct ids the history steps (2, 3, 3a, 3b) of one row may touch. */
+#define TMS_HISTORY_MAX_IDS 4096
+
+/*
+ * Per-row n-gram ban and DRY settings (tms_sample_args.history).
+ * no_repeat_ngram is ChatOpts::no_repeat_ngram, the `ngram` argument of
+ * apply_no_repeat_ngram (tensormark/tmsample.h:81-82); the dry_* fields are
+ * tmsample::DryOpts (tensormark/tmsample.h:141-146) field for field.  The
+ * sequence-breaker table (apply_dry's `is_breaker`) is shared by the batch:
+ * tms_sample_args.dry_breaker.
+ */
+typedef struct tms_history_params {
+    int32_t no_repeat_ngram;      /* < 2 disables */
+    float dry_multiplier;         /* <= 0 disables */
+    float dry_base;               /* DryOpts default 1.75 */
+    int32_t dry_allowed_length;   /* < 1 disables; DryOpts default 2 */
+    int32_t dry_penalty_last_n;   /* DryOpts default 256 */
+    int32_t reserved;             /* must be 0 */
+} tms_history_params;
 
 /* Opaque context: owns the device workspace for one device. */
 typedef struct tms_context tms_context;
@@ -144,6 +176,13 @@ typedef struct tms_sample_args {
                                  promise gets TMS_ROW_UNSUPPORTED, never a wrong
                                  sample */
     uint32_t reserved;        /* must be 0 */
+    const tms_history_params* history;   /* device, [batch], nullable: steps 3a and 3b
+                                            (then every row's history steps 2-3b run
+                                            in a pre-pass and the general kernel
+                                            samples, whatever row_kinds says) */
+    const uint8_t* dry_breaker;          /* device, [vocab], nullable: non-zero marks a
+                                            DRY sequence breaker; ids outside
+                                            [0, vocab) are not breakers */
 } tms_sample_args;
 
 typedef struct tms_spec_args {
@@ -239,8 +278,9 @@ int tms_spec_verify(tms_context* ctx, const tms_spec_args* args, hipStream_t str
 
 /*
  * The history transforms on a host row of V fp32 logits, in place, for
- * callers that run them before upload (rows with the n-gram ban or DRY on;
- * the device applies the repetition penalty itself from the window).
+ * host-side callers (the device runs them itself with
+ * tms_sample_args.history).  tms_host_dry computes base^k as the device
+ * does.
  *   tms_host_repeat_penalty   tmsample::apply_repeat_penalty  (tensormark/tmsample.h:52-63)
  *   tms_host_no_repeat_ngram  tmsample::apply_no_repeat_ngram (tensormark/tmsample.h:81-114)
  *   tms_host_dry              tmsample::apply_dry             (tensormark/tmsample.h:148-170),

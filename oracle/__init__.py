@@ -59,6 +59,17 @@ ROW_DTYPE = np.dtype(
 )
 assert ROW_DTYPE.itemsize == C.sizeof(RowParams) == 56
 
+HISTORY_DTYPE = np.dtype(
+    [
+        ("no_repeat_ngram", "<i4"),
+        ("dry_multiplier", "<f4"),
+        ("dry_base", "<f4"),
+        ("dry_allowed_length", "<i4"),
+        ("dry_penalty_last_n", "<i4"),
+        ("reserved", "<i4"),
+    ]
+)
+
 
 def build() -> None:
     """Compile the checkers (oracle/_ref only where the reference tree exists)."""
@@ -140,6 +151,22 @@ class Oracle:
                                          C.c_float(freq), C.c_float(presence))
         return row
 
+    def no_repeat_ngram(self, row, recent, ngram):
+        row = np.ascontiguousarray(row, np.float32).copy()
+        r = np.ascontiguousarray(recent, np.int32)
+        self.lib.tmo_no_repeat_ngram(_p(row, C.c_float), C.c_int(row.size), _p(r, C.c_int32),
+                                     C.c_int(r.size), C.c_int(ngram))
+        return row
+
+    def dry(self, row, recent, multiplier, base, allowed_length, penalty_last_n, is_breaker=None):
+        row = np.ascontiguousarray(row, np.float32).copy()
+        r = np.ascontiguousarray(recent, np.int32)
+        brk = None if is_breaker is None else np.ascontiguousarray(is_breaker, np.uint8)
+        self.lib.tmo_dry(_p(row, C.c_float), C.c_int(row.size), _p(r, C.c_int32), C.c_int(r.size),
+                         C.c_float(multiplier), C.c_float(base), C.c_int(allowed_length),
+                         C.c_int(penalty_last_n), _p(brk, C.c_uint8))
+        return row
+
     def sample_row(self, row, params: RowParams, w0, w1, topk_cap=0):
         row = np.ascontiguousarray(row, np.float32)
         tok, keep = C.c_int32(), C.c_int32()
@@ -152,8 +179,9 @@ class Oracle:
         return st, tok.value, keep.value, ids[:topk_cap], probs[:topk_cap]
 
     def sample_batch(self, logits, params, recent=None, n_recent=None, mask=None, draws=None,
-                     topk_cap=0):
-        """logits: float32 [B, V]; params: ROW_DTYPE [B].  Returns a dict."""
+                     topk_cap=0, history=None, dry_breaker=None):
+        """logits: float32 [B, V]; params: ROW_DTYPE [B]; history: HISTORY_DTYPE
+        [B] or None (then no n-gram ban or DRY).  Returns a dict."""
         logits = np.ascontiguousarray(logits, np.float32)
         B, V = logits.shape
         params = np.ascontiguousarray(params, ROW_DTYPE)
@@ -175,9 +203,13 @@ class Oracle:
         cap = max(topk_cap, 1)
         ids = np.full((B, cap), -1, np.int32)
         probs = np.zeros((B, cap), np.float32)
-        self.lib.tmo_sample_batch(
+        hp = None if history is None else np.ascontiguousarray(history, HISTORY_DTYPE)
+        brk = None if dry_breaker is None else np.ascontiguousarray(dry_breaker, np.uint8)
+        self.lib.tmo_sample_batch_h(
             _p(logits, C.c_float), C.c_int(B), C.c_int(V), C.c_int64(V),
-            params.ctypes.data_as(C.c_void_p), _p(recent, C.c_int32), _p(n_recent, C.c_int32),
+            params.ctypes.data_as(C.c_void_p),
+            None if hp is None else hp.ctypes.data_as(C.c_void_p), _p(brk, C.c_uint8),
+            _p(recent, C.c_int32), _p(n_recent, C.c_int32),
             C.c_int64(rs), _p(mask, C.c_uint32), C.c_int64(ms), _p(draws, C.c_uint32),
             _p(tokens, C.c_int32), _p(status, C.c_int32), _p(keep, C.c_int32),
             _p(ids, C.c_int32), _p(probs, C.c_float), C.c_int(topk_cap))

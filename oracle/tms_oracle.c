@@ -17,6 +17,12 @@
  *   tmo_apply_freq_presence closed form v - (c*freq + presence); brute force.
  *                           No reference counterpart: parity unpinned by the
  *                           reference, pinned by the closed form only.
+ *   tmo_no_repeat_ngram, tmo_dry  the reference's own outputs: committed golden
+ *                           vectors of the compiled tmsample.h
+ *                           (tests/golden/history_golden.npz), oracle/_ref on
+ *                           random histories, closed forms.
+ *   tmo_sample_batch_h      composition of the pinned steps in sample_token's
+ *                           order (llama_chat.cpp:148-151).
  *   tmo_sample_row          compiled reference tmsample::sample (oracle/_ref) on
  *                           tie-free rows (token, keep); committed golden vectors
  *                           (tests/golden/); brute-force enumeration on tiny V.
@@ -124,6 +130,64 @@ void tmo_apply_freq_presence(float* row, int V, const int32_t* recent, int n_rec
             row[i] = row[i] - t;
         }
     free(cnt);
+}
+
+/* tmsample::apply_no_repeat_ngram (tensormark/tmsample.h:81-114): the id
+ * after each earlier occurrence of the last ngram - 1 ids becomes -inf (its
+ * value saved the first time); when the row's std::max scan from -inf then
+ * finds nothing above -inf, the saved values go back. */
+void tmo_no_repeat_ngram(float* row, int V, const int32_t* recent, int n_recent, int ngram) {
+    if (ngram < 2 || n_recent < ngram) return;
+    const int m = ngram - 1, s = n_recent - m;
+    int* bid = (int*)malloc((size_t)s * sizeof(int) + 1);
+    float* bv = (float*)malloc((size_t)s * sizeof(float) + 1);
+    int nb = 0;
+    for (int i = 0; i < s; ++i) {
+        int k = 0;
+        while (k < m && recent[i + k] == recent[s + k]) ++k;
+        if (k < m) continue;
+        const int t = recent[i + m];
+        if (t < 0 || t >= V) continue;
+        if (row[t] == -INFINITY) continue;
+        bid[nb] = t;
+        bv[nb] = row[t];
+        ++nb;
+        row[t] = -INFINITY;
+    }
+    if (nb > 0) {
+        float best = -INFINITY;
+        for (int i = 0; i < V; ++i) best = (best < row[i]) ? row[i] : best;   /* std::max */
+        if (best == -INFINITY)
+            for (int j = 0; j < nb; ++j) row[bid[j]] = bv[j];
+    }
+    free(bid);
+    free(bv);
+}
+
+/* tmsample::apply_dry (tensormark/tmsample.h:148-170), with the reference's
+ * powf.  Breaker lookups of ids outside [0, V) read as "not a breaker" (the
+ * reference indexes is_breaker with them unchecked). */
+static int tmo_brk(const uint8_t* brk, int V, int id) { return brk && id >= 0 && id < V && brk[id]; }
+
+void tmo_dry(float* row, int V, const int32_t* recent, int n_recent, float multiplier, float base,
+             int allowed_length, int penalty_last_n, const uint8_t* is_breaker) {
+    if (multiplier <= 0.0f || allowed_length < 1) return;
+    if (n_recent < allowed_length + 1) return;
+    const int n = n_recent < penalty_last_n ? n_recent : penalty_last_n;
+    if (n < allowed_length + 1) return;
+    const int32_t* s = recent + (n_recent - n);
+    const int last = n - 1;
+    for (int i = 0; i < last; ++i) {
+        int L = 0;
+        while (L <= i && s[i - L] == s[last - L] &&
+               !(tmo_brk(is_breaker, V, s[i - L]) || tmo_brk(is_breaker, V, s[last - L])))
+            ++L;
+        if (L < allowed_length) continue;
+        const int nxt = s[i + 1];
+        if (nxt < 0 || nxt >= V) continue;
+        if (tmo_brk(is_breaker, V, nxt)) continue;
+        row[nxt] -= multiplier * powf(base, (float)(L - allowed_length));
+    }
 }
 
 /* --------------------------------------------------------------- sampling */
@@ -294,6 +358,63 @@ void tmo_sample_batch(const float* logits, int B, int V, int64_t row_stride,
                                    topk_ids ? topk_ids + (int64_t)b * topk_cap : NULL,
                                    topk_probs ? topk_probs + (int64_t)b * topk_cap : NULL,
                                    topk_cap);
+        if (keep) keep[b] = kp;
+    }
+    free(row);
+}
+
+/* sample_token with the grammar restriction in front (llama_chat.cpp:
+ * 787-791, then 148-151): mask, repetition penalty, frequency/presence,
+ * n-gram ban, DRY, sample.  A NaN or +inf left by the mask makes the row
+ * ROW_NONFINITE whatever the history steps do to it (the library's row
+ * contract).  hp may be NULL (then this is tmo_sample_batch). */
+void tmo_sample_batch_h(const float* logits, int B, int V, int64_t row_stride,
+                        const tmo_row_params* params, const tmo_history_params* hp,
+                        const uint8_t* breaker, const int32_t* recent, const int32_t* n_recent,
+                        int64_t recent_stride, const uint32_t* mask, int64_t mask_stride,
+                        const uint32_t* draws, int32_t* tokens, int32_t* status, int32_t* keep,
+                        int32_t* topk_ids, float* topk_probs, int topk_cap) {
+    float* row = (float*)malloc((size_t)V * sizeof(float));
+    for (int b = 0; b < B; ++b) {
+        const tmo_row_params* p = &params[b];
+        memcpy(row, logits + (int64_t)b * row_stride, (size_t)V * sizeof(float));
+        if (mask) tmo_apply_mask(row, V, mask + (int64_t)b * mask_stride);
+        int nonfinite = 0;
+        for (int i = 0; i < V; ++i) nonfinite |= isnan(row[i]) || row[i] == INFINITY;
+        if (recent) {
+            const int32_t* r = recent + (int64_t)b * recent_stride;
+            int n = n_recent ? n_recent[b] : (int)recent_stride;
+            if (n > (int)recent_stride) n = (int)recent_stride;
+            if (n < 0) n = 0;
+            tmo_apply_repeat_penalty(row, V, r, n, p->repeat_last_n, p->repeat_penalty);
+            tmo_apply_freq_presence(row, V, r, n, p->repeat_last_n, p->frequency_penalty,
+                                    p->presence_penalty);
+            if (hp) {
+                tmo_no_repeat_ngram(row, V, r, n, hp[b].no_repeat_ngram);
+                tmo_dry(row, V, r, n, hp[b].dry_multiplier, hp[b].dry_base,
+                        hp[b].dry_allowed_length, hp[b].dry_penalty_last_n, breaker);
+            }
+        }
+        uint32_t w0, w1;
+        if (draws) {
+            w0 = draws[2 * b];
+            w1 = draws[2 * b + 1];
+        } else {
+            tmo_row_words(p->seed, p->offset, 0u, &w0, &w1);
+        }
+        int32_t kp = 0;
+        int32_t* ids = topk_ids ? topk_ids + (int64_t)b * topk_cap : NULL;
+        float* probs = topk_probs ? topk_probs + (int64_t)b * topk_cap : NULL;
+        status[b] = tmo_sample_row(row, V, p, w0, w1, &tokens[b], &kp, ids, probs, topk_cap);
+        if (nonfinite && status[b] != ROW_BAD_PARAMS) {
+            status[b] = ROW_NONFINITE;
+            tokens[b] = -1;
+            kp = 0;
+            for (int j = 0; j < topk_cap; ++j) {
+                if (ids) ids[j] = -1;
+                if (probs) probs[j] = 0.0f;
+            }
+        }
         if (keep) keep[b] = kp;
     }
     free(row);

@@ -6,12 +6,15 @@ Python host side over it.
 """
 from .sampler import (  # noqa: F401
     EXPORTS,
+    HISTORY_DTYPE,
     Opts,
     RowParams,
     ROW_DTYPE,
     Sampler,
     load_library,
+    make_history,
     make_params,
 )
 
-__all__ = ["EXPORTS", "Opts", "RowParams", "ROW_DTYPE", "Sampler", "load_library", "make_params"]
+__all__ = ["EXPORTS", "HISTORY_DTYPE", "Opts", "RowParams", "ROW_DTYPE", "Sampler", "load_library",
+           "make_history", "make_params"]

@@ -45,6 +45,9 @@ struct tms_context {
     uint64_t* spec_zparts;     // [max_batch][2 * kSpecMaxK + 1][spec_chunks] chunk statistics, 2 words each
     int spec_chunks;           // ceil(max_vocab / 4096)
     uint32_t* dqueue;          // whole-row pass queue: 3 counters, then [max_batch] rows
+    int32_t* ov_n;             // [max_batch] history pre-pass: list lengths (-1: overflow)
+    int32_t* ov_ids;           // [max_batch][TMS_HISTORY_MAX_IDS] listed ids
+    float* ov_vals;            // [max_batch][TMS_HISTORY_MAX_IDS] their final values
     uint64_t* dense;           // [dense_slots][2 * max_vocab] the whole-row pass (separate allocation)
     int dense_slots;           // min(max_batch, kDenseGridMax): one region per pass workgroup
     size_t dense_bytes;

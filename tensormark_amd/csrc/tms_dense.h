@@ -225,12 +225,15 @@ __device__ __forceinline__ int dense_compact(const T* base, const uint32_t* mrow
     return n;
 }
 
-__device__ __forceinline__ void dense_count_window(uint32_t* C, int V, const int32_t* hist, int from, int nrec) {
+// Window counts per id; with `positions` (the history pre-pass's list of
+// distinct ids) the list position + 1 instead.
+__device__ __forceinline__ void dense_count_window(uint32_t* C, int V, const int32_t* hist, int from, int nrec,
+                                                   bool positions) {
     for (int i = threadIdx.x; i < V; i += kBlock) C[i] = 0u;
     dense_sync();
     for (int p = from + (int)threadIdx.x; p < nrec; p += kBlock) {
         const int id = hist[p];
-        if (id >= 0 && id < V) atomicAdd(&C[id], 1u);
+        if (id >= 0 && id < V) atomicAdd(&C[id], positions ? (uint32_t)(p + 1) : 1u);
     }
     dense_sync();
 }
@@ -285,18 +288,21 @@ __device__ __forceinline__ void dense_row(const KArgs& a, int row, tms_row_param
         nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
         if (nrec > (int)a.recent_stride) nrec = (int)a.recent_stride;
     }
+    nrec = max(nrec, 0);   // -1 (pre-pass overflow) never reaches this pass
+    const bool ovm = a.ov_vals != nullptr;
     Pen pn;
     pn.rep_on = !(P.repeat_penalty <= 1.0f);
     pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
-    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
+    pn.on = nrec > 0 && (ovm || (P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on)));
     pn.rep = P.repeat_penalty;
     pn.freq = P.frequency_penalty;
     pn.pres = P.presence_penalty;
+    if (ovm) pn.ov = a.ov_vals + (int64_t)row * kHistMax;
     // C shares its words with the sort's second half, so it is counted
     // again before each compaction.
-    const int from = nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0;
+    const int from = (!ovm && nrec > P.repeat_last_n) ? nrec - P.repeat_last_n : 0;
     const int32_t* hist = a.recent + (int64_t)row * a.recent_stride;
-    if (pn.on) dense_count_window(C, V, hist, from, nrec);
+    if (pn.on) dense_count_window(C, V, hist, from, nrec, ovm);
     const float temp = P.temperature;
     const bool divide = temp != 1.0f;
     // ---- the row maximum of lg
@@ -317,7 +323,7 @@ __device__ __forceinline__ void dense_row(const KArgs& a, int row, tms_row_param
 
     for (int pass = 0; pass < 2; ++pass) {
         const bool all = pass == 1;
-        if (all && pn.on) dense_count_window(C, V, hist, from, nrec);
+        if (all && pn.on) dense_count_window(C, V, hist, from, nrec, ovm);
         const int n = dense_compact(base, mrow, C, V, pn, temp, divide, mx, all, A, L);
         const uint64_t* S = dense_sort(A, B, n, L);
         double* pr = (double*)(S == A ? B : A);   // the other half

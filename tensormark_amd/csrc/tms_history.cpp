@@ -1,11 +1,10 @@
 // tms_history.cpp -- the deterministic history transforms of TensorMark's
 // sampler on a host row: repetition penalty, no-repeat n-gram ban and DRY.
 //
-// They run on the host, before a row is uploaded, for callers that enable
-// the n-gram ban or DRY (the device sampler applies the repetition penalty
-// itself from the window, but DRY's logit shift must follow it, so a row
-// with DRY or a ban goes through all three here in the reference's order:
-// tensormark/llama_chat.cpp:146-153).
+// Host-side forms of what the device pre-pass (tms_hist.hip) does for
+// tms_sample_args.history, for callers that hold a host row; the order of
+// the reference's sample_token is theirs to keep
+// (tensormark/llama_chat.cpp:146-153).
 
 #include <math.h>
 #include <stdint.h>
@@ -15,6 +14,7 @@
 #include <vector>
 
 #include "../../include/tmsample_hip.h"
+#include "tms_history.h"
 
 // tensormark/tmsample.h:52-63: v > 0 ? v / p : v * p, once per occurrence.
 extern "C" void tms_host_repeat_penalty(float* logits, int V, const int32_t* recent, int n_recent,
@@ -47,8 +47,9 @@ extern "C" void tms_host_no_repeat_ngram(float* logits, int V, const int32_t* re
         logits[next] = ninf;
     }
     if (undo.empty()) return;
+    // the reference's std::max scan from -inf: a NaN never becomes the best
     for (int i = 0; i < V; ++i)
-        if (logits[i] > ninf || logits[i] != logits[i]) return;   // something is left
+        if (logits[i] > ninf) return;   // something is left
     for (const auto& u : undo) logits[u.first] = u.second;
 }
 
@@ -73,6 +74,6 @@ extern "C" void tms_host_dry(float* logits, int V, const int32_t* recent, int n_
         const int next = w[i + 1];
         if (next < 0 || next >= V) continue;
         if (is_breaker && is_breaker[next]) continue;
-        logits[next] -= multiplier * powf(base, (float)(L - allowed_length));
+        logits[next] -= multiplier * tms_dry_scale(base, L - allowed_length);
     }
 }

@@ -80,6 +80,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         nrec = a.n_recent ? a.n_recent[row] : (int)a.recent_stride;
         if (nrec > (int)a.recent_stride) nrec = (int)a.recent_stride;
     }
+    // With the history pre-pass the window is its list; -1: the row touched
+    // more ids than the list holds.
+    const bool ovm = a.ov_vals != nullptr;
+    const bool hist_over = ovm && nrec < 0;
+    nrec = max(nrec, 0);
     __builtin_amdgcn_sched_barrier(0);
     const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
     const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
@@ -110,11 +115,12 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     Pen pn;
     pn.rep_on = !(P.repeat_penalty <= 1.0f);
     pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
-    pn.on = nrec > 0 && P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on);
+    pn.on = nrec > 0 && (ovm || (P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on)));
     pn.rep = P.repeat_penalty;
     pn.freq = P.frequency_penalty;
     pn.pres = P.presence_penalty;
-    const int from = pn.on ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
+    if (ovm) pn.ov = a.ov_vals + (int64_t)row * kHistMax;
+    const int from = (pn.on && !ovm) ? (nrec > P.repeat_last_n ? nrec - P.repeat_last_n : 0) : 0;
     const bool pen_own = pn.on && nrec <= kWin * kBlock;
     if (pn.on) {
         uint4* c4 = (uint4*)sm.big.cnt;
@@ -141,7 +147,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             own_m[i] = mrow[(e0 + off) >> 5];
             if (in) {
                 const uint32_t sh = (off & 1) * 16;
-                const uint32_t old = atomicAdd(&sm.big.cnt[off >> 1], 1u << sh);
+                const uint32_t add = ovm ? (uint32_t)(p + 1) : 1u;   // list position + 1, or a count
+                const uint32_t old = atomicAdd(&sm.big.cnt[off >> 1], add << sh);
                 if (((old >> sh) & 0xFFFFu) == 0) {
                     own_off[i] = off;
                     const int vv = off / VEC;
@@ -235,7 +242,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                 const int id = (p < from || p >= nrec) ? -1 : (p0 == 0 ? wid[i] : hist[p]);
                 if (id >= e0 && id < e1) {
                     const int off = id - e0;
-                    atomicAdd(&sm.big.cnt[off >> 1], 1u << ((off & 1) * 16));
+                    const uint32_t add = ovm ? (uint32_t)(p + 1) : 1u;
+                    atomicAdd(&sm.big.cnt[off >> 1], add << ((off & 1) * 16));
                 }
             }
         }
@@ -720,6 +728,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     const int fo = sm.misc[4];
     int status = TMS_ROW_OK;
     if (sm.misc[3]) status = TMS_ROW_INTERNAL;
+    else if (hist_over) status = TMS_ROW_UNSUPPORTED;
     else if (bad_params) status = TMS_ROW_BAD_PARAMS;
     else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
     else if (N == 0 && !(fo & FLAG_OVERFLOW)) status = TMS_ROW_ALL_MASKED;   // an overflowed list holds 0
@@ -1001,7 +1010,10 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_zp = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
     ctx->spec_chunks = (max_vocab + 4095) / 4096;
     const size_t off_dq = off_zp + nb * (2 * tms::kSpecMaxK + 1) * (size_t)ctx->spec_chunks * 2 * sizeof(uint64_t);
-    ctx->bytes = off_dq + (tms::kDenseQueueHead + nb) * sizeof(uint32_t);
+    const size_t off_hn = off_dq + 256 * (((tms::kDenseQueueHead + nb) * sizeof(uint32_t) + 255) / 256);
+    const size_t off_hi = off_hn + 256 * ((nb * sizeof(int32_t) + 255) / 256);
+    const size_t off_hv = off_hi + nb * tms::kHistMax * sizeof(int32_t);
+    ctx->bytes = off_hv + nb * tms::kHistMax * sizeof(float);
     int rc = TMS_OK;
     if (hipMalloc(&ctx->ws, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;
     else if (hipMemset(ctx->ws, 0, ctx->bytes) != hipSuccess) rc = TMS_ERR_HIP;   // lists start zeroed
@@ -1031,6 +1043,9 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->tlists = (uint64_t*)(p + off_tl);
     ctx->spec_zparts = (uint64_t*)(p + off_zp);
     ctx->dqueue = (uint32_t*)(p + off_dq);
+    ctx->ov_n = (int32_t*)(p + off_hn);
+    ctx->ov_ids = (int32_t*)(p + off_hi);
+    ctx->ov_vals = (float*)(p + off_hv);
     ctx->ones_begin = off_ones;
     ctx->ones_end = off_l;
     (void)hipSetDevice(prev);
@@ -1088,6 +1103,9 @@ struct SampleWs {
     uint32_t* dqueue;
     uint64_t* dense;
     int dense_slots;
+    int32_t* ov_n;         // the history pre-pass's lists
+    int32_t* ov_ids;
+    float* ov_vals;
 };
 
 // tms_sample_batch over workspace w (a context's, or the allocation-free
@@ -1146,6 +1164,38 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
 #ifdef TMS_TRACE
     k.trace = g_tms_trace_host;
 #endif
+    if (a->history && a->recent) {
+        // The history pre-pass lists every row's touched ids with their
+        // final values; the general kernel and the whole-row pass take the
+        // list as the window (tms_hist.hip).
+        const int rc = tms_launch_history(k, a->history, a->dry_breaker, a->dtype, a->batch, w.ov_n,
+                                          w.ov_ids, w.ov_vals, stream);
+        if (rc != TMS_OK) return rc;
+        k.recent = w.ov_ids;
+        k.n_recent = w.ov_n;
+        k.recent_stride = tms::kHistMax;
+        k.ov_vals = w.ov_vals;
+        k.dense = w.dense;
+        const dim3 grid((unsigned)(a->batch * k.S)), block(tms::kBlock);
+#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F>), grid, block, 0, stream, k)
+        switch (a->dtype) {
+            case TMS_DTYPE_F32:
+                if (fast) TMS_LAUNCH(float, true);
+                else TMS_LAUNCH(float, false);
+                break;
+            case TMS_DTYPE_F16:
+                if (fast) TMS_LAUNCH(_Float16, true);
+                else TMS_LAUNCH(_Float16, false);
+                break;
+            default:
+                if (fast) TMS_LAUNCH(tms::Bf16, true);
+                else TMS_LAUNCH(tms::Bf16, false);
+                break;
+        }
+#undef TMS_LAUNCH
+        if (hipGetLastError() != hipSuccess) return TMS_ERR_HIP;
+        return tms_launch_dense(k, a->dtype, dense_grid, stream);
+    }
     if (a->row_kinds == TMS_ROWS_TOPK && (!a->recent || a->recent_stride <= tms::kWideMaxWindow)) {
         // Every row greedy or top-k <= 128 (the caller's promise): the wide
         // top-k kernel, S chunks of at most 4096 16-byte vectors, CE a
@@ -1218,6 +1268,9 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     w.dqueue = ctx->dqueue;
     w.dense = ctx->dense;
     w.dense_slots = ctx->dense_slots;
+    w.ov_n = ctx->ov_n;
+    w.ov_ids = ctx->ov_ids;
+    w.ov_vals = ctx->ov_vals;
     return sample_launch(w, a, stream);
 }
 
@@ -1244,9 +1297,12 @@ constexpr size_t kNaCounters = 0;
 constexpr size_t kNaLists = kNaCounters + align32((size_t)kNoAllocRows * tms::kCounterStride / 2);
 constexpr size_t kNaTlists = kNaLists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kListStride);
 constexpr size_t kNaQueue = kNaTlists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kTopkListStride);
-constexpr size_t kNaOnes = kNaQueue + align32((tms::kDenseQueueHead + kNoAllocRows + 1) / 2);
+constexpr size_t kNaHistN = kNaQueue + align32((tms::kDenseQueueHead + kNoAllocRows + 1) / 2);
+constexpr size_t kNaHistIds = kNaHistN + align32(kNoAllocRows / 2);
+constexpr size_t kNaHistVals = kNaHistIds + (size_t)kNoAllocRows * tms::kHistMax / 2;
+constexpr size_t kNaOnes = kNaHistVals + (size_t)kNoAllocRows * tms::kHistMax / 2;
 constexpr size_t kNaDense = kNaOnes + align32(kNoAllocVocab / 64);
-constexpr size_t kNaWords = kNaDense + 2 * (size_t)kNoAllocVocab;   // 18.9 MB
+constexpr size_t kNaWords = kNaDense + 2 * (size_t)kNoAllocVocab;   // 21.0 MB
 }  // namespace
 
 static __device__ __align__(256) uint64_t scratch[kNaWords];
@@ -1306,5 +1362,8 @@ extern "C" int tms_sample_batch_noalloc(const tms_sample_args* a, hipStream_t st
     w.dqueue = (uint32_t*)(base + kNaQueue);
     w.dense = base + kNaDense;
     w.dense_slots = 1;
+    w.ov_n = (int32_t*)(base + kNaHistN);
+    w.ov_ids = (int32_t*)(base + kNaHistIds);
+    w.ov_vals = (float*)(base + kNaHistVals);
     return sample_launch(w, a, stream);
 }

@@ -56,6 +56,7 @@ constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per lis
 constexpr int kReadRounds = 64;            // bound on the merger's re-reads of a sample
 constexpr int kDenseQueueHead = 64;        // u32 words before the whole-row queue's rows
 constexpr int kDenseGridMax = 256;         // workgroups of the whole-row pass
+constexpr int kHistMax = TMS_HISTORY_MAX_IDS; // ids one row's history pre-pass may list
 
 enum : int { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_TOPP = 2 };
 enum : int { FLAG_NONFINITE = 1, FLAG_OVERFLOW = 2 };
@@ -88,20 +89,29 @@ struct KArgs {
     int64_t dense_stride;  // >= V
     uint32_t* dqueue;      // [0] rows queued, [1] rows taken, [2] pass workgroups done,
                            // [kDenseQueueHead + i] the queued rows
+    const float* ov_vals;  // [B][kHistMax] the history pre-pass's values, with `recent`,
+                           // `n_recent` its id lists (n_recent -1: the row overflowed);
+                           // null when the call has no pre-pass
 #ifdef TMS_TRACE
     uint64_t* trace;
 #endif
 };
 
-// History penalties of one row.
+// History penalties of one row.  With `ov` (calls with the history
+// pre-pass) the window holds the pre-pass's list of distinct ids instead of
+// the history, each window word holds the id's list position + 1 instead of
+// a count, and ov[] holds the ids' final values.
 struct Pen {
     bool on, rep_on, fp_on;
     float rep, freq, pres;
+    const float* ov = nullptr;
 };
 
 // Repetition penalty applied `cnt` times (tmsample.h:61), then frequency and
-// presence: v -= (float)cnt * freq + presence.
+// presence: v -= (float)cnt * freq + presence.  With pn.ov, the pre-pass's
+// value of list entry cnt - 1.
 __device__ __forceinline__ float apply_pen(float v, uint32_t cnt, const Pen& pn) {
+    if (pn.ov) return pn.ov[cnt - 1];
     if (pn.rep_on)
         for (uint32_t r = 0; r < cnt; ++r) v = v > 0.f ? v / pn.rep : v * pn.rep;
     if (pn.fp_on) {
@@ -845,3 +855,6 @@ int tms_launch_topk(const tms::KArgs& k, int dtype, bool fast, int batch, hipStr
 int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
 // Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.
 int tms_launch_dense(const tms::KArgs& k, int dtype, int workgroups, hipStream_t stream);
+int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,
+                       int dtype, int batch, int32_t* ov_n, int32_t* ov_ids, float* ov_vals,
+                       hipStream_t stream);

@@ -94,6 +94,29 @@ ROW_DTYPE = np.dtype(
 assert ROW_DTYPE.itemsize == C.sizeof(RowParams) == 56
 
 
+HISTORY_DTYPE = np.dtype(
+    [
+        ("no_repeat_ngram", "<i4"), ("dry_multiplier", "<f4"), ("dry_base", "<f4"),
+        ("dry_allowed_length", "<i4"), ("dry_penalty_last_n", "<i4"), ("reserved", "<i4"),
+    ]
+)
+HISTORY_MAX_IDS = 4096   # TMS_HISTORY_MAX_IDS
+
+
+def make_history(B: int, *, no_repeat_ngram=0, dry_multiplier=0.0, dry_base=1.75,
+                 dry_allowed_length=2, dry_penalty_last_n=256) -> np.ndarray:
+    """A [B] HISTORY_DTYPE array (tms_history_params): the n-gram ban and
+    tmsample::DryOpts (tensormark/tmsample.h:141-146, same defaults);
+    scalars broadcast, arrays give per-row values."""
+    h = np.zeros(B, HISTORY_DTYPE)
+    h["no_repeat_ngram"] = no_repeat_ngram
+    h["dry_multiplier"] = dry_multiplier
+    h["dry_base"] = dry_base
+    h["dry_allowed_length"] = dry_allowed_length
+    h["dry_penalty_last_n"] = dry_penalty_last_n
+    return h
+
+
 @dataclasses.dataclass
 class Opts:
     """tmsample::Opts (tensormark/tmsample.h:31-35), same defaults."""
@@ -132,6 +155,7 @@ class SampleArgs(C.Structure):
         ("draws", C.c_void_p), ("out_tokens", C.c_void_p), ("out_status", C.c_void_p),
         ("out_keep", C.c_void_p), ("out_topk_ids", C.c_void_p), ("out_topk_probs", C.c_void_p),
         ("row_kinds", C.c_uint32), ("reserved", C.c_uint32),
+        ("history", C.c_void_p), ("dry_breaker", C.c_void_p),
     ]
 
 
@@ -280,7 +304,8 @@ class Sampler:
         return self.torch.from_numpy(raw.copy()).to(f"cuda:{self.device}")
 
     def sample(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
-               topk_cap: int = 0, out=None, stream=None, row_kinds=None, noalloc=False):
+               topk_cap: int = 0, out=None, stream=None, row_kinds=None, noalloc=False,
+               history=None, dry_breaker=None):
         """Sample one token per row of ``logits`` ([B, V] fp32/fp16/bf16, cuda).
 
         ``params`` is a device uint8 tensor from params_tensor() (or a numpy
@@ -289,7 +314,10 @@ class Sampler:
         numpy params (ROWS_ANY for device params), and a Sampler created with
         kernel="general" always passes ROWS_ANY.  ``noalloc`` takes the
         context-free entry point tms_sample_batch_noalloc (its static
-        workspace) instead of this context's.  Returns a dict of device
+        workspace) instead of this context's.  ``history`` (a
+        HISTORY_DTYPE array from make_history, or a device uint8 tensor of
+        one) turns on the n-gram ban and DRY, with ``dry_breaker`` an
+        optional device uint8 [V] breaker table.  Returns a dict of device
         tensors: tokens, status, keep, and topk_ids/topk_probs when
         topk_cap > 0.
         """
@@ -300,6 +328,9 @@ class Sampler:
                 row_kinds = row_kinds_of(params)
         if isinstance(params, np.ndarray):
             params = self.params_tensor(params)
+        if isinstance(history, np.ndarray):
+            raw = np.ascontiguousarray(history, HISTORY_DTYPE).view(np.uint8)
+            history = torch.from_numpy(raw.copy()).to(f"cuda:{self.device}")
         B, V = logits.shape
         dev = logits.device
         if out is None:
@@ -313,6 +344,8 @@ class Sampler:
                 out["topk_probs"] = torch.empty((B, topk_cap), dtype=torch.float32, device=dev)
         a = self.make_args(logits, params, recent=recent, n_recent=n_recent, mask=mask,
                            draws=draws, topk_cap=topk_cap, out=out, row_kinds=row_kinds)
+        a.history = _ptr(history)
+        a.dry_breaker = _ptr(dry_breaker)
         s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
         if noalloc:
             _check(self.lib.tms_sample_batch_noalloc(C.byref(a), C.c_void_p(s)),

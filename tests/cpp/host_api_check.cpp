@@ -117,7 +117,8 @@ int main() {
         expect(r1 == r2, "sample_token: generator state", c);
     }
 
-    // sample_token with DRY and an n-gram ban: all three transforms on the host.
+    // sample_token with DRY and an n-gram ban: the device pre-pass, against
+    // the oracle's restatement of the reference's steps.
     for (int i = 0; i < 20; ++i, ++c) {
         const int V = 4096;
         std::vector<float> row = make_row(g, V, 2.0f);
@@ -128,12 +129,17 @@ int main() {
         o.repeat_penalty = 1.1f;
         o.no_repeat_ngram = 3;
         o.dry.multiplier = 0.8f;
+        std::vector<unsigned char> brk(static_cast<size_t>(V), 0);
+        if (i % 2) {
+            brk[13] = 1;
+            o.dry_breaker = brk.data();
+        }
         std::vector<float> ref = row;
         const int n = static_cast<int>(hist.size());
-        tms_host_repeat_penalty(ref.data(), V, hist.data(), n, o.repeat_last_n, o.repeat_penalty);
-        tms_host_no_repeat_ngram(ref.data(), V, hist.data(), n, o.no_repeat_ngram);
-        tms_host_dry(ref.data(), V, hist.data(), n, o.dry.multiplier, o.dry.base,
-                     o.dry.allowed_length, o.dry.penalty_last_n, nullptr);
+        tmo_apply_repeat_penalty(ref.data(), V, hist.data(), n, o.repeat_last_n, o.repeat_penalty);
+        tmo_no_repeat_ngram(ref.data(), V, hist.data(), n, o.no_repeat_ngram);
+        tmo_dry(ref.data(), V, hist.data(), n, o.dry.multiplier, o.dry.base, o.dry.allowed_length,
+                o.dry.penalty_last_n, o.dry_breaker);
         std::mt19937 r1(static_cast<unsigned>(5 + i)), r2 = r1;
         const int want = oracle_sample(ref, tmsample_amd::Opts{o.temperature, o.top_k, o.top_p},
                                        false, r1);

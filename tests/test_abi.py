@@ -7,6 +7,8 @@ import glob
 import os
 import re
 
+import pytest
+
 from tensormark_amd import sampler
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -32,9 +34,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_sizes():
     lib = sampler.load_library()
-    assert lib.tms_abi_version() == 2
-    assert ctypes.sizeof(sampler.SampleArgs) == 136
+    assert lib.tms_abi_version() == 3
+    assert ctypes.sizeof(sampler.SampleArgs) == 152
     assert ctypes.sizeof(sampler.RowParams) == 56
+    assert sampler.HISTORY_DTYPE.itemsize == 24
     assert lib.tms_status_string(-2).decode().startswith("batch")
 
 
@@ -45,3 +48,41 @@ def test_invalid_arguments_rejected_without_device_work():
     h = ctypes.c_void_p()
     assert lib.tms_create(0, 0, 100, ctypes.byref(h)) == -1
     assert lib.tms_create(0, 1, 1 << 30, ctypes.byref(h)) == -1
+
+
+def test_ctypes_layouts_match_the_c_header(tmp_path):
+    """sizeof and offsetof of the header's structs, from the C compiler, equal
+    the ctypes / numpy mirrors field for field."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc")
+    if cc is None:
+        pytest.skip("no gcc")
+    fields = {
+        "tms_sample_args": [f for f, _ in sampler.SampleArgs._fields_],
+        "tms_row_params": [f for f, _ in sampler.RowParams._fields_],
+        "tms_history_params": list(sampler.HISTORY_DTYPE.names),
+    }
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tmsample_hip.h"', "int main(void) {"]
+    for st, fs in fields.items():
+        lines.append(f'printf("{st} %zu\\n", sizeof({st}));')
+        for f in fs:
+            lines.append(f'printf("{st}.{f} %zu\\n", offsetof({st}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    subprocess.run([cc, "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(root, "include"),
+                    "-I", "/opt/rocm/include", str(src), "-o", str(exe)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                    text=True).stdout.splitlines())
+    mirrors = {"tms_sample_args": sampler.SampleArgs, "tms_row_params": sampler.RowParams}
+    for st, cls in mirrors.items():
+        assert int(got[st]) == ctypes.sizeof(cls), st
+        for f, _ in cls._fields_:
+            assert int(got[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
+    assert int(got["tms_history_params"]) == sampler.HISTORY_DTYPE.itemsize
+    for f in sampler.HISTORY_DTYPE.names:
+        assert int(got[f"tms_history_params.{f}"]) == sampler.HISTORY_DTYPE.fields[f][1], f

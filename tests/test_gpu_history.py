@@ -1,0 +1,227 @@
+"""GPU parity of the history pre-pass (tms_sample_args.history): the n-gram
+ban and DRY after the penalties, on the device, against the oracle's
+composition of the reference's steps (tmo_sample_batch_h: mask, repetition
+penalty, frequency/presence, apply_no_repeat_ngram, apply_dry, sample).
+Tokens, keep counts and top-k ids bit-exact; top-k probabilities within
+1e-6 relative.
+
+DRY's base^k is correctly rounded on the device and glibc's powf in the
+oracle; they differ by 1 ulp for about 0.1% of (base, k).  The cases here use
+bases and run lengths where the two agree (base 2.0 is exact, 1.5 agrees for
+every k <= 1000, 1.75 below k = 83); the CPU test
+test_history.py::test_dry_scale_against_glibc_powf states the bound."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tensormark_amd import make_history, workloads
+from tests.helpers import params_array
+from tests.test_gpu_sample import check
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(sampler, x, p, *, recent, n_recent=None, mask=None, history=None, breaker=None,
+         topk_cap=0, dtype="f32", noalloc=False):
+    import torch
+
+    if dtype == "f32":
+        t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to("cuda:0")
+    elif dtype == "f16":
+        t = torch.from_numpy(np.ascontiguousarray(x, np.float16)).to("cuda:0")
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(x)).view(torch.bfloat16).to("cuda:0")
+    dev = lambda a, dt: None if a is None else torch.from_numpy(np.ascontiguousarray(a, dt)).to("cuda:0")
+    out = sampler.sample(t, p, recent=dev(recent, np.int32), n_recent=dev(n_recent, np.int32),
+                         mask=None if mask is None else dev(mask.astype(np.uint32).view(np.int32), np.int32),
+                         topk_cap=topk_cap, history=history, dry_breaker=dev(breaker, np.uint8),
+                         noalloc=noalloc)
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in out.items()}
+
+
+def _repeating(rng, B, n, alpha, flip=0.03):
+    """Histories that loop: a short period over a small alphabet, a few
+    random flips, drawn from ids spread over the vocabulary."""
+    h = np.zeros((B, n), np.int32)
+    for b in range(B):
+        ids = rng.choice(50000, size=alpha, replace=False)
+        period = int(rng.integers(2, 9))
+        pat = ids[rng.integers(0, alpha, period)]
+        row = np.resize(pat, n)
+        f = rng.random(n) < flip
+        row[f] = ids[rng.integers(0, alpha, int(f.sum()))]
+        h[b] = row
+    return h
+
+
+def _boost(x, recent, V, by=6.0):
+    """Lift the logits of each row's history ids so the ban and DRY decide
+    the draws (random logits would rarely put them in the top k)."""
+    for b in range(x.shape[0]):
+        ids = np.unique(recent[b][(recent[b] >= 0) & (recent[b] < V)])
+        x[b, ids] += np.float32(by)
+
+
+def _row_mix(rng, B):
+    p = params_array(B, temperature=0.8, top_k=40, top_p=0.95, seed=np.arange(B) + 100)
+    kind = np.arange(B) % 4
+    p["greedy"] = (kind == 0).astype(np.int32)
+    p["top_k"] = np.where(kind == 2, 0, np.where(kind == 3, 200, 40))
+    p["top_p"] = rng.choice([0.8, 0.95, 1.0], size=B)
+    p["min_p"] = rng.choice([0.0, 0.05], size=B)
+    p["repeat_penalty"] = rng.choice([1.0, 1.1, 1.3], size=B)
+    p["repeat_last_n"] = rng.choice([16, 64, 256], size=B)
+    p["frequency_penalty"] = rng.choice([0.0, 0.2], size=B)
+    p["presence_penalty"] = rng.choice([0.0, 0.1], size=B)
+    return p
+
+
+def _hist_mix(rng, B):
+    h = make_history(B)
+    k = np.arange(B) % 3
+    h["no_repeat_ngram"] = np.where(k != 1, rng.choice([2, 3, 4], size=B), 0)
+    h["dry_multiplier"] = np.where(k != 0, rng.choice([0.5, 0.8], size=B), 0.0)
+    h["dry_base"] = rng.choice([1.5, 2.0], size=B)
+    h["dry_allowed_length"] = rng.choice([1, 2, 3], size=B)
+    h["dry_penalty_last_n"] = rng.choice([32, 256, 1000], size=B)
+    return h
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_history_rows_vs_oracle(sampler, orc, dtype):
+    rng = np.random.default_rng({"f32": 1, "f16": 2, "bf16": 3}[dtype])
+    B, V, n = 48, 50000, 400
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = _repeating(rng, B, n, alpha=12)
+    _boost(x, recent, V)
+    if dtype == "f16":
+        x = x.astype(np.float16)
+        x32 = x.astype(np.float32)
+    elif dtype == "bf16":
+        x = workloads.to_bf16_bits(x)
+        x32 = workloads.bf16_bits_to_f32(x)
+    else:
+        x32 = x
+    n_recent = rng.integers(n // 2, n + 1, B).astype(np.int32)
+    bits = rng.random((B, ((V + 31) // 32) * 32)) < 0.7
+    bits[: B // 2] = True
+    mask = workloads.pack_bits(bits)
+    p = _row_mix(rng, B)
+    h = _hist_mix(rng, B)
+    want = orc.sample_batch(x32, p, recent=recent, n_recent=n_recent, mask=mask, topk_cap=20,
+                            history=h)
+    g = _run(sampler, x, p, recent=recent, n_recent=n_recent, mask=mask, history=h, topk_cap=20,
+             dtype=dtype)
+    check(g, want, 20)
+    # the ban and DRY moved the answer on many rows
+    plain = orc.sample_batch(x32, p, recent=recent, n_recent=n_recent, mask=mask, topk_cap=20)
+    assert (plain["tokens"] != want["tokens"]).sum() >= B // 8
+
+
+def test_ngram_restore_rule(sampler, orc):
+    """The ban would leave nothing above -inf: the banned ids keep their
+    values (tmsample.h:105-112).  Row 0: the grammar allows only the banned
+    id; row 1: no mask, every logit -inf but the banned id's (the pre-pass
+    scans the row); row 2: one more allowed id far down the row stays, so
+    the ban holds and that id is sampled."""
+    V = 70000
+    rng = np.random.default_rng(9)
+    x = rng.normal(0.0, 1.0, (3, V)).astype(np.float32)
+    recent = np.array([[5, 6, 7, 5, 6]] * 3, np.int32)   # ngram 3: context (5, 6) -> 7 banned
+    bits = np.zeros((3, ((V + 31) // 32) * 32), bool)
+    bits[0, 7] = True
+    bits[1] = True
+    bits[2, 7] = bits[2, 65001] = True
+    x[1, :] = -np.inf
+    x[1, 7] = 0.5
+    mask = workloads.pack_bits(bits)
+    p = params_array(3, temperature=1.0, top_k=40, top_p=1.0, seed=np.arange(3))
+    h = make_history(3, no_repeat_ngram=3)
+    want = orc.sample_batch(x, p, recent=recent, mask=mask, topk_cap=4, history=h)
+    assert want["tokens"].tolist() == [7, 7, 65001]
+    g = _run(sampler, x, p, recent=recent, mask=mask, history=h, topk_cap=4)
+    check(g, want, 4)
+
+
+def test_dry_breakers_and_out_of_range_ids(sampler, orc):
+    rng = np.random.default_rng(11)
+    B, V, n = 16, 32000, 300
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = _repeating(rng, B, n, alpha=6, flip=0.01) % V
+    _boost(x, recent, V)
+    recent[:, ::37] = -5          # out of range: skipped by every step
+    recent[:, 5::41] = V + 3
+    breaker = np.zeros(V, np.uint8)
+    breaker[np.unique(recent[recent >= 0][::7] % V)[:4]] = 1
+    p = _row_mix(rng, B)
+    h = make_history(B, no_repeat_ngram=3, dry_multiplier=0.8, dry_base=1.5, dry_allowed_length=2,
+                     dry_penalty_last_n=256)
+    want = orc.sample_batch(x, p, recent=recent, topk_cap=8, history=h, dry_breaker=breaker)
+    g = _run(sampler, x, p, recent=recent, history=h, breaker=breaker, topk_cap=8)
+    check(g, want, 8)
+
+
+def test_long_history_lists(sampler, orc):
+    """Lists longer than the general kernel's owned window (1024 entries):
+    3000 distinct ids in the repetition window, plus bans and DRY targets."""
+    rng = np.random.default_rng(13)
+    B, V, n = 8, 128256, 3600
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = np.zeros((B, n), np.int32)
+    for b in range(B):
+        recent[b, :3000] = rng.choice(V, 3000, replace=False)
+        recent[b, 3000:] = np.resize(recent[b, 100:140], 600)   # a loop at the end
+    _boost(x, recent[:, 3000:], V)
+    p = _row_mix(rng, B)
+    p["repeat_last_n"] = 3600
+    p["repeat_penalty"] = 1.2
+    h = make_history(B, no_repeat_ngram=4, dry_multiplier=0.8, dry_base=2.0, dry_penalty_last_n=700)
+    want = orc.sample_batch(x, p, recent=recent, topk_cap=16, history=h)
+    g = _run(sampler, x, p, recent=recent, history=h, topk_cap=16)
+    check(g, want, 16)
+
+
+def test_history_list_overflow_reports_unsupported(sampler, orc):
+    """A row whose history touches more than TMS_HISTORY_MAX_IDS (4096)
+    distinct ids reports TMS_ROW_UNSUPPORTED; the other rows are sampled."""
+    rng = np.random.default_rng(17)
+    B, V, n = 4, 60000, 5000
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = np.tile(rng.integers(0, 50, n).astype(np.int32), (B, 1))
+    recent[1] = rng.choice(V, n, replace=False)
+    p = _row_mix(rng, B)
+    p["repeat_last_n"] = n
+    p["repeat_penalty"] = 1.1
+    h = make_history(B, no_repeat_ngram=3)
+    want = orc.sample_batch(x, p, recent=recent, history=h)
+    g = _run(sampler, x, p, recent=recent, history=h)
+    assert g["status"][1] == 4 and g["tokens"][1] == -1
+    check(g, want, 0, rows=[0, 2, 3])
+
+
+def test_history_noalloc_matches_context(sampler, orc):
+    rng = np.random.default_rng(19)
+    B, V, n = 32, 40000, 256
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = _repeating(rng, B, n, alpha=10)
+    _boost(x, recent, V)
+    p = _row_mix(rng, B)
+    h = _hist_mix(rng, B)
+    a = _run(sampler, x, p, recent=recent, history=h, topk_cap=10)
+    b = _run(sampler, x, p, recent=recent, history=h, topk_cap=10, noalloc=True)
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+    want = orc.sample_batch(x, p, recent=recent, topk_cap=10, history=h)
+    check(a, want, 10)
+
+
+def test_history_without_ngram_or_dry_equals_plain(sampler, orc):
+    """History params that switch both steps off leave the answers of the
+    plain call (the pre-pass still forms the repetition-penalty values)."""
+    w = workloads.cfg2(B=16, V=40000, seed=23)
+    h = make_history(16)
+    a = _run(sampler, w["logits"], w["params"], recent=w["recent"], history=h, topk_cap=40)
+    want = orc.sample_batch(w["logits"], w["params"], recent=w["recent"], topk_cap=40)
+    check(a, want, 40)

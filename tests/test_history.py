@@ -65,3 +65,120 @@ def test_repeat_penalty_host_closed_form():
     row = np.array([2.0, -2.0, 3.0], np.float32)
     sampler.apply_repeat_penalty(row, np.array([0, 1, 0, 7], np.int32), 64, 2.0)
     assert row.tolist() == [0.5, -4.0, 3.0]
+
+
+# ---- the oracle's restatement (the GPU tests' checker) against the same
+#      reference outputs, and the DRY scale the device and host compute.
+
+def test_oracle_history_matches_reference_golden(hist_golden, orc):
+    g = hist_golden
+    for i, m in enumerate(g["meta"]):
+        x, h, want = g[f"x{i}"], g[f"h{i}"], g[f"y{i}"]
+        if m["kind"] == 0:
+            got = orc.no_repeat_ngram(x, h, int(m["ngram"]))
+        else:
+            brk = g[f"brk{i}"] if m["brk"] else None
+            got = orc.dry(x, h, float(m["mult"]), float(m["base"]), int(m["allowed"]),
+                          int(m["last_n"]), brk)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), i
+
+
+def _histories(rng, n_cases):
+    """Histories that repeat: a short alphabet, periodic stretches, breakers."""
+    for c in range(n_cases):
+        n = int(rng.integers(2, 300))
+        alpha = int(rng.integers(2, 12))
+        if c % 3 == 0:
+            period = int(rng.integers(1, 6))
+            base = rng.integers(0, alpha, period)
+            h = np.resize(base, n)
+            flips = rng.random(n) < 0.05
+            h = np.where(flips, rng.integers(0, alpha, n), h)
+        else:
+            h = rng.integers(0, alpha, n)
+        if c % 7 == 0:
+            h[rng.integers(0, n)] = -3          # out-of-range ids are skipped
+        yield c, h.astype(np.int32)
+
+
+def test_oracle_ngram_matches_compiled_reference(orc, ref):
+    rng = np.random.default_rng(5)
+    for c, h in _histories(rng, 300):
+        V = 16
+        x = rng.normal(0, 2, V).astype(np.float32)
+        if c % 5 == 0:
+            x[rng.random(V) < 0.8] = -np.inf      # few left: the restore rule
+        ng = int(rng.integers(2, 6))
+        assert np.array_equal(orc.no_repeat_ngram(x, h, ng).view(np.uint32),
+                              ref.no_repeat_ngram(x, h, ng).view(np.uint32)), c
+
+
+def test_oracle_dry_matches_compiled_reference(orc, ref):
+    rng = np.random.default_rng(6)
+    for c, h in _histories(rng, 300):
+        V = 16
+        x = rng.normal(0, 2, V).astype(np.float32)
+        brk = (rng.random(V) < 0.2).astype(np.uint8) if c % 2 else None
+        args = (float(rng.choice([0.5, 0.8, 2.0])), float(rng.choice([1.75, 1.5, 2.0, 1.1])),
+                int(rng.integers(1, 4)), int(rng.choice([8, 64, 256])))
+        got = orc.dry(x, h, *args, brk)
+        want = ref.dry(x, h, *args, brk)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), c
+
+
+def _scale_by_host(base, k, allowed=2):
+    """base^k as tms_host_dry computes it: a history whose only DRY match has
+    L = k + allowed, multiplier 1, on a zero row -> row[y] = -scale."""
+    L = k + allowed
+    t = np.arange(10, 10 + L, dtype=np.int32)
+    h = np.concatenate([[1], t, [2], t]).astype(np.int32)   # ... x t y t: one match, y follows
+    row = np.zeros(10 + L, np.float32)
+    sampler.apply_dry(row, h, 1.0, base, allowed, 10 * L + 10)
+    hit = np.nonzero(row)[0]
+    assert hit.tolist() == [2], hit
+    return -row[2]
+
+
+def _round_f32(q):
+    """A positive Fraction rounded to the nearest float32 (ties to even)."""
+    from fractions import Fraction
+
+    e = q.numerator.bit_length() - q.denominator.bit_length()
+    if Fraction(2) ** e > q:
+        e -= 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 23)
+    m = q / ulp
+    lo = m.numerator // m.denominator
+    r = m - lo
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and lo % 2):
+        lo += 1
+    return np.float32(float(lo * ulp)) if lo * ulp < Fraction(2) ** 128 else np.float32(np.inf)
+
+
+def test_dry_scale_is_correctly_rounded():
+    from fractions import Fraction
+
+    for b in (1.75, 1.5, 2.0, 1.1, 1.05, 1.9, 0.9):
+        bf = Fraction(float(np.float32(b)))
+        for k in list(range(0, 40)) + [57, 83, 100, 171, 294]:
+            assert _scale_by_host(np.float32(b), k) == _round_f32(bf ** k), (b, k)
+
+
+def test_dry_scale_against_glibc_powf(orc):
+    """The reference's powf (through the oracle) agrees with the library's
+    scale to 1 ulp everywhere sampled and exactly for base 1.75 below k = 83."""
+    diff = 0
+    for b in (1.75, 1.5, 1.25, 2.0):
+        for k in range(0, 120):
+            L = k + 2
+            t = np.arange(10, 10 + L, dtype=np.int32)
+            h = np.concatenate([[1], t, [2], t]).astype(np.int32)
+            g = -orc.dry(np.zeros(10 + L, np.float32), h, 1.0, b, 2, 10 * L + 10)[2]
+            m = _scale_by_host(np.float32(b), k)
+            d = abs(int(np.float32(g).view(np.int32)) - int(np.float32(m).view(np.int32)))
+            assert d <= 1, (b, k)
+            if b == 1.75 and k < 83:
+                assert d == 0, k
+            diff += d
+    assert diff <= 4
