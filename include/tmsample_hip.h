@@ -342,6 +342,125 @@ int tms_vocab_consume(tms_vocab* v, tms_grammar* g, tms_gstate* s, int id);
 void tms_vocab_clear_cache(tms_vocab* v);
 
 /*
+ * Vocabulary byte tables: the bytes each id contributes to a running decode,
+ * as the reference's tokenizers derive them at load (tensormark/tmtok.h:40-42
+ * piece_bytes; llama_chat.cpp:510-524), and the whitespace-only flags of
+ * the stall narrowing.
+ *   tms_token_table_spm   SentencePiece pieces (sp_tokenizer.h:154-172):
+ *                         type 3 (CONTROL) no bytes, type 6 (BYTE) "<0xNN>"
+ *                         the byte NN, any other type the piece with U+2581
+ *                         read as a space
+ *   tms_token_table_bpe   byte-level BPE pieces (bpe.h:91-110, 576-586): each
+ *                         codepoint back to its byte through GPT-2's
+ *                         bytes_to_unicode table; a NULL piece is an id the
+ *                         vocabulary lacks (no bytes).  NULL on an unmapped
+ *                         codepoint, with the message in err
+ *   tms_token_table_bytes piece_bytes(id): pointer and length (empty for an
+ *                         id outside the table)
+ *   tms_token_table_ws_only  non-empty and only ' ', '\t', '\n', '\r'
+ *                         (llama_chat.cpp:519-524)
+ *   tms_vocab_from_table  tms_vocab_create over the table's bytes
+ */
+typedef struct tms_token_table tms_token_table;
+tms_token_table* tms_token_table_spm(const char* const* pieces, const size_t* lens,
+                                     const uint8_t* types, int n, char* err, size_t err_cap);
+tms_token_table* tms_token_table_bpe(const char* const* pieces, const size_t* lens, int n,
+                                     char* err, size_t err_cap);
+void tms_token_table_free(tms_token_table* t);
+int tms_token_table_size(const tms_token_table* t);
+int tms_token_table_bytes(const tms_token_table* t, int id, const char** bytes, size_t* len);
+int tms_token_table_ws_only(const tms_token_table* t, int id);
+tms_vocab* tms_vocab_from_table(tms_grammar* g, const tms_token_table* t, int eos,
+                                const unsigned char* skip);
+
+/*
+ * One decode's grammar restriction: GrammarFilter (tensormark/llama_chat.cpp:
+ * 159-223).  Host-only; a filter's grammar and vocab are used by one thread
+ * at a time.
+ *   tms_filter_create    state at the grammar's start, stall 0; the table
+ *                        (nullable) gives the whitespace-only ids
+ *   tms_filter_reset     reset (llama_chat.cpp:169-179) without the memo drop
+ *                        (tms_vocab_clear_cache does that)
+ *   tms_filter_mask      restrict (llama_chat.cpp:184-209) as mask words: the
+ *                        allowed ids, minus the whitespace-only ones once the
+ *                        state has not changed for 4 tokens (unless none
+ *                        would be left); returns the ids set.  No allowed id:
+ *                        every word all ones (fails open) and 0
+ *   tms_filter_consume   consume (llama_chat.cpp:216-221); the stall count
+ *                        grows while the state stays the same
+ *   tms_filter_complete  complete (llama_chat.cpp:212-215)
+ *   tms_filter_done      done (llama_chat.cpp:222)
+ */
+typedef struct tms_filter tms_filter;
+tms_filter* tms_filter_create(tms_grammar* g, tms_vocab* v, const tms_token_table* t);
+void tms_filter_free(tms_filter* f);
+int tms_filter_reset(tms_filter* f);
+int tms_filter_mask(tms_filter* f, uint32_t* words, int n_words);
+int tms_filter_consume(tms_filter* f, int id);
+int tms_filter_complete(tms_filter* f, int eos);
+int tms_filter_done(const tms_filter* f);
+int tms_filter_stall(const tms_filter* f);
+
+/*
+ * The mask producer overlapped with the device: the per-step restriction of
+ * llama_chat.cpp:787-803 (restrict, sample, consume) for a batch of
+ * filters, with the next step's masks computed on `threads` worker threads
+ * into pinned staging while the device runs the current step, uploaded on
+ * the pipe's own stream (default priority) and ordered before the sampler
+ * by an event.  Two slots, so one step's upload never overwrites the words
+ * the previous step's sampler may still read.  No counterpart in the
+ * reference (its restriction runs inline on the host).
+ *   tms_mask_pipe_set_row  the row's filter (NULL: unconstrained, all ones);
+ *                          rows with one grammar go to one worker
+ *   tms_mask_pipe_submit   each filter consumes tokens[row] (host, >= 0;
+ *                          NULL or < 0: nothing) and writes its mask; returns
+ *                          at once
+ *   tms_mask_pipe_acquire  waits for the workers; makes `stream` wait for the
+ *                          upload; *words = device [batch][n_words]; allowed
+ *                          (nullable) = ids per row (0: failed open, -1: no
+ *                          filter)
+ *   tms_mask_pipe_release  after enqueueing the launches that read the words
+ *                          on `stream`
+ */
+typedef struct tms_mask_pipe tms_mask_pipe;
+tms_mask_pipe* tms_mask_pipe_create(int device, int batch, int n_words, int threads);
+void tms_mask_pipe_free(tms_mask_pipe* p);
+int tms_mask_pipe_set_row(tms_mask_pipe* p, int row, tms_filter* f);
+int tms_mask_pipe_submit(tms_mask_pipe* p, const int32_t* tokens);
+int tms_mask_pipe_acquire(tms_mask_pipe* p, hipStream_t stream, const uint32_t** words,
+                          int32_t* allowed);
+int tms_mask_pipe_release(tms_mask_pipe* p, hipStream_t stream);
+
+/*
+ * Chained device-resident decode (gpu_chain_begin / gpu_chain_poll,
+ * tensormark/llama.h:6047-6130; the token-slot peek, tensormark/metal.h:
+ * 3216-3228): n steps enqueued at once, each step's sampled ids gathered
+ * into the next step's input on the device, the host polling the ids as
+ * they land.
+ *   tms_token_slot_create  `capacity` int32 entries of host memory the
+ *                          device writes (pinned, mapped, coherent), all -1
+ *   tms_token_slot_device  the entries' device address
+ *   tms_token_slot_fill    host: every entry := value (no chain in flight)
+ *   tms_token_slot_peek    host: entry i with an acquire load, no wait; -1
+ *                          while pending, -2 for a row the sampler could not
+ *                          sample (its status says why)
+ *   tms_embed_gather       x[b][:] = table[tokens[b]][:] (rows x dim of
+ *                          dtype; an id outside [0, rows) gives zeros), and
+ *                          slot_out[b] = tokens[b] (nullable) by system-scope
+ *                          release stores.  table NULL: publish only.  Row
+ *                          bytes, table and x 16-byte aligned
+ */
+typedef struct tms_token_slot tms_token_slot;
+tms_token_slot* tms_token_slot_create(int device, int capacity);
+void tms_token_slot_free(tms_token_slot* s);
+int32_t* tms_token_slot_device(tms_token_slot* s);
+int tms_token_slot_capacity(const tms_token_slot* s);
+int tms_token_slot_fill(tms_token_slot* s, int32_t value);
+int32_t tms_token_slot_peek(const tms_token_slot* s, int i);
+int tms_embed_gather(const void* table, int dtype, int64_t rows, int64_t dim, const int32_t* tokens,
+                     int batch, void* x, int32_t* slot_out, hipStream_t stream);
+
+/*
  * Test hooks.  Run the device Philox4x32-10 on n (counter[4], key[2])
  * tuples packed as 6 words each and write 4 words each; evaluate the device
  * double exp on n inputs (which = 0: the HIP math library, 1: the

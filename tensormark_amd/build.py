@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtmsample_hip.so")
-SOURCES = ["tms_sample.hip", "tms_topk.hip", "tms_wide.hip", "tms_dense.hip", "tms_hist.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp"]
+SOURCES = ["tms_sample.hip", "tms_topk.hip", "tms_wide.hip", "tms_dense.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
 
 # -ffp-contract=off keeps every a*b+c as two rounded operations, so the
 # device arithmetic matches the host checker bit for bit.  Packed-FP32 ops

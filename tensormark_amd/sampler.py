@@ -61,6 +61,34 @@ EXPORTS = (
     "tms_vocab_mask",
     "tms_vocab_consume",
     "tms_vocab_clear_cache",
+    "tms_token_table_spm",
+    "tms_token_table_bpe",
+    "tms_token_table_free",
+    "tms_token_table_size",
+    "tms_token_table_bytes",
+    "tms_token_table_ws_only",
+    "tms_vocab_from_table",
+    "tms_filter_create",
+    "tms_filter_free",
+    "tms_filter_reset",
+    "tms_filter_mask",
+    "tms_filter_consume",
+    "tms_filter_complete",
+    "tms_filter_done",
+    "tms_filter_stall",
+    "tms_mask_pipe_create",
+    "tms_mask_pipe_free",
+    "tms_mask_pipe_set_row",
+    "tms_mask_pipe_submit",
+    "tms_mask_pipe_acquire",
+    "tms_mask_pipe_release",
+    "tms_token_slot_create",
+    "tms_token_slot_free",
+    "tms_token_slot_device",
+    "tms_token_slot_capacity",
+    "tms_token_slot_fill",
+    "tms_token_slot_peek",
+    "tms_embed_gather",
 )
 
 
@@ -232,6 +260,46 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         lib.tms_vocab_consume.argtypes = [vp, vp, vp, C.c_int]
         lib.tms_vocab_clear_cache.argtypes = [vp]
         lib.tms_vocab_clear_cache.restype = None
+        cp, sp = C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)
+        lib.tms_token_table_spm.restype = vp
+        lib.tms_token_table_spm.argtypes = [cp, sp, vp, C.c_int, C.c_char_p, C.c_size_t]
+        lib.tms_token_table_bpe.restype = vp
+        lib.tms_token_table_bpe.argtypes = [cp, sp, C.c_int, C.c_char_p, C.c_size_t]
+        lib.tms_token_table_free.argtypes = [vp]
+        lib.tms_token_table_free.restype = None
+        lib.tms_token_table_size.argtypes = [vp]
+        lib.tms_token_table_bytes.argtypes = [vp, C.c_int, C.POINTER(C.c_void_p), sp]
+        lib.tms_token_table_ws_only.argtypes = [vp, C.c_int]
+        lib.tms_vocab_from_table.restype = vp
+        lib.tms_vocab_from_table.argtypes = [vp, vp, C.c_int, vp]
+        lib.tms_filter_create.restype = vp
+        lib.tms_filter_create.argtypes = [vp, vp, vp]
+        lib.tms_filter_free.argtypes = [vp]
+        lib.tms_filter_free.restype = None
+        for f in (lib.tms_filter_reset, lib.tms_filter_done, lib.tms_filter_stall):
+            f.argtypes = [vp]
+        lib.tms_filter_mask.argtypes = [vp, vp, C.c_int]
+        lib.tms_filter_consume.argtypes = [vp, C.c_int]
+        lib.tms_filter_complete.argtypes = [vp, C.c_int]
+        lib.tms_mask_pipe_create.restype = vp
+        lib.tms_mask_pipe_create.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int]
+        lib.tms_mask_pipe_free.argtypes = [vp]
+        lib.tms_mask_pipe_free.restype = None
+        lib.tms_mask_pipe_set_row.argtypes = [vp, C.c_int, vp]
+        lib.tms_mask_pipe_submit.argtypes = [vp, vp]
+        lib.tms_mask_pipe_acquire.argtypes = [vp, vp, C.POINTER(C.c_void_p), vp]
+        lib.tms_mask_pipe_release.argtypes = [vp, vp]
+        lib.tms_token_slot_create.restype = vp
+        lib.tms_token_slot_create.argtypes = [C.c_int, C.c_int]
+        lib.tms_token_slot_free.argtypes = [vp]
+        lib.tms_token_slot_free.restype = None
+        lib.tms_token_slot_device.restype = vp
+        lib.tms_token_slot_device.argtypes = [vp]
+        lib.tms_token_slot_capacity.argtypes = [vp]
+        lib.tms_token_slot_fill.argtypes = [vp, C.c_int32]
+        lib.tms_token_slot_peek.restype = C.c_int32
+        lib.tms_token_slot_peek.argtypes = [vp, C.c_int]
+        lib.tms_embed_gather.argtypes = [vp, C.c_int, C.c_int64, C.c_int64, vp, C.c_int, vp, vp, vp]
         _LIB = lib
     return _LIB
 
@@ -368,8 +436,11 @@ class Sampler:
         a.recent = _ptr(recent)
         a.recent_stride = recent.shape[1] if recent is not None else 0
         a.n_recent = _ptr(n_recent)
-        a.mask = _ptr(mask)
-        a.mask_stride = mask.shape[1] if mask is not None else 0
+        if isinstance(mask, tuple):   # (device address, words per row), e.g. from a MaskPipe
+            a.mask, a.mask_stride = mask
+        else:
+            a.mask = _ptr(mask)
+            a.mask_stride = mask.shape[1] if mask is not None else 0
         a.draws = _ptr(draws)
         a.out_tokens = out["tokens"].data_ptr()
         a.out_status = out["status"].data_ptr()
