@@ -179,14 +179,17 @@ def measure_traffic(args):
             v = float(row["Counter_Value"])
             name = row["Kernel_Name"]
             if "copyBuffer" in name:
-                copy.append(v)
+                copy.append((int(row["Dispatch_Id"]), v))
             elif "tms::" in name:
                 tms.append(v)
         shutil.rmtree(out, ignore_errors=True)
-        if not copy or not tms:
+        if len(copy) < 3 or not tms:
             return None, f"rocprofv3 {ctr} pass: no copy or sampler dispatches"
+        # the calibration copies are the run's first three copy dispatches
+        # (before any input upload)
+        cal = sorted(v for _, v in sorted(copy)[:3])[1]
         known_kib = mib * 1024.0   # the copy reads mib MiB and writes mib MiB
-        factor = known_kib / max(copy)
+        factor = known_kib / cal
         vals[ctr] = (sum(tms) / (steps + warm), factor)
     fetch, ff = vals["FETCH_SIZE"]
     write, fw = vals["WRITE_SIZE"]
