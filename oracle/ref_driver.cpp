@@ -18,6 +18,7 @@
 #include <cstring>
 #include <limits>
 #include <random>
+#include <sstream>
 #include <thread>
 #include <vector>
 
@@ -49,9 +50,49 @@ int one_row(const float* logits, int V, float T, int top_k, float top_p, int gre
     return tmsample::sample(lg, V, tmsample::Opts{T, top_k, top_p}, greedy != 0, rng);
 }
 
+// The mt19937 word y such that the engine's tempering gives w.
+std::uint32_t untemper(std::uint32_t w) {
+    std::uint32_t y = w;
+    y ^= y >> 18;
+    y ^= (y << 15) & 0xefc60000u;
+    std::uint32_t t = y;
+    for (int i = 0; i < 5; ++i) t = y ^ ((t << 7) & 0x9d2c5680u);
+    y = t;
+    y ^= (y >> 11) ^ (y >> 22);
+    return y;
+}
+
+// An std::mt19937 whose next two outputs are w0, w1: its state, read back
+// through the engine's own stream operator, holds the untempered words at
+// positions 0 and 1 with the position at 0 (no twist before them).
+std::mt19937 engine_giving(std::uint32_t w0, std::uint32_t w1) {
+    std::ostringstream os;
+    os << untemper(w0) << ' ' << untemper(w1);
+    for (int i = 2; i < 624; ++i) os << ' ' << 0x9908b0dfu + i;
+    os << ' ' << 0;
+    std::istringstream is(os.str());
+    std::mt19937 e;
+    is >> e;
+    return e;
+}
+
 }  // namespace
 
 extern "C" {
+
+// tmsample::sample itself (the unmodified header), driven by an mt19937 that
+// yields w0 then w1: the reference's token for that uniform, under this
+// standard library's nth_element / sort / discrete_distribution.  Returns -1
+// if the crafted engine does not give (w0, w1).
+int ref_sample_words(const float* logits, int V, float T, int top_k, float top_p, int greedy,
+                     std::uint32_t w0, std::uint32_t w1) {
+    std::mt19937 check = engine_giving(w0, w1);
+    if (check() != w0 || check() != w1) return -1;
+    std::mt19937 rng = engine_giving(w0, w1);
+    std::vector<float> lg(logits, logits + V);
+    return tmsample::sample(lg, V, tmsample::Opts{T, top_k, top_p}, greedy != 0, rng);
+}
+
 
 // std::generate_canonical<double, 53> on the words (w0, w1).
 double ref_canonical(std::uint32_t w0, std::uint32_t w1) {

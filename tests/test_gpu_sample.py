@@ -486,3 +486,25 @@ def test_topk_kernel_error_rows(sampler, orc):
     torch.cuda.synchronize()
     assert list(out["status"].cpu().numpy()) == [0, 0]
     assert np.array_equal(out["tokens"].cpu().numpy(), want2["tokens"])
+
+
+def test_tie_fixture_rows(sampler, orc):
+    """Rows full of exact ties (tests/golden/tie_golden.npz): the device gives
+    the oracle's lowest-id-first order, keep and draws, in groups of equal
+    shape (the reference's libstdc++ order is checked against the oracle on
+    the CPU)."""
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tie_golden.npz"),
+                allow_pickle=False)
+    meta = g["meta"]
+    groups = {}
+    for i, m in enumerate(meta):
+        groups.setdefault((g[f"x{i}"].size, float(m["T"]), int(m["k"]), float(m["p"])), []).append(i)
+    for (V, T, k, p), idx in groups.items():
+        x = np.stack([g[f"x{i}"] for i in idx])
+        draws = np.stack([g[f"draws{i}"][0, :2] for i in idx]).astype(np.uint32)
+        prm = params_array(len(idx), temperature=T, top_k=k, top_p=p)
+        want = orc.sample_batch(x, prm, draws=draws, topk_cap=k)
+        got = run_gpu(sampler, x, prm, draws=draws, topk_cap=k)
+        check(got, want, k)

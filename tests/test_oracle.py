@@ -5,6 +5,7 @@ and brute force.  CPU only."""
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -296,3 +297,66 @@ def test_spec_marginal_equals_target(orc):
         st, acc, tok = orc.spec_verify_seq(t, d, np.array([x], np.int32), 1.0, words)
         counts[x if acc == 1 else tok] += 1
     assert np.allclose(counts / n, pt, atol=4 * np.sqrt(pt / n) + 1e-3)
+
+
+# ---- ties: the reference's order among equal values (libstdc++) against the
+#      library's lowest-id-first contract
+
+TIE_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tie_golden.npz")
+
+
+def _tie_rows():
+    g = np.load(TIE_GOLDEN, allow_pickle=False)
+    for i, m in enumerate(g["meta"]):
+        yield i, g[f"x{i}"], g[f"ref{i}"], g[f"draws{i}"], m
+
+
+def test_tie_fixtures_same_values_at_every_rank(orc):
+    """At every rank of the kept prefix the reference (libstdc++'s
+    nth_element/sort) and the oracle hold the same value; the oracle's ids
+    are lowest-first within equal values (brute-force sort), the reference's
+    mostly are not; draws at random uniforms land on the same value."""
+    from tests.helpers import params_array
+
+    differ = 0
+    for i, x, ref, draws, m in _tie_rows():
+        V, k = x.size, int(m["k"])
+        p = params_array(1, temperature=float(m["T"]), top_k=k, top_p=float(m["p"]))
+        r = orc.sample_batch(x[None], p, draws=np.array([[0, 0]], np.uint32), topk_cap=k)
+        ids = r["topk_ids"][0]
+        brute = sorted(range(V), key=lambda j: (-float(x[j]), j))[:k]
+        assert ids.tolist() == brute, i
+        keep = int(m["keep"])
+        assert len(ref) == keep and len(set(ref.tolist())) == keep
+        assert np.array_equal(x[ref], x[ids[:keep]]), i
+        differ += int(ref.tolist() != ids[:keep].tolist())
+        for w0, w1, want in draws:
+            got = orc.sample_batch(x[None], p, draws=np.array([[w0, w1]], np.uint32))["tokens"][0]
+            assert x[got] == x[want], (i, w0, w1)
+            if np.count_nonzero(x == x[want]) == 1:
+                assert got == want
+    assert differ >= 40   # the unspecified tie order is not lowest-id-first under libstdc++
+
+
+def test_tie_order_brute_force_tiny(orc):
+    """Every row over V = 5 with values in {0, 1, 2}, every k: the oracle's
+    top-k ids are the (value desc, id asc) sort, and a draw in the middle of
+    each probability bucket returns that rank's id."""
+    import itertools
+
+    from tests.golden.make_tie_golden import buckets, words_for
+    from tests.helpers import params_array
+
+    for row in itertools.product([0.0, 1.0, 2.0], repeat=5):
+        x = np.array(row, np.float32)
+        for k in range(1, 6):
+            want = sorted(range(5), key=lambda j: (-float(x[j]), j))[:k]
+            p = params_array(1, temperature=1.0, top_k=k, top_p=1.0)
+            r = orc.sample_batch(x[None], p, draws=np.array([[0, 0]], np.uint32), topk_cap=k)
+            assert r["topk_ids"][0].tolist() == want, (row, k)
+            keep, cp = buckets([float(x[j]) for j in want], 1.0, 1.0)
+            for j in range(keep):
+                lo = cp[j - 1] if j else 0.0
+                w0, w1 = words_for((lo + cp[j]) / 2.0)
+                t = orc.sample_batch(x[None], p, draws=np.array([[w0, w1]], np.uint32))["tokens"][0]
+                assert t == want[j], (row, k, j)
