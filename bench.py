@@ -103,42 +103,109 @@ def cpu_model():
     return "unknown"
 
 
+def _timed(run, budget=10.0):
+    """(median pass seconds, passes): one pass to size, then passes for
+    about `budget` seconds of host work (median taken by the callee)."""
+    dt = run(1)
+    reps = max(3, min(5000, int(budget / max(dt, 1e-4))))
+    return run(reps), reps
+
+
 def cpu_baseline(w, cfg):
-    """The reference's own tmsample.h (oracle/_ref), timed on this host: rows
-    dealt to a thread pool, median pass of about 10 s of work, and a
-    one-thread figure beside it."""
+    """The reference's own tmsample.h (oracle/_ref) on this host for configs
+    2, 3 and 5: rows dealt to a thread pool, the median pass of about 10 s of
+    work, and a one-thread figure beside it.  Config 4 has no reference
+    implementation: the oracle's C restatement of the verify rule is timed
+    instead, one thread (kind "port")."""
     import oracle
 
-    ref = oracle.reference()
-    if ref is None or cfg != 2:
-        return None
-    x = w["logits"]
     nproc = os.cpu_count() or 1
     # the GPU box's CPU share is 16 threads (OMP_NUM_THREADS there), whatever nproc shows
     threads = max(1, min(nproc, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16))
-    kw = dict(recent=w["recent"], window=256, penalty=1.1, mask=w["mask"])
     t0 = time.perf_counter()
-    dt, _ = ref.bench(x, 0.7, 40, 0.95, threads=threads, reps=1, **kw)
-    reps = max(3, min(5000, int(10.0 / max(dt, 1e-4))))   # about 10 s of host work
-    dt, _ = ref.bench(x, 0.7, 40, 0.95, threads=threads, reps=reps, **kw)
-    B = x.shape[0]
-    rows1 = x[:8]   # one thread: 8 rows, median of 5 passes
-    dt1, _ = ref.bench(rows1, 0.7, 40, 0.95, recent=w["recent"][:8], window=256, penalty=1.1,
-                       mask=w["mask"][:8], threads=1, reps=5)
-    wall = time.perf_counter() - t0
+    if cfg == 4:
+        orc = oracle.oracle()
+        tg, dr, tok, prm = w["target"], w["draft"], w["tokens"], w["params"]
+        B, k = tok.shape
+        words = np.zeros((B, k + 1, 2), np.uint32)
+        for b in range(B):
+            for i in range(k + 1):
+                words[b, i] = orc.row_words(int(prm["seed"][b]), int(prm["offset"][b]), i)
+
+        def run(reps):
+            ts = []
+            for _ in range(reps):
+                a = time.perf_counter()
+                for b in range(B):
+                    orc.spec_verify_seq(tg[b], dr[b], tok[b], float(prm["temperature"][b]), words[b])
+                ts.append(time.perf_counter() - a)
+            return float(np.median(ts))
+
+        dt, reps = _timed(run)
+        return {"value": round(B / dt, 1), "unit": "sequences/s", "cores": 1, "kind": "port",
+                "cpu": cpu_model(), "nproc": nproc,
+                "sample": (f"the oracle's C restatement (tmo_spec_verify_seq; the reference has no "
+                           f"stochastic verify) over the same {B} sequences x {k} drafts, V="
+                           f"{tg.shape[2]}, one thread, median of {reps} passes; "
+                           f"{time.perf_counter() - t0:.1f} s wall")}
+    ref = oracle.reference()
+    if ref is None:
+        return None
+    if cfg == 2:
+        x = w["logits"]
+        groups = [(x, dict(recent=w["recent"], window=256, penalty=1.1, mask=w["mask"]),
+                   (0.7, 40, 0.95, False))]
+        what = "mask -> apply_repeat_penalty 1.1/256 -> sample T=0.7 k=40 p=0.95"
+    elif cfg == 3:
+        x = w["logits"].astype(np.float32)   # fp16 widened before the timed region
+        groups = [(x, dict(mask=w["mask"]), (1.0, x.shape[1], 0.9, False))]
+        what = "fp16 rows widened beforehand; mask -> sample T=1.0 k=V p=0.9"
+    else:
+        from tensormark_amd import workloads
+
+        x = workloads.bf16_bits_to_f32(w["logits"])   # bf16 widened before the timed region
+        g = np.asarray(w["params"]["greedy"]) != 0
+        rec = w["recent"]
+        groups = []
+        for sel, greedy in ((~g, False), (g, True)):
+            groups.append((np.ascontiguousarray(x[sel]),
+                           dict(recent=np.ascontiguousarray(rec[sel]), window=512, penalty=1.05),
+                           (1.2, 100, 0.98, greedy)))
+        what = ("bf16 rows widened beforehand; apply_repeat_penalty 1.05/512 -> sample T=1.2 k=100 "
+                "p=0.98 on the sampled half, greedy on the other half (two pools, times added)")
+    B, V = x.shape
+
+    def run_all(thr, rows=None):
+        def run(reps):
+            tot = 0.0
+            for xx, kw, (T, k, p, gr) in groups:
+                kk = dict(kw)
+                xs = xx if rows is None else xx[:rows]
+                if rows is not None:
+                    for key in ("recent", "mask"):
+                        if kk.get(key) is not None:
+                            kk[key] = kk[key][:rows]
+                d, _ = ref.bench(xs, T, k, p, threads=thr, reps=reps, greedy=gr, **kk)
+                tot += d
+            return tot
+        return run
+
+    dt, reps = _timed(run_all(threads))
+    dt1 = run_all(1, rows=4)(5)
+    n1 = 4 * len(groups)
     return {
         "value": round(B / dt, 1),
         "unit": "rows/s",
         "cores": threads,
         "kind": "reference",
-        "one_core": round(8 / dt1, 1),
+        "one_core": round(n1 / dt1, 1),
         "cpu": cpu_model(),
         "nproc": nproc,
-        "sample": (f"the reference tmsample.h compiled -O3 (mask -> apply_repeat_penalty 1.1/256 -> "
-                   f"sample T=0.7 k=40 p=0.95) over the same {B} x {x.shape[1]} fp32 rows, rows dealt "
-                   f"to {threads} threads (the GPU box's CPU share; nproc {nproc}), median of {reps} "
-                   f"passes; one_core: 8 rows on 1 thread, median of 5; {wall:.1f} s wall in all; "
-                   f"frequency/presence/min-p are absent from the reference"),
+        "sample": (f"the reference tmsample.h compiled -O3 ({what}) over the same {B} x {V} rows, "
+                   f"rows dealt to {threads} threads (the GPU box's CPU share; nproc {nproc}), "
+                   f"median of {reps} passes; one_core: {n1} rows on 1 thread, median of 5; "
+                   f"{time.perf_counter() - t0:.1f} s wall in all; frequency/presence/min-p are "
+                   f"absent from the reference"),
     }
 
 
@@ -180,7 +247,7 @@ def measure_traffic(args):
             name = row["Kernel_Name"]
             if "copyBuffer" in name:
                 copy.append((int(row["Dispatch_Id"]), v))
-            elif "tms::" in name:
+            elif "tms::" in name or "_ZN3tms" in name:
                 tms.append(v)
         shutil.rmtree(out, ignore_errors=True)
         if len(copy) < 3 or not tms:

@@ -253,7 +253,7 @@ int tms_sample_batch(tms_context* ctx, const tms_sample_args* args, hipStream_t 
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  No counterpart in the
  * reference.  Same arguments, semantics and results as tms_sample_batch;
- * the workspace is a fixed 18.9 MB device array inside the library (one
+ * the workspace is a fixed 21.0 MB device array inside the library (one
  * copy per device, held until the process ends), so batch <= 64 rows and
  * vocab <= 262144 ids, else TMS_ERR_CAPACITY.  Runs on the current device
  * (the stream's device must be current).  The first call on each device

@@ -299,7 +299,7 @@ class Ref:
         return tok, w0.value, w1.value, used.value
 
     def bench(self, logits, temperature, top_k, top_p, recent=None, window=0, penalty=1.0,
-              mask=None, threads=1, reps=1):
+              mask=None, threads=1, reps=1, greedy=False):
         logits = np.ascontiguousarray(logits, np.float32)
         B, V = logits.shape
         r = None if recent is None else np.ascontiguousarray(recent, np.int32)
@@ -307,7 +307,7 @@ class Ref:
         toks = np.zeros(B, np.int32)
         dt = self.lib.ref_bench(_p(logits, C.c_float), C.c_int(B), C.c_int(V),
                                 C.c_float(temperature), C.c_int(top_k), C.c_float(top_p),
-                                _p(r, C.c_int32), C.c_int(0 if r is None else r.shape[1]),
+                                C.c_int(1 if greedy else 0), _p(r, C.c_int32), C.c_int(0 if r is None else r.shape[1]),
                                 C.c_int(window), C.c_float(penalty), _p(m, C.c_uint32),
                                 C.c_int(0 if m is None else m.shape[1]), C.c_int(threads),
                                 C.c_int(reps), _p(toks, C.c_int32))

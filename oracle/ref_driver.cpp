@@ -142,7 +142,7 @@ int ref_sample(const float* logits, int V, float T, int top_k, float top_p, int 
 // CPU baseline: sample B rows with `threads` workers, `reps` times; returns
 // the median wall time of one pass in seconds.  Rows are independent, so they
 // are dealt round-robin to the workers.
-double ref_bench(const float* logits, int B, int V, float T, int top_k, float top_p,
+double ref_bench(const float* logits, int B, int V, float T, int top_k, float top_p, int greedy,
                  const std::int32_t* recent, int recent_stride, int window, float penalty,
                  const std::uint32_t* mask, int mask_stride, int threads, int reps,
                  std::int32_t* tokens) {
@@ -157,7 +157,7 @@ double ref_bench(const float* logits, int B, int V, float T, int top_k, float to
                 std::mt19937 rng(1234u + static_cast<unsigned>(w));
                 for (int b = w; b < B; b += threads)
                     tokens[b] = one_row(logits + static_cast<std::size_t>(b) * V, V, T, top_k,
-                                        top_p, 0, rng,
+                                        top_p, greedy, rng,
                                         recent ? recent + static_cast<std::size_t>(b) * recent_stride
                                                : nullptr,
                                         recent_stride, window, penalty,
