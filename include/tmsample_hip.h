@@ -464,7 +464,8 @@ int tms_embed_gather(const void* table, int dtype, int64_t rows, int64_t dim, co
  * Test hooks.  Run the device Philox4x32-10 on n (counter[4], key[2])
  * tuples packed as 6 words each and write 4 words each; evaluate the device
  * double exp on n inputs (which = 0: the HIP math library, 1: the
- * library's own exp used by tms_spec_verify).
+ * library's own exp used by tms_spec_verify, 2: tms_spec_verify's weight
+ * q44(exp(x)) for x <= 0 as a double, the integer count of 2^-44 units).
  */
 int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipStream_t stream);
 /* Checks of the device ordering the cross-workgroup protocols rely on

@@ -42,8 +42,6 @@ struct tms_context {
     uint32_t* spec_tickets;    // [max_batch][kCounterStride] verify arrival counters (word 0)
     uint64_t* spec_parts;      // [max_batch][kSpecParts][2] published partial sums
     tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]
-    uint64_t* spec_zparts;     // [max_batch][2 * kSpecMaxK + 1][spec_chunks] chunk statistics, 2 words each
-    int spec_chunks;           // ceil(max_vocab / 4096)
     uint32_t* dqueue;          // whole-row pass queue: 3 counters, then [max_batch] rows
     int32_t* ov_n;             // [max_batch] history pre-pass: list lengths (-1: overflow)
     int32_t* ov_ids;           // [max_batch][TMS_HISTORY_MAX_IDS] listed ids

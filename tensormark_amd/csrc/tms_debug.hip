@@ -29,7 +29,7 @@ __global__ void exp_kernel(const double* in, double* out, int n, int which) {
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    out[i] = which ? exp64(in[i], tab) : exp(in[i]);
+    out[i] = which == 2 ? (double)q44_exp_nonpos(in[i], tab) : which ? exp64(in[i], tab) : exp(in[i]);
 }
 
 // ---- ordering checks (tms_debug_ordering)
@@ -173,7 +173,7 @@ extern "C" int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipS
 }
 
 extern "C" int tms_debug_exp(const double* in, double* out, int n, int which, hipStream_t stream) {
-    if (!in || !out || n < 0 || (which != 0 && which != 1)) return TMS_ERR_INVALID_ARG;
+    if (!in || !out || n < 0 || which < 0 || which > 2) return TMS_ERR_INVALID_ARG;
     if (n == 0) return TMS_OK;
     hipLaunchKernelGGL(tms::exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, in, out, n, which);
     return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;

@@ -140,6 +140,31 @@ __device__ __forceinline__ int64_t q44(double y) {
     return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
+// q44(exp64(x)) for x <= 0, bit-identical to the pair above.  Below -40 the
+// weight is 0: exp64(x) < e^-40 < 2^-57, which rounds to 0 on the 2^-44
+// grid.  On [-40, 0] exp64 takes none of its special cases (2^m is normal,
+// m >= -58), and its final scaling by 2^m and q44's by 2^44 are both exact,
+// so they fold into one multiplication by 2^(m + 44).  A NaN gives 0.
+__device__ __forceinline__ int64_t q44_exp_nonpos(double x, const double* tab) {
+    const bool zero = !(x >= -40.0);
+    const double xc = zero ? 0.0 : x;
+    const double kd = floor(xc * 0x1.71547652b82fep+6 + 0.5);
+    double r = fma(-kd, 0x1.62e42fefa39efp-7, xc);
+    r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
+    double p = 1.0 / 120;
+    p = fma(p, r, 1.0 / 24);
+    p = fma(p, r, 1.0 / 6);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    const int ki = (int)kd;
+    const double y = tab[ki & 63] * p;
+    const double s = __longlong_as_double((long long)((ki >> 6) + 44 + 1023) << 52);
+    const double f = floor(y * s + 0.5);
+    const int64_t w = __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
+    return zero ? 0 : w;
+}
+
 // ------------------------------------------------------------ reductions
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {

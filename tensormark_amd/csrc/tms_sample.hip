@@ -1007,9 +1007,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_ss = off_sp + nb * tms::kSpecParts * 2 * sizeof(uint64_t);
     const size_t off_tl = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
     const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kLeanMaxChunksHost);
-    const size_t off_zp = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
-    ctx->spec_chunks = (max_vocab + 4095) / 4096;
-    const size_t off_dq = off_zp + nb * (2 * tms::kSpecMaxK + 1) * (size_t)ctx->spec_chunks * 2 * sizeof(uint64_t);
+    const size_t off_dq = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
     const size_t off_hn = off_dq + 256 * (((tms::kDenseQueueHead + nb) * sizeof(uint32_t) + 255) / 256);
     const size_t off_hi = off_hn + 256 * ((nb * sizeof(int32_t) + 255) / 256);
     const size_t off_hv = off_hi + nb * tms::kHistMax * sizeof(int32_t);
@@ -1041,7 +1039,6 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->spec_parts = (uint64_t*)(p + off_sp);
     ctx->spec_stats = (tms_spec_stat*)(p + off_ss);
     ctx->tlists = (uint64_t*)(p + off_tl);
-    ctx->spec_zparts = (uint64_t*)(p + off_zp);
     ctx->dqueue = (uint32_t*)(p + off_dq);
     ctx->ov_n = (int32_t*)(p + off_hn);
     ctx->ov_ids = (int32_t*)(p + off_hi);

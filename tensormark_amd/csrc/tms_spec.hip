@@ -2,11 +2,13 @@
 //
 // Two launches per call, both stream-ordered:
 //
-//   spec_stats    one workgroup per row (the k + 1 target rows and the k draft
+//   statistics    one record per row (the k + 1 target rows and the k draft
 //                 rows of every sequence): m = max(v / T), the exact integer
 //                 sum Z of the row's weights q44(exp64(v / T - m)), and the
-//                 weight of the row's draft token.  Two passes over the row;
-//                 the second re-reads it from cache.
+//                 weight of the row's draft token.  16-byte aligned rows of
+//                 up to 64K fp32 (32K fp16/bf16) ids: spec_row_kernel, one
+//                 1024-thread workgroup per row holding the row in registers
+//                 (one read); other rows: spec_stats_kernel, two passes.
 //   spec_resolve  B x P workgroups.  Every workgroup of a sequence evaluates
 //                 the accept tests u_i < p_t(x_i) / p_d(x_i) from the row
 //                 statistics (the same decision in each), then sums the
@@ -37,21 +39,15 @@ __constant__ double kSpecExpTab[64] = {TMS_EXP2_64THS};
 constexpr uint64_t kPartReady = 1ull << 63;   // published partial sum is complete
 constexpr int kPartPoll = 1 << 20;            // bound on the finisher's wait per part
 
-constexpr int kSpecChunk = 4096;   // ids per chunk of the chunked statistics
-
-// One chunk's statistics: max of v / T, NaN/+inf flag, share of Z.
-struct SpecPart {
-    float m;
-    int nf;
-    int64_t z;
-};
+constexpr int kRowT = 1024;          // threads of the row kernel
+constexpr int kRowW = kRowT / 64;
 
 struct SArgs {
     const void* target;
     const void* draft;
     int B, k, V;
     bool fast;   // rows 16-byte aligned and V a multiple of the vector width
-    int P, Lp;   // vocabulary parts of the draw and their length
+    int P, Lp;   // vocabulary parts of the two-launch resolve and their length
     const int32_t* tokens;
     const tms_row_params* params;
     const uint32_t* draws;
@@ -60,9 +56,20 @@ struct SArgs {
     int32_t* out_status;
     tms_spec_stat* stats;
     uint64_t* parts;
-    uint32_t* tickets;
-    SpecPart* zparts;   // [B * (2k + 1)][C] chunk statistics
-    int C;              // chunks per row of the chunked statistics (0: spec_stats_kernel)
+    uint32_t* tickets;   // [B][kCounterStride]: resolve parts, or rows of the row kernel
+};
+
+// LDS of a verify workgroup (up to 16 waves).
+struct SpecLds {
+    double tab[64];
+    float shf[kRowW];
+    int64_t shl[2 * kRowW];
+    int64_t part_w[kSpecParts];
+    int64_t part_t[kSpecParts];
+    int misc[kRowW];
+    tms_spec_stat srow[2 * kSpecMaxK + 1];
+    int stok[kSpecMaxK];
+    double su[kSpecMaxK];
 };
 
 __device__ __forceinline__ void load_exp_table(double* tab) {
@@ -116,43 +123,53 @@ __device__ __forceinline__ void for_range2(const T* r0, const T* r1, int lo, int
     }
 }
 
+template <int NW = kWaves>
 __device__ __forceinline__ float block_max_f32(float v, float* sh) {
     v = wave_max_f32(v);
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
     float r = sh[0];
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) r = fmaxf(r, sh[i]);
+    for (int i = 1; i < NW; ++i) r = fmaxf(r, sh[i]);
     __syncthreads();
     return r;
 }
 
+template <int NW = kWaves>
 __device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* sh) {
     v = wave_sum_i64(v);
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
     int64_t r = 0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) r += sh[i];
+    for (int i = 0; i < NW; ++i) r += sh[i];
     __syncthreads();
     return r;
 }
 
+template <int NW = kWaves>
 __device__ __forceinline__ int block_or(int v, int* sh) {
     v = __any(v) ? 1 : 0;
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
     int r = 0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) r |= sh[i];
+    for (int i = 0; i < NW; ++i) r |= sh[i];
     __syncthreads();
     return r;
 }
 
-// Weight of a scaled logit on the 2^-44 grid.
+// v / T.  The hot loops are instantiated twice, DIV false for T = 1 (where
+// the division is the identity) and true otherwise, and pick one per row:
+// a per-element test compiles to a select that still divides.
+template <bool DIV = true>
+__device__ __forceinline__ float scaled(float v, float temp) { return DIV ? v / temp : v; }
+
+// Weight of a scaled logit on the 2^-44 grid: q44(exp64(v / T - m)), where m
+// is the maximum of v / T over the row, so the argument is never positive.
+template <bool DIV = true>
 __device__ __forceinline__ int64_t weight(float v, float temp, double m, const double* tab) {
-    const float l = v / temp;
-    return q44(exp64((double)l - m, tab));
+    return q44_exp_nonpos((double)scaled<DIV>(v, temp) - m, tab);
 }
 
 // Residual weight q44(max(p_t - p_d, 0)) from the two rows' weights.
@@ -180,7 +197,7 @@ __global__ __launch_bounds__(kBlock) void spec_stats_kernel(SArgs a) {
     int nf = 0;
     for_range(row, 0, a.V, a.fast, [&](int, float v) {
         nf |= __builtin_amdgcn_class(v, 0x203);   // NaN or +inf
-        mx = fmaxf(mx, v / temp);
+        mx = fmaxf(mx, scaled(v, temp));
     });
     mx = block_max_f32(mx, shf);   // also orders the table's LDS writes
     nf = block_or(nf, shi);
@@ -211,196 +228,109 @@ __global__ __launch_bounds__(kBlock) void spec_stats_kernel(SArgs a) {
     }
 }
 
-// Chunked statistics (16-byte aligned rows): the vocabulary in chunks of
-// kSpecChunk ids, one workgroup per (row, chunk), in two launches.  Whole
-// rows as work units left a CU in 8 with a third row while the rest idled
-// (544 rows of exp64 work on 256 CUs).
-//   spec_chunk_max_kernel: the chunk's max of v / T and NaN/+inf flag.
-//   spec_chunk_z_kernel:   the row's max and status from its chunks' parts,
-//                          then the chunk's share of Z (exact int64); chunk 0
-//                          writes the row's record: m, status and the draft
-//                          token's weight ex.
-// The resolve kernel sums a row's Z shares (exact in any order).  m, status,
-// Z and ex equal those of spec_stats_kernel.
-template <typename T>
-__global__ __launch_bounds__(kBlock) void spec_chunk_max_kernel(SArgs a) {
+// Loops over a thread's registers (slot sl holds vector t + sl * NT, in
+// while below nv): the max of v / T and the NaN/+inf flag, then the share
+// of Z.
+template <typename T, int NS, int NT, bool DIV>
+__device__ __forceinline__ void row_max(const uint4 (&q)[NS], int nv, float temp, float& mx, int& nf) {
     constexpr int VEC = Elt<T>::kVec;
-    constexpr int NS = kSpecChunk / VEC / kBlock;   // vectors per thread
-    __shared__ float shf[kWaves];
-    __shared__ int shi[kWaves];
     const int t = threadIdx.x;
-    const int g = blockIdx.x / a.C, c = blockIdx.x - g * a.C;
-    const int R = 2 * a.k + 1;
-    const int b = g / R, i = g - b * R;
-    const T* row = spec_row<T>(a, b, i);
-    const float temp = a.params[b].temperature;
-    const int nv = a.V / VEC;
-    const int v0 = c * (kSpecChunk / VEC);
-    uint4 q[NS];
-#pragma unroll
-    for (int sl = 0; sl < NS; ++sl) q[sl] = *(const uint4*)(row + (int64_t)min(v0 + t + sl * kBlock, nv - 1) * VEC);
-    float mx = -__builtin_huge_valf();
-    int nf = 0;
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) {
-        const bool in = v0 + t + sl * kBlock < nv;
+        const bool in = t + sl * NT < nv;
         float x[VEC];
         Elt<T>::widen(q[sl], x);
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
             nf |= in ? __builtin_amdgcn_class(x[e], 0x203) : 0;   // NaN or +inf
-            mx = in ? fmaxf(mx, x[e] / temp) : mx;
+            mx = in ? fmaxf(mx, scaled<DIV>(x[e], temp)) : mx;
         }
     }
-    mx = block_max_f32(mx, shf);
-    nf = block_or(nf, shi);
-    if (t == 0) {
-        // Agent-scope stores: workgroups on different XCDs write neighbouring
-        // records of one cache line, read by the next kernel.
-        uint64_t* w = (uint64_t*)(a.zparts + (int64_t)g * a.C + c);
-        st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)nf << 32));
-        st_agent(&w[1], (uint64_t)0);
-    }
 }
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void spec_chunk_z_kernel(SArgs a) {
+template <typename T, int NS, int NT, bool DIV>
+__device__ __forceinline__ int64_t row_z(const uint4 (&q)[NS], int nv, float temp, double md, const double* tab) {
     constexpr int VEC = Elt<T>::kVec;
-    constexpr int NS = kSpecChunk / VEC / kBlock;
-    __shared__ double tab[64];
-    __shared__ int64_t shl[kWaves];
-    load_exp_table(tab);
     const int t = threadIdx.x;
-    const int g = blockIdx.x / a.C, c = blockIdx.x - g * a.C;
-    const int R = 2 * a.k + 1;
-    const int b = g / R, i = g - b * R;
-    const T* row = spec_row<T>(a, b, i);
-    const float temp = a.params[b].temperature;
-    const int nv = a.V / VEC;
-    const int v0 = c * (kSpecChunk / VEC);
-    uint4 q[NS];
-#pragma unroll
-    for (int sl = 0; sl < NS; ++sl) q[sl] = *(const uint4*)(row + (int64_t)min(v0 + t + sl * kBlock, nv - 1) * VEC);
-    // The row's max and flag from its chunks (every thread reads them all).
-    const SpecPart* parts = a.zparts + (int64_t)g * a.C;
-    float mx = -__builtin_huge_valf();
-    int nf = 0;
-    for (int u = 0; u < a.C; ++u) {
-        const uint64_t w = ld_agent((uint64_t*)(parts + u));
-        mx = fmaxf(mx, __uint_as_float((uint32_t)w));
-        nf |= (int)(w >> 32);
-    }
-    int st = TMS_ROW_OK;
-    if (nf) st = TMS_ROW_NONFINITE;
-    else if (mx == -__builtin_huge_valf()) st = TMS_ROW_ALL_MASKED;
-    else if (mx == __builtin_huge_valf()) st = TMS_ROW_NONFINITE;
-    const double md = (double)mx;
     int64_t z = 0;
-    if (st == TMS_ROW_OK) {
 #pragma unroll
-        for (int sl = 0; sl < NS; ++sl) {
-            float x[VEC];
-            Elt<T>::widen(q[sl], x);
-            if (v0 + t + sl * kBlock < nv) {
+    for (int sl = 0; sl < NS; ++sl) {
+        float x[VEC];
+        Elt<T>::widen(q[sl], x);
+        if (t + sl * NT < nv) {
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) z += weight(x[e], temp, md, tab);
-            }
-        }
-        z = block_sum_i64(z, shl);
-    } else {
-        __syncthreads();   // the table's LDS writes, as block_sum_i64 orders them
-    }
-    if (t == 0) {
-        st_agent((uint64_t*)(a.zparts + (int64_t)g * a.C + c) + 1, (uint64_t)z);
-        const int di = i < a.k ? i : (i > a.k ? i - a.k - 1 : -1);
-        const int x = di >= 0 ? a.tokens[(int64_t)b * a.k + di] : -1;
-        const bool xin = x >= 0 && x < a.V;
-        if (c == 0) {
-            // The whole record from one workgroup (the token's weight by one
-            // scalar load), so no two workgroups write parts of it.
-            const int64_t ex = (st == TMS_ROW_OK && xin) ? weight(Elt<T>::scalar(row + x), temp, md, tab) : 0;
-            uint64_t* w = (uint64_t*)(a.stats + g);
-            st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)st << 32));
-            st_agent(&w[1], (uint64_t)0);
-            st_agent(&w[2], (uint64_t)ex);
-            st_agent(&w[3], (uint64_t)0);
+            for (int e = 0; e < VEC; ++e) z += weight<DIV>(x[e], temp, md, tab);
         }
     }
+    return z;
 }
 
+// The sequence's statistics, draft tokens and accept uniforms staged in LDS
+// (one load or Philox draw per thread), then the accept tests
+// u_i < (e_t * Z_d) / (e_d * Z_t), evaluated identically by every workgroup
+// that runs them.  rej < 0: every draft accepted (the bonus draw).
 template <typename T>
-__global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
-    __shared__ double tab[64];
-    __shared__ int64_t shl[2 * kWaves];
-    __shared__ int64_t part_w[kSpecParts];
-    __shared__ int64_t part_t[kSpecParts];
-    __shared__ int misc[4];
-    load_exp_table(tab);
+__device__ void accept_tests(const SArgs& a, int b, SpecLds& L, int& status, int& acc, int& rej) {
     const int t = threadIdx.x;
-    const int b = blockIdx.x / a.P, p = blockIdx.x - b * a.P;
+    const int R = 2 * a.k + 1;
     const tms_row_params P = a.params[b];
-    const int g0 = b * (2 * a.k + 1);
+    const int g0 = b * R;
     const uint32_t* dw = a.draws ? a.draws + (int64_t)b * (a.k + 1) * 2 : nullptr;
-    // The sequence's statistics, draft tokens and accept uniforms, staged in
-    // LDS with one load (or Philox draw) per thread, so the sequential accept
-    // loop below waits on no memory.  With chunked statistics Z is the sum
-    // of the chunks' shares, gathered the same way.
-    __shared__ tms_spec_stat srow[2 * kSpecMaxK + 1];
-    __shared__ int64_t zrow[2 * kSpecMaxK + 1];
-    __shared__ int stok[kSpecMaxK];
-    __shared__ double su[kSpecMaxK];
-    {
-        const int R = 2 * a.k + 1;
-        if (t < R) {
-            const uint64_t* w = (const uint64_t*)(a.stats + g0 + t);
-            const uint64_t w0 = ld_agent(&w[0]);
-            srow[t].m = __uint_as_float((uint32_t)w0);
-            srow[t].status = (int32_t)(w0 >> 32);
-            srow[t].Z = (int64_t)ld_agent(&w[1]);
-            srow[t].ex = (int64_t)ld_agent(&w[2]);
-            srow[t].pad = 0;
-            zrow[t] = 0;
-        }
-        if (t < a.k) {
-            stok[t] = a.tokens[(int64_t)b * a.k + t];
-            uint32_t w0, w1;
-            if (dw) { w0 = dw[2 * t]; w1 = dw[2 * t + 1]; }
-            else row_words(P.seed, P.offset, (uint32_t)t, w0, w1);
-            su[t] = canonical(w0, w1);
-        }
-        __syncthreads();
-        if (a.C > 0) {
-            for (int idx = t; idx < R * a.C; idx += kBlock)
-                atomicAdd((unsigned long long*)&zrow[idx / a.C],
-                          (unsigned long long)ld_agent((const uint64_t*)(a.zparts + (int64_t)g0 * a.C + idx) + 1));
-            __syncthreads();
-            if (t < R) srow[t].Z = zrow[t];
-            __syncthreads();
-        }
+    if (t < R) {
+        const uint64_t* w = (const uint64_t*)(a.stats + g0 + t);
+        const uint64_t w0 = ld_agent(&w[0]);
+        L.srow[t].m = __uint_as_float((uint32_t)w0);
+        L.srow[t].status = (int32_t)(w0 >> 32);
+        L.srow[t].Z = (int64_t)ld_agent(&w[1]);
+        L.srow[t].ex = (int64_t)ld_agent(&w[2]);
+        L.srow[t].pad = 0;
     }
-
-    // ---- the accept tests, evaluated identically by every workgroup.
-    int status = TMS_ROW_OK, acc = 0, rej = -1;   // rej < 0: all accepted, bonus draw
+    if (t < a.k) {
+        L.stok[t] = a.tokens[(int64_t)b * a.k + t];
+        uint32_t w0, w1;
+        if (dw) { w0 = dw[2 * t]; w1 = dw[2 * t + 1]; }
+        else row_words(P.seed, P.offset, (uint32_t)t, w0, w1);
+        L.su[t] = canonical(w0, w1);
+    }
+    __syncthreads();
+    status = TMS_ROW_OK;
+    acc = 0;
+    rej = -1;
     if (!(P.temperature > 0.0f && P.temperature <= FLT_MAX)) {
         status = TMS_ROW_BAD_PARAMS;
-    } else {
-        acc = a.k;
-        for (int i = 0; i < a.k; ++i) {
-            const tms_spec_stat ts = srow[i], ds = srow[a.k + 1 + i];
-            if (ts.status) { status = ts.status; break; }
-            if (ds.status) { status = ds.status; break; }
-            const int x = stok[i];
-            if (x < 0 || x >= a.V) { status = TMS_ROW_BAD_PARAMS; break; }
-            double r;
-            if (ds.ex == 0) r = ts.ex > 0 ? 1.0 : 0.0;
-            else r = ((double)ts.ex * (double)ds.Z) / ((double)ds.ex * (double)ts.Z);
-            if (su[i] < r) continue;
-            acc = i;
-            rej = i;
-            break;
-        }
-        if (status == TMS_ROW_OK && rej < 0 && srow[a.k].status) status = srow[a.k].status;
+        return;
     }
+    acc = a.k;
+    for (int i = 0; i < a.k; ++i) {
+        const tms_spec_stat ts = L.srow[i], ds = L.srow[a.k + 1 + i];
+        if (ts.status) { status = ts.status; return; }
+        if (ds.status) { status = ds.status; return; }
+        const int x = L.stok[i];
+        if (x < 0 || x >= a.V) { status = TMS_ROW_BAD_PARAMS; return; }
+        double r;
+        if (ds.ex == 0) r = ts.ex > 0 ? 1.0 : 0.0;
+        else r = ((double)ts.ex * (double)ds.Z) / ((double)ds.ex * (double)ts.Z);
+        if (L.su[i] < r) continue;
+        acc = i;
+        rej = i;
+        break;
+    }
+    if (rej < 0 && L.srow[a.k].status) status = L.srow[a.k].status;
+}
+
+// Part p of sequence b's resolution.
+template <typename T>
+__device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
+    const double* tab = L.tab;
+    int64_t* shl = L.shl;
+    int64_t* part_w = L.part_w;
+    int64_t* part_t = L.part_t;
+    int* misc = L.misc;
+    const tms_spec_stat* srow = L.srow;
+    const int t = threadIdx.x;
+    const tms_row_params P = a.params[b];
+    const uint32_t* dw = a.draws ? a.draws + (int64_t)b * (a.k + 1) * 2 : nullptr;
+    int status, acc, rej;
+    accept_tests<T>(a, b, L, status, acc, rej);
     if (status != TMS_ROW_OK) {
         if (p == 0 && t == 0) {
             a.out_acc[b] = 0;
@@ -564,6 +494,67 @@ __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     }
 }
 
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
+    __shared__ SpecLds L;
+    load_exp_table(L.tab);
+    resolve_part<T>(a, blockIdx.x / a.P, blockIdx.x % a.P, L);
+}
+
+// Row statistics for 16-byte aligned rows of at most kRowT x NS vectors:
+// one 1024-thread workgroup per row holds the row in registers (one read)
+// and writes the row's record: m = max(v / T), the status,
+// Z = sum of q44(exp64(v / T - m)) and the draft token's weight, equal to
+// spec_stats_kernel's.  Two workgroups per CU (64 registers a thread) up to
+// 8 vectors a thread.  The parts-wise resolve follows on the stream.
+template <typename T, int NS>
+__global__ __launch_bounds__(kRowT) __attribute__((amdgpu_waves_per_eu(NS <= 8 ? 8 : 4, 8)))
+void spec_row_kernel(SArgs a) {
+    constexpr int VEC = Elt<T>::kVec;
+    __shared__ SpecLds L;
+    load_exp_table(L.tab);
+    const int t = threadIdx.x;
+    const int R = 2 * a.k + 1;
+    const int g = blockIdx.x;
+    const int b = g / R, i = g - b * R;
+    const T* row = spec_row<T>(a, b, i);
+    const float temp = a.params[b].temperature;
+    const bool div = temp != 1.0f;
+    const int nv = a.V / VEC;
+    uint4 q[NS];
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) q[sl] = *(const uint4*)(row + (int64_t)min(t + sl * kRowT, nv - 1) * VEC);
+    float mx = -__builtin_huge_valf();
+    int nf = 0;
+    if (div) row_max<T, NS, kRowT, true>(q, nv, temp, mx, nf);
+    else row_max<T, NS, kRowT, false>(q, nv, temp, mx, nf);
+    mx = block_max_f32<kRowW>(mx, L.shf);   // also orders the table's LDS writes
+    nf = block_or<kRowW>(nf, L.misc);
+    int st = TMS_ROW_OK;
+    if (nf) st = TMS_ROW_NONFINITE;
+    else if (mx == -__builtin_huge_valf()) st = TMS_ROW_ALL_MASKED;
+    else if (mx == __builtin_huge_valf()) st = TMS_ROW_NONFINITE;
+    const double md = (double)mx;
+    int64_t z = 0;
+    if (st == TMS_ROW_OK)
+        z = div ? row_z<T, NS, kRowT, true>(q, nv, temp, md, L.tab) : row_z<T, NS, kRowT, false>(q, nv, temp, md, L.tab);
+    z = block_sum_i64<kRowW>(z, L.shl);
+    if (t == 0) {
+        const int di = i < a.k ? i : (i > a.k ? i - a.k - 1 : -1);
+        int64_t ex = 0;
+        if (st == TMS_ROW_OK && di >= 0) {
+            const int x = a.tokens[(int64_t)b * a.k + di];
+            if (x >= 0 && x < a.V) ex = weight(Elt<T>::scalar(row + x), temp, md, L.tab);
+        }
+        uint64_t* w = (uint64_t*)(a.stats + g);
+        st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)st << 32));
+        st_agent(&w[1], (uint64_t)z);
+        st_agent(&w[2], (uint64_t)ex);
+        st_agent(&w[3], (uint64_t)0);
+    }
+}
+
 }  // namespace tms
 
 extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStream_t stream) {
@@ -603,28 +594,34 @@ extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStre
     s.stats = ctx->spec_stats;
     s.parts = ctx->spec_parts;
     s.tickets = ctx->spec_tickets;
-    s.zparts = (tms::SpecPart*)ctx->spec_zparts;
-    s.C = s.fast ? (a->vocab + tms::kSpecChunk - 1) / tms::kSpecChunk : 0;
-    static_assert(sizeof(tms::SpecPart) == 2 * sizeof(uint64_t), "chunk statistics layout");
+    // 16-byte aligned rows of at most kRowT x 16 vectors (fp32) or x 4
+    // (fp16, bf16: 8 spill): the row kernel (two workgroups per CU up to 8
+    // vectors a thread); others: the per-row statistics.  Then the resolve.
+    const int R = 2 * a->k + 1;
+    const int slots = (a->vocab / vec + tms::kRowT - 1) / tms::kRowT;
+    const int max_ns = esz == 4 ? 16 : 4;
+    const int row_ns = (!s.fast || slots > max_ns) ? 0 : slots <= 4 ? 4 : slots <= 8 ? 8 : 16;
     const dim3 block(tms::kBlock);
-    const dim3 g1((unsigned)(a->batch * (2 * a->k + 1))), g2((unsigned)(a->batch * s.P));
-    // 16-byte aligned rows take the chunked statistics; others the per-row
-    // kernel.
-    const dim3 gc((unsigned)(a->batch * (2 * a->k + 1) * (s.C > 0 ? s.C : 1)));
-#define TMS_SPEC_LAUNCH(T)                                                                 \
+    const dim3 g1((unsigned)(a->batch * R)), g2((unsigned)(a->batch * s.P));
+    const dim3 brow(tms::kRowT);
+#define TMS_SPEC_LAUNCH(T, NS2, NS3)                                                       \
     do {                                                                                   \
-        if (s.C > 0) {                                                                     \
-            hipLaunchKernelGGL(tms::spec_chunk_max_kernel<T>, gc, block, 0, stream, s);    \
-            hipLaunchKernelGGL(tms::spec_chunk_z_kernel<T>, gc, block, 0, stream, s);      \
+        if (row_ns > 0) {                                                                  \
+            if (row_ns == 4)                                                               \
+                hipLaunchKernelGGL((tms::spec_row_kernel<T, 4>), g1, brow, 0, stream, s);  \
+            else if (row_ns == 8)                                                          \
+                hipLaunchKernelGGL((tms::spec_row_kernel<T, NS2>), g1, brow, 0, stream, s);\
+            else                                                                           \
+                hipLaunchKernelGGL((tms::spec_row_kernel<T, NS3>), g1, brow, 0, stream, s);\
         } else {                                                                           \
             hipLaunchKernelGGL(tms::spec_stats_kernel<T>, g1, block, 0, stream, s);        \
         }                                                                                  \
-        hipLaunchKernelGGL(tms::spec_resolve_kernel<T>, g2, block, 0, stream, s);         \
+        hipLaunchKernelGGL(tms::spec_resolve_kernel<T>, g2, block, 0, stream, s);          \
     } while (0)
     switch (a->dtype) {
-        case TMS_DTYPE_F32: TMS_SPEC_LAUNCH(float); break;
-        case TMS_DTYPE_F16: TMS_SPEC_LAUNCH(_Float16); break;
-        default: TMS_SPEC_LAUNCH(tms::Bf16); break;
+        case TMS_DTYPE_F32: TMS_SPEC_LAUNCH(float, 8, 16); break;
+        case TMS_DTYPE_F16: TMS_SPEC_LAUNCH(_Float16, 4, 4); break;   // row_ns is 4 or 0
+        default: TMS_SPEC_LAUNCH(tms::Bf16, 4, 4); break;              // row_ns is 4 or 0
     }
 #undef TMS_SPEC_LAUNCH
     return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;

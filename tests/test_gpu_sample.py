@@ -81,6 +81,24 @@ def test_exp64_device_bitwise_equals_oracle(orc):
     assert np.array_equal(y.view(np.uint64), want.view(np.uint64))
 
 
+def test_q44_weight_fast_path_bitwise_equals_oracle(orc):
+    """The verify weight q44(exp64(x)) for x <= 0 through the device's folded
+    form equals the oracle's two-step form bit for bit, including the -40
+    cut-off, where the weight reaches 0, and the grid's rounding midpoints."""
+    import torch
+
+    from tensormark_amd.sampler import debug_exp
+
+    rng = np.random.default_rng(2)
+    xs = np.concatenate([-rng.random(100000) * 45, -rng.random(2000) * 800, -rng.random(2000) * 1e-6,
+                         [0.0, -0.0, -40.0, np.nextafter(-40.0, 0), np.nextafter(-40.0, -50), -31.0,
+                          -30.49, -745.0, -np.inf]])
+    y = debug_exp(torch.from_numpy(xs).to("cuda:0"), 2).cpu().numpy()
+    want = np.array([float(orc.lib.tmo_q44(orc.exp64(float(v)))) for v in xs])
+    assert np.array_equal(y, want)
+    assert (want[xs < -40] == 0).all() and want[xs == 0.0].max() == 2.0 ** 44
+
+
 def test_device_libm_exp_vs_glibc_report():
     """The sampler's fp64 softmax uses the HIP math library's exp where the
     reference uses glibc's.  Report how often they differ (at most 1 ulp)."""
