@@ -1201,16 +1201,24 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
         // that runs in several rounds keeps each workgroup (16 waves) through
         // its serial tail; there the general kernel is faster (B = 1024,
         // V = 256000 bf16: 336 us against 234 us).
-        const int cap = tms::kWideChunkVecs * vec;
-        const int s_w = (a->vocab + cap - 1) / cap;
-        const int per_w = (a->vocab + s_w - 1) / s_w;
-        const int ce = (per_w + 31) / 32 * 32;
-        if (s_w <= tms::kWideMaxChunksHost && ce <= cap && a->batch * s_w <= 2 * device_cus()) {
-            tms::KArgs kw = k;
-            kw.CE = ce;
-            kw.S = (a->vocab + ce - 1) / ce;
-            kw.dense = nullptr;   // rows that break the promise report TMS_ROW_UNSUPPORTED
-            return tms_launch_wide(kw, a->dtype, fast, a->batch, stream);
+        // fp32 rows whose grid fits one workgroup per CU with 8 vectors a
+        // thread take that form: half the waves to start and to share each
+        // CU's issue slots, and half the lists to merge.
+        const int cus = device_cus();
+        for (int slots : {8, 4}) {
+            if (slots == 8 && esz != 4) continue;
+            const int cap = tms::kWideChunkVecs / 4 * slots * vec;
+            const int s_w = (a->vocab + cap - 1) / cap;
+            const int per_w = (a->vocab + s_w - 1) / s_w;
+            const int ce = (per_w + 31) / 32 * 32;
+            const int resident = (slots == 8 ? 1 : 2) * cus;
+            if (s_w <= tms::kWideMaxChunksHost && ce <= cap && a->batch * s_w <= resident) {
+                tms::KArgs kw = k;
+                kw.CE = ce;
+                kw.S = (a->vocab + ce - 1) / ce;
+                kw.dense = nullptr;   // rows that break the promise report TMS_ROW_UNSUPPORTED
+                return tms_launch_wide(kw, a->dtype, fast, a->batch, slots, stream);
+            }
         }
     }
     if (a->row_kinds == TMS_ROWS_TOPK) {

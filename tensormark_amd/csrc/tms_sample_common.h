@@ -852,7 +852,7 @@ __device__ bool tail_topp_fast(const KArgs& a, int row, const tms_row_params& P,
 // Launches the top-k kernel (tms_topk.hip) over `batch` rows.
 int tms_launch_topk(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
 // Launches the wide top-k kernel (tms_wide.hip) over `batch` rows.
-int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
+int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream);
 // Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.
 int tms_launch_dense(const tms::KArgs& k, int dtype, int workgroups, hipStream_t stream);
 int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,

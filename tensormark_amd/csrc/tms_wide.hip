@@ -38,7 +38,7 @@ namespace wide {
 
 constexpr int kT = 1024;            // threads per workgroup
 constexpr int kW = kT / 64;         // waves per workgroup
-constexpr int kSlots = 4;           // 16-byte slots per thread
+constexpr int kMaxSlots = 8;        // 16-byte slots per thread: 4, or 8 (fp32, one workgroup per CU)
 constexpr int kMaxS = kWideMaxChunksHost;
 constexpr int kKMax = kTopkFast;    // largest K
 constexpr int kLStride = 136;       // u64 per (row, chunk) list: header + kKMax keys, padded
@@ -83,12 +83,13 @@ struct Smem {
     alignas(16) uint64_t slist[kKMax + 8];    // this chunk's sorted top keys
     alignas(16) uint64_t srt[kKMax + 8];      // the row's sorted top-K
     alignas(16) uint32_t gmax[kT / 8];        // order keys of the 8-lane group maxima
-    alignas(16) uint4 hot[kW * kHot * kSlots];   // per wave: the words of its hot lanes
+    alignas(16) uint4 hot[kW * kHot * kMaxSlots];   // per wave: the words of its hot lanes
     int hotlane[kW * kHot];                   // per wave: the lane of each hot slot
     uint32_t tkey;                            // the chunk's bound (order key)
     float vlo;                                // the least value that can be a candidate
     alignas(16) uint32_t wnf[kW];             // per wave: a NaN or +inf seen
     alignas(16) int hist[256];
+    int rcnt[kCap];                 // block rank: the keys above each candidate
     alignas(16) uint64_t mk[kMaxS]; // merge: each list's rm-th key (0 if shorter)
     alignas(16) int mn[kMaxS];      // merge: list lengths
     alignas(16) int mf[kMaxS];      // merge: list flags
@@ -265,29 +266,42 @@ __device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, u
     }
 }
 
-// One wave: the keys keys[0..n) (distinct, 16-byte aligned, followed by a
-// zero word) whose rank (the number of larger keys) is below K land at
-// out[rank] (and at gout[rank] in memory, with agent-scope stores, when gout
-// is given).  Each lane ranks one key a pass, reading the list in 16-byte
-// broadcast reads.
-__device__ __forceinline__ void rank_wave(const uint64_t* keys, int n, int K, uint64_t* out,
-                                          uint64_t* gout) {
-    const int lane = threadIdx.x & 63;
+// The whole workgroup: the keys keys[0..n) (distinct, n <= kCap, 16-byte
+// aligned, followed by a zero word) whose rank is below K land at out[rank]
+// (and at gout[rank] with agent-scope stores, when gout is given).  Thread
+// t counts the keys above key t % R in segment t / R of the list (R the
+// power of two >= n, at least a wave, so a wave reads one segment: 16-byte
+// broadcast reads); the segments' counts meet in rcnt (zero on entry, left
+// nonzero).  Ends with every key placed in out.
+__device__ __forceinline__ void rank_block(const uint64_t* keys, int n, int K, int* rcnt, uint64_t* out,
+                                           uint64_t* gout) {
+    const int t = threadIdx.x;
+    int R = 64;
+    while (R < n) R <<= 1;
+    const int nseg = kT / R;
+    const int len = ((n + nseg - 1) / nseg + 1) & ~1;   // even: segments start on a 16-byte pair
+    const int i = t & (R - 1), j0 = (t / R) * len;
+    const int j1 = min(j0 + len, n);
     const ulonglong2* c2 = (const ulonglong2*)keys;
-    for (int base = 0; base < n; base += 64) {
-        const int i = base + lane;
-        const uint64_t k = i < n ? keys[i] : ~0ull;
+    if (i < n && j0 < j1) {
+        const uint64_t k = keys[i];
         int cnt = 0;
 #pragma unroll 2
-        for (int q = 0; q < (n + 1) >> 1; ++q) {
+        for (int q = j0 >> 1; q < (j1 + 1) >> 1; ++q) {   // a pair past n reads the zero word
             const ulonglong2 y = c2[q];
             cnt += (y.x > k ? 1 : 0) + (y.y > k ? 1 : 0);
         }
-        if (i < n && cnt < K) {
-            out[cnt] = k;
-            if (gout) st_agent(&gout[cnt], k);
+        if (cnt) atomicAdd(&rcnt[i], cnt);
+    }
+    lds_sync();
+    for (int q = t; q < n; q += kT) {
+        const int r = rcnt[q];
+        if (r < K) {
+            out[r] = keys[q];
+            if (gout) st_agent(&gout[r], keys[q]);
         }
     }
+    lds_sync();
 }
 
 // The exact top-K keys of a chunk whose bound admits more than kCap
@@ -388,8 +402,9 @@ __device__ void window_out(uint4& q, uint32_t wb, int off, Smem& sm) {
     q = fold_bits<T>(q, ~wb & ((1u << VEC) - 1u));
 }
 
-template <typename T, bool FAST>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void topk_wide_kernel(KArgs a) {
+template <typename T, bool FAST, int kSlots>
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : 4, 8)))
+void topk_wide_kernel(KArgs a) {
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NV = kSlots * VEC;         // stream values per thread
     constexpr int kChunkIds = kT * NV;       // ids a chunk can hold
@@ -485,6 +500,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
         sm.onf = 0;
         sm.ncand = 0;
     }
+    sm.rcnt[t] = 0;
     lds_sync();
     const bool in_chunk = pn.on && t >= from && t < nrec && wid_raw >= e0 && wid_raw < e1;
     bool owner = false;
@@ -637,55 +653,82 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     }
     vlo = fmaxf(vlo, -FLT_MAX);
     auto key_of = [&](float v, uint32_t id) { return ckey(divide ? v / temp : v, id); };
-    // Candidates are appended as (value bits, id) to one LDS array: one
-    // ballot and one LDS atomic per wave and pass.
-    auto append = [&](bool tk, float x, uint32_t id) {
-        const uint64_t b = __ballot(tk);
-        if (b) {
-            int base = 0;
-            if (lane == 0) base = atomicAdd(&sm.ncand, __popcll(b));
-            base = __builtin_amdgcn_readfirstlane(base);
-            const int p = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-            if (tk && p < kCap) sm.u.c.cand[p] = ((uint64_t)__float_as_uint(x) << 32) | id;
-        }
-    };
+    // Candidates are appended as (value bits, id) to one LDS array: a
+    // ballot per pass and one LDS atomic per wave and round.
     if (select) {
         // A lane holds candidates only if its maximum reaches vlo ("hot").
         const bool hot = m >= vlo;
         const uint64_t hb = __ballot(hot);
         const int nh = __popcll(hb);
         // The hot lanes' words go to LDS, kHot lanes a round, and the wave
-        // examines only those entries, 64 a pass.
+        // examines only those entries, 64 a pass; the owner's value joins
+        // the last round.
         const int hs = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(hb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)hb, 0u));
         uint4* hw = sm.hot + (wv * kHot) * kSlots;
         const T* hv = (const T*)hw;   // hot slot s, entry q: hv[s * NV + q] with q = j * VEC + e
-        for (int g0 = 0; g0 < nh; g0 += kHot) {
-            const int ng = min(nh - g0, kHot);
-            if (hot && hs >= g0 && hs < g0 + kHot) {
+        constexpr int kPass = kHot * NV / 64;
+        for (int g0 = 0; g0 == 0 || g0 < nh; g0 += kHot) {
+            const int ng = max(0, min(nh - g0, kHot));
+            const bool last = g0 + kHot >= nh;
+            if (ng) {
+                if (hot && hs >= g0 && hs < g0 + kHot) {
 #pragma unroll
-                for (int j = 0; j < kSlots; ++j) hw[(hs - g0) * kSlots + j] = raw[j];
-                sm.hotlane[wv * kHot + hs - g0] = lane;
-            }
-            wave_lds_sync();
-            for (int p = 0; p < ng * NV; p += 64) {
-                const int q = p + lane, sidx = q / NV, qi = q % NV;
-                float x = NEG_INF;
-                int id = 0;
-                if (sidx < ng) {
-                    x = Elt<T>::scalar(hv + q);
-                    id = e0 + VEC * ((qi / VEC) * kT + wv * 64 + sm.hotlane[wv * kHot + sidx]) + qi % VEC;
+                    for (int j = 0; j < kSlots; ++j) hw[(hs - g0) * kSlots + j] = raw[j];
+                    sm.hotlane[wv * kHot + hs - g0] = lane;
                 }
-                append(x >= vlo, x, (uint32_t)id);
+                wave_lds_sync();
             }
-            wave_lds_sync();   // the next round writes over these slots
+            uint64_t bits[kPass];
+            float xs[kPass];
+            uint32_t ids[kPass];
+            int total = 0;
+#pragma unroll
+            for (int pi = 0; pi < kPass; ++pi) {
+                bits[pi] = 0ull;
+                xs[pi] = NEG_INF;
+                ids[pi] = 0u;
+                if (pi * 64 < ng * NV) {
+                    const int q = pi * 64 + lane, sidx = q / NV, qi = q % NV;
+                    if (sidx < ng) {
+                        xs[pi] = Elt<T>::scalar(hv + q);
+                        ids[pi] = (uint32_t)(e0 + VEC * ((qi / VEC) * kT + wv * 64 + sm.hotlane[wv * kHot + sidx]) +
+                                             qi % VEC);
+                    }
+                    bits[pi] = __ballot(xs[pi] >= vlo);
+                    total += __popcll(bits[pi]);
+                }
+            }
+            const bool ot = last && owner && own_v >= vlo;
+            const uint64_t ob = __ballot(ot);
+            total += __popcll(ob);
+            if (total) {
+                int base = 0;
+                if (lane == 0) base = atomicAdd(&sm.ncand, total);
+                base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+                for (int pi = 0; pi < kPass; ++pi) {
+                    const uint64_t b = bits[pi];
+                    const int p = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32),
+                                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+                    if (((b >> lane) & 1ull) && p < kCap)
+                        sm.u.c.cand[p] = ((uint64_t)__float_as_uint(xs[pi]) << 32) | ids[pi];
+                    base += __popcll(b);
+                }
+                const int p = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(ob >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)ob, 0u));
+                if (ot && p < kCap) sm.u.c.cand[p] = ((uint64_t)__float_as_uint(own_v) << 32) | (uint32_t)wid_raw;
+            }
+            if (ng) wave_lds_sync();   // the next round writes over these slots
         }
-        append(owner && own_v >= vlo, own_v, (uint32_t)wid_raw);
     }
+#ifdef TMS_TRACE
+    if (t == 0 && a.trace && ticket != 0xDEADBEEFu) a.trace[(blockIdx.x * kW) * 16 + 12] = __builtin_amdgcn_s_memrealtime();
+#endif
     if (t == 0) sm.ticket = ticket;
     lds_sync();
     int ncand = select ? sm.ncand : 0;
     const bool merger = S == 1 || (int)sm.ticket == S - 1;   // the last chunk of the row to arrive
+    WTR(4);
     WSTOP(22, (float)ncand);
     const bool radixed = ncand > kCap;
     if (radixed) {
@@ -703,32 +746,31 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     // of lane i, entry 64 + i in key1); wave 0 holds this chunk's own.
     uint64_t key0 = 0, key1 = 0;
     int ncc = 0;
-    if (wv == 0) {
-        // ---- wave 0 alone (the other waves wait at a barrier or have
-        //      ended): the keys (the division, one per lane), the rank, and
-        //      the publish straight from the rank (every word is non-zero;
-        //      the merger reads a word again while it reads 0)
-        if (select && !radixed) {
-            for (int i = lane; i < ncand; i += 64) {
-                const uint64_t rv = sm.u.c.cand[i];
-                sm.u.c.cand[i] = key_of(__uint_as_float((uint32_t)(rv >> 32)), (uint32_t)rv);
-            }
+    // ---- the keys (the division, one per candidate), the rank (every
+    //      wave), and the publish straight from the rank (every word is
+    //      non-zero; the merger reads a word again while it reads 0).  The
+    //      merger's own list stays in LDS.
+    if (select && !radixed) {
+        for (int i = t; i < ncand; i += kT) {
+            const uint64_t rv = sm.u.c.cand[i];
+            sm.u.c.cand[i] = key_of(__uint_as_float((uint32_t)(rv >> 32)), (uint32_t)rv);
         }
-        if (lane == 0) sm.u.c.cand[ncand] = 0ull;   // rank_wave reads keys in pairs
-        wave_lds_sync();
-        if (sm.onf) flags |= FLAG_NONFINITE;      // a penalised window value
-        // (the merger's own list stays in LDS)
-        if (select) rank_wave(sm.u.c.cand, ncand, K, sm.slist, merger ? nullptr : my + 1);
-        if (!merger && lane == 0) st_agent(&my[0], header(flags, nlist));
-        if (merger) {
-            wave_lds_sync();
-            key0 = lane < nlist ? sm.slist[lane] : 0ull;
-            key1 = lane + 64 < nlist ? sm.slist[lane + 64] : 0ull;
-            ncc = nlist;
-            if (lane == 0) sm.mf[0] = flags;
-        }
-    } else if (!merger) {
+    }
+    if (t == 0) sm.u.c.cand[ncand] = 0ull;   // rank_block reads keys in pairs
+    if (sm.onf) flags |= FLAG_NONFINITE;     // a penalised window value
+    lds_sync();
+    WTR(10);
+    if (select) rank_block(sm.u.c.cand, ncand, K, sm.rcnt, sm.slist, merger ? nullptr : my + 1);
+    WTR(11);
+    if (!merger) {
+        if (t == 0) st_agent(&my[0], header(flags, nlist));
         return;
+    }
+    if (wv == 0) {
+        key0 = lane < nlist ? sm.slist[lane] : 0ull;
+        key1 = lane + 64 < nlist ? sm.slist[lane + 64] : 0ull;
+        ncc = nlist;
+        if (lane == 0) sm.mf[0] = flags;
     } else if (wv == kW - 1 && S < kW) {
         // an idle merger wave: the row's draw words meanwhile
         uint32_t w0 = dw0, w1 = dw1;
@@ -774,7 +816,6 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
     }
     WTR(5);
     WSTOP(3, (float)(key0 + key1));
-    if (!merger) return;   // wave 0 of a chunk that does not merge
 
     // ================= merge (the last chunk of the row)
     WTR(6);
@@ -931,12 +972,15 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(8, 8))) void
 // tms_sample_common.h): same argument block as the general kernel, with
 // k.S <= kWideMaxChunksHost chunks of k.CE ids (a multiple of 32, at most
 // 4096 * the vector width).
-int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream) {
+int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream) {
     const dim3 grid((unsigned)(batch * k.S)), block(tms::wide::kT);
-#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::wide::topk_wide_kernel<T, F>), grid, block, 0, stream, k)
+#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::wide::topk_wide_kernel<T, F, 4>), grid, block, 0, stream, k)
     switch (dtype) {
         case TMS_DTYPE_F32:
-            if (fast) TMS_LAUNCH(float, true);
+            if (slots == 8) {
+                if (fast) hipLaunchKernelGGL((tms::wide::topk_wide_kernel<float, true, 8>), grid, block, 0, stream, k);
+                else hipLaunchKernelGGL((tms::wide::topk_wide_kernel<float, false, 8>), grid, block, 0, stream, k);
+            } else if (fast) TMS_LAUNCH(float, true);
             else TMS_LAUNCH(float, false);
             break;
         case TMS_DTYPE_F16:

@@ -369,12 +369,14 @@ def test_decisions_on_exact_boundaries(sampler, orc, top_k):
         check(g, want, cap)
 
 
-@pytest.mark.parametrize("B,V", [(1, 128256), (7, 70000), (13, 128256), (37, 70000)])
+@pytest.mark.parametrize("B,V", [(1, 128256), (7, 70000), (13, 128256), (37, 70000), (150, 40000)])
 def test_batch_sizes_off_the_xcd_grouping(sampler, orc, B, V):
     """Workgroups map to (row, chunk) so that rows of the first 8 * (B // 8)
     stay whole on one XCD and the rest follow in order: batches that are not
-    a multiple of 8 mix both parts (S = 8 and 5 chunks here).  Half the rows
-    greedy, the rest top-k 40 with the history penalties and a mask."""
+    a multiple of 8 mix both parts (4 and 3 chunks of the 8-slot form here).
+    B = 150, V = 40000 is too many workgroups for one per CU and fits two:
+    fp32 in the 4-slot form (3 chunks).  Half the rows greedy, the rest
+    top-k 40 with the history penalties and a mask."""
     w = workloads.cfg2(B=B, V=V, seed=40 + B, with_mask=True)
     p = w["params"].copy()
     p["greedy"] = (np.arange(B) % 2).astype(np.int32)
