@@ -48,13 +48,17 @@ constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr int kHot = 8;             // lanes a wave examines from LDS (more: every entry in place)
 constexpr int kCap = 1024;          // chunk candidates held in LDS
 constexpr int kPad = 256;           // zero keys after a ranked list (rank_place reads past it)
+constexpr int kList = 128;          // a chunk's candidates published unranked up to this many
 static_assert(kMaxS <= kW, "the merger reads one list per wave");
-static_assert(kLStride >= 1 + kKMax, "list layout");
+static_assert(kLStride >= 1 + kKMax && kLStride >= 1 + kList && kList >= kKMax && kList <= 128, "list layout");
 
-// Header word: ready bit, flags (bits 48-55), list length (bits 32-47).
-__device__ __forceinline__ uint64_t header(int flags, int n) {
-    return kReady | ((uint64_t)(flags & 0xFF) << 48) | ((uint64_t)(n & 0xFFFF) << 32);
+// Header word: ready bit, flags (bits 48-55), list length (bits 32-47),
+// the chunk's two bounds as the top 16 bits of their order keys (bits
+// 16-31: K groups; bits 0-15: ceil(K / S) groups).
+__device__ __forceinline__ uint64_t header(int flags, int n, uint32_t bound) {
+    return kReady | ((uint64_t)(flags & 0xFF) << 48) | ((uint64_t)(n & 0xFFFF) << 32) | bound;
 }
+__device__ __forceinline__ uint32_t hdr_bound(uint64_t h) { return (uint32_t)h; }
 __device__ __forceinline__ int hdr_n(uint64_t h) { return (int)((h >> 32) & 0xFFFF); }
 __device__ __forceinline__ int hdr_flags(uint64_t h) { return (int)((h >> 48) & 0xFF); }
 
@@ -86,11 +90,11 @@ struct Smem {
     alignas(16) uint4 hot[kW * kHot * kMaxSlots];   // per wave: the words of its hot lanes
     int hotlane[kW * kHot];                   // per wave: the lane of each hot slot
     uint32_t tkey;                            // the chunk's bound (order key)
+    uint32_t tkey_rm;                         // the same for ceil(K / S) groups
     float vlo;                                // the least value that can be a candidate
     alignas(16) uint32_t wnf[kW];             // per wave: a NaN or +inf seen
     alignas(16) int hist[256];
-    int rcnt[kCap];                 // block rank: the keys above each candidate
-    alignas(16) uint64_t mk[kMaxS]; // merge: each list's rm-th key (0 if shorter)
+    alignas(16) uint32_t mt[kMaxS]; // merge: each chunk's bound (order key)
     alignas(16) int mn[kMaxS];      // merge: list lengths
     alignas(16) int mf[kMaxS];      // merge: list flags
     alignas(16) int scnt[kMaxS];    // merge: keys of each list that can place
@@ -175,33 +179,15 @@ __device__ __forceinline__ int wave_or_i32(int v) {
     u |= dpp_u32<0x143, 0xC, false>(0u, u);   // row_bcast:31
     return __builtin_amdgcn_readlane((int)u, 63);
 }
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#define TMS_MINSTEP(MOVE)                                                                 \
-    {                                                                                     \
-        const uint64_t w = ((uint64_t)MOVE((uint32_t)(v >> 32)) << 32) | MOVE((uint32_t)v); \
-        v = w < v ? w : v;                                                                \
-    }
-    TMS_MINSTEP(dpp_mov<kQxor1>)
-    TMS_MINSTEP(dpp_mov<kQxor2>)
-    TMS_MINSTEP(dpp_mov<kHalfMirror>)
-    TMS_MINSTEP(dpp_mov<kMirror>)
-#undef TMS_MINSTEP
-    // rows: lanes outside the broadcast keep their own value (old = v)
-    {
-        const uint32_t lo = dpp_u32<0x142, 0xA, false>((uint32_t)v, (uint32_t)v);
-        const uint32_t hi = dpp_u32<0x142, 0xA, false>((uint32_t)(v >> 32), (uint32_t)(v >> 32));
-        const uint64_t w = ((uint64_t)hi << 32) | lo;
-        v = w < v ? w : v;
-    }
-    {
-        const uint32_t lo = dpp_u32<0x143, 0xC, false>((uint32_t)v, (uint32_t)v);
-        const uint32_t hi = dpp_u32<0x143, 0xC, false>((uint32_t)(v >> 32), (uint32_t)(v >> 32));
-        const uint64_t w = ((uint64_t)hi << 32) | lo;
-        v = w < v ? w : v;
-    }
-    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63) << 32) |
-           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+// The maximum over lanes 0 .. 15 (DPP row shifts within row 0).
+__device__ __forceinline__ uint32_t lanes16_max(uint32_t v) {
+    v = max(v, dpp_u32<0x111, 0xF, true>(0u, v));   // row_shr:1
+    v = max(v, dpp_u32<0x112, 0xF, true>(0u, v));   // row_shr:2
+    v = max(v, dpp_u32<0x114, 0xF, true>(0u, v));   // row_shr:4
+    v = max(v, dpp_u32<0x118, 0xF, true>(0u, v));   // row_shr:8
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
 }
+
 // Sum over each aligned group of P lanes (P a power of two <= 16), every
 // lane of the group receiving it.
 __device__ __forceinline__ int group_sum(int v, int P) {
@@ -242,7 +228,8 @@ __device__ __forceinline__ void pick_digit(const int* hist, int remaining, int* 
 // are summed across the P lanes (DPP): P = kT / n rounded down to a power of
 // two (at most 16), so a short list is ranked in a few steps by every wave
 // instead of n steps by a few.
-__device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, uint64_t* out) {
+__device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, uint64_t* out,
+                                           uint64_t* gout = nullptr) {
     const int t = threadIdx.x;
     int P = 16;
     while (P > 1 && P * n > kT) P >>= 1;
@@ -262,46 +249,11 @@ __device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, u
             cnt += (y.x > k ? 1 : 0) + (y.y > k ? 1 : 0);
         }
         cnt = group_sum(cnt, P);
-        if (part == 0 && i < n && cnt < K) out[cnt] = k;
-    }
-}
-
-// The whole workgroup: the keys keys[0..n) (distinct, n <= kCap, 16-byte
-// aligned, followed by a zero word) whose rank is below K land at out[rank]
-// (and at gout[rank] with agent-scope stores, when gout is given).  Thread
-// t counts the keys above key t % R in segment t / R of the list (R the
-// power of two >= n, at least a wave, so a wave reads one segment: 16-byte
-// broadcast reads); the segments' counts meet in rcnt (zero on entry, left
-// nonzero).  Ends with every key placed in out.
-__device__ __forceinline__ void rank_block(const uint64_t* keys, int n, int K, int* rcnt, uint64_t* out,
-                                           uint64_t* gout) {
-    const int t = threadIdx.x;
-    int R = 64;
-    while (R < n) R <<= 1;
-    const int nseg = kT / R;
-    const int len = ((n + nseg - 1) / nseg + 1) & ~1;   // even: segments start on a 16-byte pair
-    const int i = t & (R - 1), j0 = (t / R) * len;
-    const int j1 = min(j0 + len, n);
-    const ulonglong2* c2 = (const ulonglong2*)keys;
-    if (i < n && j0 < j1) {
-        const uint64_t k = keys[i];
-        int cnt = 0;
-#pragma unroll 2
-        for (int q = j0 >> 1; q < (j1 + 1) >> 1; ++q) {   // a pair past n reads the zero word
-            const ulonglong2 y = c2[q];
-            cnt += (y.x > k ? 1 : 0) + (y.y > k ? 1 : 0);
-        }
-        if (cnt) atomicAdd(&rcnt[i], cnt);
-    }
-    lds_sync();
-    for (int q = t; q < n; q += kT) {
-        const int r = rcnt[q];
-        if (r < K) {
-            out[r] = keys[q];
-            if (gout) st_agent(&gout[r], keys[q]);
+        if (part == 0 && i < n && cnt < K) {
+            out[cnt] = k;
+            if (gout) st_agent(&gout[cnt], k);
         }
     }
-    lds_sync();
 }
 
 // The exact top-K keys of a chunk whose bound admits more than kCap
@@ -500,7 +452,6 @@ void topk_wide_kernel(KArgs a) {
         sm.onf = 0;
         sm.ncand = 0;
     }
-    sm.rcnt[t] = 0;
     lds_sync();
     const bool in_chunk = pn.on && t >= from && t < nrec && wid_raw >= e0 && wid_raw < e1;
     bool owner = false;
@@ -611,17 +562,30 @@ void topk_wide_kernel(KArgs a) {
             flags |= (q.x | q.y | q.z | q.w) ? FLAG_NONFINITE : 0;
         }
     }
-    if (!skip && wv == 0) {
+    if (!skip && (wv == 0 || (wv == 1 && S > 1))) {
+        // wave 0: the chunk's bound for K groups; wave 1, meanwhile: for
+        // ceil(K / S) groups (S chunks holding that many each hold K), which
+        // only the merger's pruning uses, to 16 bits
         const uint32_t g0 = sm.gmax[lane], g1 = sm.gmax[lane + 64];
-        uint32_t th = 0;
         // the top 20 key bits: the bound rounds down to a multiple of 2^12
         // (at most 2^-11 relative below the exact K-th group maximum), which
         // keeps it a lower bound
-        for (int bit = 31; bit >= 12; --bit) {
-            const uint32_t cand = th | (1u << bit);
-            if (__popcll(__ballot(g0 >= cand)) + __popcll(__ballot(g1 >= cand)) >= K) th = cand;
+        auto bisect = [&](auto lo, int kg) {
+            uint32_t th = 0;
+#pragma unroll
+            for (int bit = 31; bit >= decltype(lo)::value; --bit) {
+                const uint32_t cand = th | (1u << bit);
+                if (__popcll(__ballot(g0 >= cand)) + __popcll(__ballot(g1 >= cand)) >= kg) th = cand;
+            }
+            return th;
+        };
+        if (wv == 0) {
+            const uint32_t th = bisect(std::integral_constant<int, 12>{}, K);
+            if (lane == 0) sm.tkey = th;
+        } else {
+            const uint32_t th = bisect(std::integral_constant<int, 16>{}, (K + S - 1) / S);
+            if (lane == 0) sm.tkey_rm = th;
         }
-        if (lane == 0) sm.tkey = th;
     }
     lds_sync();
     const uint32_t tkey = sm.tkey;
@@ -721,9 +685,6 @@ void topk_wide_kernel(KArgs a) {
             if (ng) wave_lds_sync();   // the next round writes over these slots
         }
     }
-#ifdef TMS_TRACE
-    if (t == 0 && a.trace && ticket != 0xDEADBEEFu) a.trace[(blockIdx.x * kW) * 16 + 12] = __builtin_amdgcn_s_memrealtime();
-#endif
     if (t == 0) sm.ticket = ticket;
     lds_sync();
     int ncand = select ? sm.ncand : 0;
@@ -737,40 +698,52 @@ void topk_wide_kernel(KArgs a) {
                                (uint32_t)wid_raw, sm);
     }
     WTV(15, ncand);
-    const int nlist = min(ncand, K);
     uint64_t* rl = a.tlists + (int64_t)row * S * kLStride;   // this row's lists
     uint64_t* my = rl + (int64_t)c * kLStride;
-    // The merge bound uses each list's rm-th key, rm = ceil(K / S).
-    const int rm = (K + S - 1) / S;
     // Merger waves 1 .. S - 1 hold the other lists (wave w: entry i in key0
     // of lane i, entry 64 + i in key1); wave 0 holds this chunk's own.
     uint64_t key0 = 0, key1 = 0;
     int ncc = 0;
-    // ---- the keys (the division, one per candidate), the rank (every
-    //      wave), and the publish straight from the rank (every word is
-    //      non-zero; the merger reads a word again while it reads 0).  The
+    // ---- the keys (the division, one per candidate) and the publish
+    //      (every word is non-zero; the merger reads a word again while it
+    //      reads 0).  Up to kList candidates go out as they are, unranked;
+    //      more are ranked first and their top K go out.  The header
+    //      carries the chunk's bound, from which the merger prunes.  The
     //      merger's own list stays in LDS.
-    if (select && !radixed) {
-        for (int i = t; i < ncand; i += kT) {
-            const uint64_t rv = sm.u.c.cand[i];
-            sm.u.c.cand[i] = key_of(__uint_as_float((uint32_t)(rv >> 32)), (uint32_t)rv);
-        }
-    }
-    if (t == 0) sm.u.c.cand[ncand] = 0ull;   // rank_block reads keys in pairs
     if (sm.onf) flags |= FLAG_NONFINITE;     // a penalised window value
-    lds_sync();
+    const bool ranked = ncand > kList;
+    const int nlist = ranked ? K : ncand;
+    // the two bounds, each rounded down to 16 bits (still lower bounds)
+    const uint32_t bound = select ? ((tkey >> 16) << 16) | (S > 1 ? sm.tkey_rm >> 16 : 0u) : 0u;
+    for (int i = t; i < ncand; i += kT) {
+        uint64_t key = sm.u.c.cand[i];
+        if (!radixed) {
+            key = key_of(__uint_as_float((uint32_t)(key >> 32)), (uint32_t)key);
+            sm.u.c.cand[i] = key;
+        }
+        if (!merger && !ranked) st_agent(&my[1 + i], key);
+    }
     WTR(10);
-    if (select) rank_block(sm.u.c.cand, ncand, K, sm.rcnt, sm.slist, merger ? nullptr : my + 1);
+    if (ranked) {
+        if (t < kPad) sm.u.c.cand[ncand + t] = 0ull;   // rank_place reads past the keys
+        lds_sync();
+        rank_place(sm.u.c.cand, ncand, K, sm.slist, merger ? nullptr : my + 1);
+    }
     WTR(11);
     if (!merger) {
-        if (t == 0) st_agent(&my[0], header(flags, nlist));
+        if (t == 0) st_agent(&my[0], header(flags, nlist, bound));
         return;
     }
+    lds_sync();   // the own list (keys or ranked) is in LDS
     if (wv == 0) {
-        key0 = lane < nlist ? sm.slist[lane] : 0ull;
-        key1 = lane + 64 < nlist ? sm.slist[lane + 64] : 0ull;
+        const uint64_t* own = ranked ? sm.slist : sm.u.c.cand;
+        key0 = lane < nlist ? own[lane] : 0ull;
+        key1 = lane + 64 < nlist ? own[lane + 64] : 0ull;
         ncc = nlist;
-        if (lane == 0) sm.mf[0] = flags;
+        if (lane == 0) {
+            sm.mf[0] = flags;
+            sm.mt[0] = bound;
+        }
     } else if (wv == kW - 1 && S < kW) {
         // an idle merger wave: the row's draw words meanwhile
         uint32_t w0 = dw0, w1 = dw1;
@@ -786,7 +759,7 @@ void topk_wide_kernel(KArgs a) {
         // header and keys at once; a word still in flight reads 0
         uint64_t h = ld_agent(&L[0]);
         uint64_t k0 = ld_agent(&L[1 + lane]);
-        uint64_t k1 = K > 64 ? ld_agent(&L[65 + lane]) : 0ull;
+        uint64_t k1 = ld_agent(&L[65 + lane]);   // unranked lists hold up to kList
         int spins = 0;
         while (!(h & kReady) && spins < kPollCap) {
             h = ld_agent(&L[0]);
@@ -806,7 +779,10 @@ void topk_wide_kernel(KArgs a) {
         key0 = lane < n ? k0 : 0ull;
         key1 = lane + 64 < n ? k1 : 0ull;
         ncc = n;
-        if (lane == 0) sm.mf[wv] = hdr_flags(h);
+        if (lane == 0) {
+            sm.mf[wv] = hdr_flags(h);
+            sm.mt[wv] = hdr_bound(h);
+        }
         // every word read goes back to zero for the next call
         if (!lost) {
             if (lane < n) st_agent(&L[1 + lane], (uint64_t)0);
@@ -821,38 +797,27 @@ void topk_wide_kernel(KArgs a) {
     WTR(6);
     WSTOP(4, (float)nlist);
     if (t == 0 && S > 1) st_agent(&a.counters[row * kCounterStride], 0u);
-    if (wv < S) {
-        // the list's rm-th key (0 when it holds fewer)
-        uint64_t kr = 0;
-        if (ncc >= rm) {
-            const uint64_t src = rm <= 64 ? key0 : key1;
-            const int l = (rm - 1) & 63;
-            kr = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(src >> 32), l) << 32) |
-                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)src, l);
-        }
-        if (lane == 0) {
-            sm.mn[wv] = ncc;
-            sm.mk[wv] = kr;
-        }
-    }
+    if (wv < S && lane == 0) sm.mn[wv] = ncc;
     lds_sync();
 
     WTR(7);
     WSTOP(5, (float)(key0 + key1));
-    // the lists' flags, lengths and rm-th keys: lane l reads list l, and
-    // wave reductions give each wave the totals
-    int fo, ntot, nlong;
-    uint64_t tm;
+    // the lists' flags, lengths and bounds: lane l reads list l, and wave
+    // reductions give each wave the totals and the largest bound
+    int fo, ntot;
+    uint32_t tmax;
     {
         const bool in = lane < S;
         const int f = in ? sm.mf[lane] : 0, n = in ? sm.mn[lane] : 0;
-        const bool lg = in && n >= rm;
-        uint64_t k = lg ? sm.mk[lane] : ~0ull;
         fo = wave_or_i32(f);
         ntot = wave_sum_dpp(n);
-        nlong = __popcll(__ballot(lg));
-        tm = wave_min_u64(k);
+        const uint32_t b = in ? sm.mt[lane] : 0u;
+        // the largest K-group bound, and the least ceil(K / S)-group bound
+        const uint32_t bk = lanes16_max(in ? b & 0xFFFF0000u : 0u);
+        const uint32_t brm = ~lanes16_max(in ? ~(b << 16) : 0u);
+        tmax = max(bk, brm);
     }
+    WTR(12);
     int status = TMS_ROW_OK;
     if (sm.lost) status = TMS_ROW_INTERNAL;
     else if (bad_params) status = TMS_ROW_BAD_PARAMS;
@@ -876,16 +841,26 @@ void topk_wide_kernel(KArgs a) {
         return;
     }
 
-    // ---- rank merge.  When the lists holding rm keys number at least
-    //      K / rm, the least of their rm-th keys bounds the row's K-th key
-    //      from below (they hold K keys at or above it); only keys at or
-    //      above it can place.  They are compacted and ranked among
-    //      themselves (the set is closed upward, so the ranks are the row's).
+    // ---- rank merge.  Chunk c holds K entries at or above its bound tau_c
+    //      (K groups, each with a distinct entry at or above it) and
+    //      ceil(K / S) at or above its bound rho_c, so the row's K-th largest
+    //      value is at least T = max(max_c tau_c, min_c rho_c), and each of
+    //      the row's top K keys has a quotient at least fl(T / temp) (the
+    //      division is monotone).  Each of the row's top K keys is in its
+    //      chunk's list: fewer than K keys of its chunk are above it, so it
+    //      is at or above the chunk's bound (a candidate) and in a ranked
+    //      list's top K.  The keys at or above that quotient are compacted
+    //      and ranked among themselves: they hold the row's top K, so a key
+    //      ranks below K there exactly when it does in the row, at the same
+    //      rank.  A bound below -FLT_MAX prunes nothing.
     {
-        const uint64_t tg = nlong * rm >= K ? tm : 0ull;
-        const int lim = min(ncc, K);
-        const bool s0 = wv < S && lane < lim && key0 >= tg;
-        const bool s1 = wv < S && lane + 64 < lim && key1 >= tg;
+        uint64_t tg = 0ull;
+        if (tmax >= okey(-FLT_MAX)) {
+            const float tb = okey_inv(tmax);
+            tg = (uint64_t)okey(divide ? tb / temp : tb) << 32;
+        }
+        const bool s0 = wv < S && lane < ncc && key0 >= tg;
+        const bool s1 = wv < S && lane + 64 < ncc && key1 >= tg;
         const uint64_t b0 = __ballot(s0), b1 = __ballot(s1);
         if (wv < S && lane == 0) sm.scnt[wv] = __popcll(b0) + __popcll(b1);
         WSTOP(51, (float)(b0 + b1));
@@ -901,6 +876,7 @@ void topk_wide_kernel(KArgs a) {
         if (s1) sm.u.surv[off + __popcll(b0) + r1] = key1;
         if (t < kPad) sm.u.surv[nsurv + t] = 0ull;
         lds_sync();
+        WTR(13);
         WTV(14, nsurv);
         WSTOP(52, (float)nsurv);
         rank_place(sm.u.surv, nsurv, K, sm.srt);
