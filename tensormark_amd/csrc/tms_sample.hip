@@ -1202,17 +1202,21 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
         // its serial tail; there the general kernel is faster (B = 1024,
         // V = 256000 bf16: 336 us against 234 us).
         // fp32 rows whose grid fits one workgroup per CU with 8 vectors a
-        // thread take that form: half the waves to start and to share each
-        // CU's issue slots, and half the lists to merge.
+        // thread take that form: half the waves to start and half the lists
+        // to merge.  (512 threads of 16 vectors were slower: 18.5 against
+        // 16.9 us at B = 64, V = 128256; the stream and the hot-lane select
+        // take longer with fewer waves.)
         const int cus = device_cus();
-        for (int slots : {8, 4}) {
-            if (slots == 8 && esz != 4) continue;
-            const int cap = tms::kWideChunkVecs / 4 * slots * vec;
+        struct Form { int slots, nt, per_cu; };
+        for (const Form f : {Form{8, 1024, 1}, Form{4, 1024, 2}}) {
+            if (f.slots > 4 && esz != 4) continue;
+            if (a->recent && a->recent_stride > f.nt) continue;
+            const int cap = f.nt * f.slots * vec;
             const int s_w = (a->vocab + cap - 1) / cap;
             const int per_w = (a->vocab + s_w - 1) / s_w;
             const int ce = (per_w + 31) / 32 * 32;
-            const int resident = (slots == 8 ? 1 : 2) * cus;
-            if (s_w <= tms::kWideMaxChunksHost && ce <= cap && a->batch * s_w <= resident) {
+            if (s_w <= f.nt / 64 && ce <= cap && a->batch * s_w <= f.per_cu * cus) {
+                const int slots = f.slots;
                 tms::KArgs kw = k;
                 kw.CE = ce;
                 kw.S = (a->vocab + ce - 1) / ce;

@@ -36,9 +36,9 @@
 namespace tms {
 namespace wide {
 
-constexpr int kT = 1024;            // threads per workgroup
-constexpr int kW = kT / 64;         // waves per workgroup
-constexpr int kMaxSlots = 8;        // 16-byte slots per thread: 4, or 8 (fp32, one workgroup per CU)
+constexpr int kTMax = 1024;         // threads per workgroup, at most
+constexpr int kWMax = kTMax / 64;   // waves per workgroup, at most
+constexpr int kWaveSlots = 128;     // waves x slots per thread, at most (32768 ids a chunk in fp32)
 constexpr int kMaxS = kWideMaxChunksHost;
 constexpr int kKMax = kTopkFast;    // largest K
 constexpr int kLStride = 136;       // u64 per (row, chunk) list: header + kKMax keys, padded
@@ -47,9 +47,8 @@ constexpr int kCntBits = 11;        // occurrence count bits of a table word (<=
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr int kHot = 8;             // lanes a wave examines from LDS (more: every entry in place)
 constexpr int kCap = 1024;          // chunk candidates held in LDS
-constexpr int kPad = 256;           // zero keys after a ranked list (rank_place reads past it)
+constexpr int kPad = 256;           // slack after a ranked list (rank_place reads past it)
 constexpr int kList = 128;          // a chunk's candidates published unranked up to this many
-static_assert(kMaxS <= kW, "the merger reads one list per wave");
 static_assert(kLStride >= 1 + kKMax && kLStride >= 1 + kList && kList >= kKMax && kList <= 128, "list layout");
 
 // Header word: ready bit, flags (bits 48-55), list length (bits 32-47),
@@ -71,7 +70,7 @@ __device__ uint32_t kNoDraws[2] = {0u, 0u};
 __device__ int32_t kNoHistory[1] = {-1};
 
 struct Smem {
-    uint32_t wbits[kT];             // window ids of the chunk, one bit per id (<= 32768 ids)
+    uint32_t wbits[1024];           // window ids of the chunk, one bit per id (<= 32768 ids)
     uint32_t wtab[kHash];           // window ids: chunk offset << kCntBits | occurrences, or kEmpty
     float wval[kHash];              // each window id's masked value
     alignas(16) union {
@@ -86,19 +85,18 @@ struct Smem {
     } u;
     alignas(16) uint64_t slist[kKMax + 8];    // this chunk's sorted top keys
     alignas(16) uint64_t srt[kKMax + 8];      // the row's sorted top-K
-    alignas(16) uint32_t gmax[kT / 8];        // order keys of the 8-lane group maxima
-    alignas(16) uint4 hot[kW * kHot * kMaxSlots];   // per wave: the words of its hot lanes
-    int hotlane[kW * kHot];                   // per wave: the lane of each hot slot
+    alignas(16) uint32_t gmax[128];           // order keys of the 128 lane-group maxima
+    alignas(16) uint4 hot[kHot * kWaveSlots]; // per wave: the words of its hot lanes
+    int hotlane[kWMax * kHot];                // per wave: the lane of each hot slot
     uint32_t tkey;                            // the chunk's bound (order key)
     uint32_t tkey_rm;                         // the same for ceil(K / S) groups
     float vlo;                                // the least value that can be a candidate
-    alignas(16) uint32_t wnf[kW];             // per wave: a NaN or +inf seen
+    alignas(16) uint32_t wnf[kWMax];          // per wave: a NaN or +inf seen
     alignas(16) int hist[256];
     alignas(16) uint32_t mt[kMaxS]; // merge: each chunk's bound (order key)
     alignas(16) int mn[kMaxS];      // merge: list lengths
     alignas(16) int mf[kMaxS];      // merge: list flags
-    alignas(16) int scnt[kMaxS];    // merge: keys of each list that can place
-    int ncand, lost, onf;
+    int ncand, nsurv, lost, onf;
     uint32_t ticket;
     uint32_t draw[2];               // the merger's draw words
     int flags;
@@ -125,13 +123,13 @@ struct Smem {
 #define WTR(i)                                                                          \
     do {                                                                                \
         if ((threadIdx.x & 63) == 0 && a.trace)                                         \
-            a.trace[(blockIdx.x * kW + (threadIdx.x >> 6)) * 16 + (i)] =                \
+            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 16 + (i)] =                \
                 __builtin_amdgcn_s_memrealtime();                                       \
     } while (0)
 #define WTV(i, val)                                                                     \
     do {                                                                                \
         if ((threadIdx.x & 63) == 0 && a.trace)                                         \
-            a.trace[(blockIdx.x * kW + (threadIdx.x >> 6)) * 16 + (i)] = (uint64_t)(val); \
+            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 16 + (i)] = (uint64_t)(val); \
     } while (0)
 #else
 #define WTR(i) ((void)0)
@@ -222,22 +220,22 @@ __device__ __forceinline__ void pick_digit(const int* hist, int remaining, int* 
 }
 
 // Every thread of the workgroup: the keys keys[0..n) (distinct, 16-byte
-// aligned, followed by kPad zero words) whose rank (the number of larger
-// keys) is below K land at out[rank].  P neighbouring lanes share a key,
+// aligned, readable up to n + 32) whose rank (the number of larger keys)
+// is below K land at out[rank].  P neighbouring lanes share a key,
 // each counting the larger keys in its share of the list, and their counts
-// are summed across the P lanes (DPP): P = kT / n rounded down to a power of
+// are summed across the P lanes (DPP): P = NT / n rounded down to a power of
 // two (at most 16), so a short list is ranked in a few steps by every wave
 // instead of n steps by a few.
+template <int NT>
 __device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, uint64_t* out,
                                            uint64_t* gout = nullptr) {
     const int t = threadIdx.x;
     int P = 16;
-    while (P > 1 && P * n > kT) P >>= 1;
-    // lane `part` of a key's P counts the keys [part * L, part * L + L), L
-    // even, in 16-byte reads; P * L <= n + 3P <= n + kPad, and the keys are
-    // zero (below every key) from n on.
+    while (P > 1 && P * n > NT) P >>= 1;
+    // lane `part` of a key's P counts the keys [part * L, part * L + L) below
+    // n, L even, in 16-byte reads (P * L <= n + 2P)
     const int L = ((n + P - 1) / P + 1) & ~1;
-    const int per_pass = kT / P;
+    const int per_pass = NT / P;
     for (int base = 0; base < n; base += per_pass) {
         const int i = base + t / P, part = t & (P - 1);
         const uint64_t k = i < n ? keys[i] : ~0ull;
@@ -246,7 +244,8 @@ __device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, u
 #pragma unroll 2
         for (int q = 0; q < (L >> 1); ++q) {
             const ulonglong2 y = c2[q];
-            cnt += (y.x > k ? 1 : 0) + (y.y > k ? 1 : 0);
+            const int j = part * L + 2 * q;
+            cnt += (j < n && y.x > k ? 1 : 0) + (j + 1 < n && y.y > k ? 1 : 0);
         }
         cnt = group_sum(cnt, P);
         if (part == 0 && i < n && cnt < K) {
@@ -264,7 +263,7 @@ __device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, u
 // (the chunk holds more than kCap >= K finite entries).  Reading the chunk
 // again, rather than from the registers of the stream, keeps the kernel's
 // registers at what two workgroups per CU allow.
-template <typename T>
+template <typename T, int NT>
 __device__ __forceinline__ int radix_chunk(const T* base, const uint32_t* mrow, int e0, int e1, int K,
                                         float temp, bool divide, bool win, bool owner, float own_v,
                                         uint32_t own_id, Smem& sm) {
@@ -286,7 +285,7 @@ __device__ __forceinline__ int radix_chunk(const T* base, const uint32_t* mrow, 
     for (int shift = 56; shift >= 0; shift -= 8) {
         if (t < 256) sm.hist[t] = 0;
         lds_sync();
-        for (int id = e0 + t; id < e1; id += kT) {
+        for (int id = e0 + t; id < e1; id += NT) {
             uint64_t k;
             if (key_at(id, k) && (k & pmask) == prefix) atomicAdd(&sm.hist[(k >> shift) & 0xFF], 1);
         }
@@ -302,7 +301,7 @@ __device__ __forceinline__ int radix_chunk(const T* base, const uint32_t* mrow, 
     // prefix is the K-th largest key (keys are distinct): the K keys >= it
     if (t == 0) sm.ncand = 0;
     lds_sync();
-    for (int id = e0 + t; id < e1; id += kT) {
+    for (int id = e0 + t; id < e1; id += NT) {
         uint64_t k;
         if (key_at(id, k) && k >= prefix) {
             const int p = atomicAdd(&sm.ncand, 1);
@@ -354,13 +353,17 @@ __device__ void window_out(uint4& q, uint32_t wb, int off, Smem& sm) {
     q = fold_bits<T>(q, ~wb & ((1u << VEC) - 1u));
 }
 
-template <typename T, bool FAST, int kSlots>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : 4, 8)))
-void topk_wide_kernel(KArgs a) {
+// NT threads of kSlots 16-byte slots each: (1024, 4) two workgroups per
+// CU; (1024, 8), fp32, one workgroup per CU.
+template <typename T, bool FAST, int kSlots, int NT>
+__global__ __launch_bounds__(NT)
+__attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wide_kernel(KArgs a) {
+    constexpr int kT = NT, kW = NT / 64;
+    static_assert(kW * kSlots <= kWaveSlots, "hot-lane staging");
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NV = kSlots * VEC;         // stream values per thread
     constexpr int kChunkIds = kT * NV;       // ids a chunk can hold
-    static_assert(kChunkIds / 32 <= kT, "window bitmap");
+    static_assert(kChunkIds / 32 <= 1024, "window bitmap");
     __shared__ Smem sm;
     const float NEG_INF = -__builtin_huge_valf();
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -451,6 +454,7 @@ void topk_wide_kernel(KArgs a) {
         sm.lost = 0;
         sm.onf = 0;
         sm.ncand = 0;
+        sm.nsurv = 0;
     }
     lds_sync();
     const bool in_chunk = pn.on && t >= from && t < nrec && wid_raw >= e0 && wid_raw < e1;
@@ -535,19 +539,20 @@ void topk_wide_kernel(KArgs a) {
     for (int j = 0; j < kSlots; ++j)
         asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
 
-    // ---- bound: the maxima of the 128 groups of 8 lanes (DPP, on order
-    //      keys), then the K-th largest of those (wave 0, a bisection with
-    //      ballot counts).  K groups, each with a distinct entry at or above
+    // ---- bound: the maxima of the 128 groups of G = NT / 128 lanes (DPP,
+    //      on order keys), then the K-th largest of those (wave 0, a
+    //      bisection with ballot counts).  K groups, each with a distinct entry at or above
     //      it, bound the chunk's K-th value from below.  Per wave this costs
     //      a few instructions: at two workgroups per CU every instruction all
     //      waves execute costs about 13 ns.
     const uint32_t mkey = nf ? 0u : okey(m);
     {
+        constexpr int G = kT / 128;
         uint32_t g = mkey;
-        g = max(g, dpp_u32<0x111, 0xF, true>(0u, g));   // row_shr:1
-        g = max(g, dpp_u32<0x112, 0xF, true>(0u, g));   // row_shr:2
-        g = max(g, dpp_u32<0x114, 0xF, true>(0u, g));   // row_shr:4
-        if ((lane & 7) == 7) sm.gmax[wv * 8 + (lane >> 3)] = g;   // lane 8q + 7: lanes 8q .. 8q + 7
+        if constexpr (G >= 2) g = max(g, dpp_u32<0x111, 0xF, true>(0u, g));   // row_shr:1
+        if constexpr (G >= 4) g = max(g, dpp_u32<0x112, 0xF, true>(0u, g));   // row_shr:2
+        if constexpr (G >= 8) g = max(g, dpp_u32<0x114, 0xF, true>(0u, g));   // row_shr:4
+        if ((lane & (G - 1)) == G - 1) sm.gmax[wv * (64 / G) + lane / G] = g;   // lanes Gq .. Gq + G - 1
     }
     const uint64_t nfw = __ballot(nf);
     if (lane == 0) sm.wnf[wv] = nfw ? 1 : 0;
@@ -685,6 +690,7 @@ void topk_wide_kernel(KArgs a) {
             if (ng) wave_lds_sync();   // the next round writes over these slots
         }
     }
+    WTR(6);
     if (t == 0) sm.ticket = ticket;
     lds_sync();
     int ncand = select ? sm.ncand : 0;
@@ -694,7 +700,7 @@ void topk_wide_kernel(KArgs a) {
     const bool radixed = ncand > kCap;
     if (radixed) {
         // ---- exact radix select (every wave): the chunk's K keys
-        ncand = radix_chunk<T>(base, mrow, e0, e1, K, temp, divide, pn.on, owner, own_v,
+        ncand = radix_chunk<T, kT>(base, mrow, e0, e1, K, temp, divide, pn.on, owner, own_v,
                                (uint32_t)wid_raw, sm);
     }
     WTV(15, ncand);
@@ -725,9 +731,8 @@ void topk_wide_kernel(KArgs a) {
     }
     WTR(10);
     if (ranked) {
-        if (t < kPad) sm.u.c.cand[ncand + t] = 0ull;   // rank_place reads past the keys
         lds_sync();
-        rank_place(sm.u.c.cand, ncand, K, sm.slist, merger ? nullptr : my + 1);
+        rank_place<kT>(sm.u.c.cand, ncand, K, sm.slist, merger ? nullptr : my + 1);
     }
     WTR(11);
     if (!merger) {
@@ -794,7 +799,6 @@ void topk_wide_kernel(KArgs a) {
     WSTOP(3, (float)(key0 + key1));
 
     // ================= merge (the last chunk of the row)
-    WTR(6);
     WSTOP(4, (float)nlist);
     if (t == 0 && S > 1) st_agent(&a.counters[row * kCounterStride], 0u);
     if (wv < S && lane == 0) sm.mn[wv] = ncc;
@@ -861,25 +865,24 @@ void topk_wide_kernel(KArgs a) {
         }
         const bool s0 = wv < S && lane < ncc && key0 >= tg;
         const bool s1 = wv < S && lane + 64 < ncc && key1 >= tg;
+        // in any order (the rank counts): one LDS atomic per list wave
         const uint64_t b0 = __ballot(s0), b1 = __ballot(s1);
-        if (wv < S && lane == 0) sm.scnt[wv] = __popcll(b0) + __popcll(b1);
+        if (wv < S && (b0 | b1)) {
+            int off = 0;
+            if (lane == 0) off = atomicAdd(&sm.nsurv, __popcll(b0) + __popcll(b1));
+            off = __builtin_amdgcn_readfirstlane(off);
+            const int r0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
+            const int r1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
+            if (s0) sm.u.surv[off + r0] = key0;
+            if (s1) sm.u.surv[off + __popcll(b0) + r1] = key1;
+        }
         WSTOP(51, (float)(b0 + b1));
         lds_sync();
-        // this wave's offset and the total, from lane l's count of list l
-        const int q = lane < S ? sm.scnt[lane] : 0;
-        const int qi = wave_incl_scan_i32(q);
-        const int nsurv = __builtin_amdgcn_readlane(qi, 63);
-        const int off = wv < S ? __builtin_amdgcn_readlane(qi - q, wv) : 0;
-        const int r0 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b0, 0u));
-        const int r1 = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b1, 0u));
-        if (s0) sm.u.surv[off + r0] = key0;
-        if (s1) sm.u.surv[off + __popcll(b0) + r1] = key1;
-        if (t < kPad) sm.u.surv[nsurv + t] = 0ull;
-        lds_sync();
+        const int nsurv = sm.nsurv;
         WTR(13);
         WTV(14, nsurv);
         WSTOP(52, (float)nsurv);
-        rank_place(sm.u.surv, nsurv, K, sm.srt);
+        rank_place<kT>(sm.u.surv, nsurv, K, sm.srt);
     }
     lds_sync();
     WTR(8);
@@ -949,23 +952,24 @@ void topk_wide_kernel(KArgs a) {
 // k.S <= kWideMaxChunksHost chunks of k.CE ids (a multiple of 32, at most
 // 4096 * the vector width).
 int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream) {
-    const dim3 grid((unsigned)(batch * k.S)), block(tms::wide::kT);
-#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::wide::topk_wide_kernel<T, F, 4>), grid, block, 0, stream, k)
+    const dim3 grid((unsigned)(batch * k.S));
+#define TMS_LAUNCH(T, F, SL, NT) \
+    hipLaunchKernelGGL((tms::wide::topk_wide_kernel<T, F, SL, NT>), grid, dim3(NT), 0, stream, k)
     switch (dtype) {
         case TMS_DTYPE_F32:
             if (slots == 8) {
-                if (fast) hipLaunchKernelGGL((tms::wide::topk_wide_kernel<float, true, 8>), grid, block, 0, stream, k);
-                else hipLaunchKernelGGL((tms::wide::topk_wide_kernel<float, false, 8>), grid, block, 0, stream, k);
-            } else if (fast) TMS_LAUNCH(float, true);
-            else TMS_LAUNCH(float, false);
+                if (fast) TMS_LAUNCH(float, true, 8, 1024);
+                else TMS_LAUNCH(float, false, 8, 1024);
+            } else if (fast) TMS_LAUNCH(float, true, 4, 1024);
+            else TMS_LAUNCH(float, false, 4, 1024);
             break;
         case TMS_DTYPE_F16:
-            if (fast) TMS_LAUNCH(_Float16, true);
-            else TMS_LAUNCH(_Float16, false);
+            if (fast) TMS_LAUNCH(_Float16, true, 4, 1024);
+            else TMS_LAUNCH(_Float16, false, 4, 1024);
             break;
         default:
-            if (fast) TMS_LAUNCH(tms::Bf16, true);
-            else TMS_LAUNCH(tms::Bf16, false);
+            if (fast) TMS_LAUNCH(tms::Bf16, true, 4, 1024);
+            else TMS_LAUNCH(tms::Bf16, false, 4, 1024);
             break;
     }
 #undef TMS_LAUNCH
