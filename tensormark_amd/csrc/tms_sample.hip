@@ -44,6 +44,100 @@
 
 namespace tms {
 
+// Ranks of the n distinct keys keys[0..n) (n <= kUni, any order; the
+// whole workgroup): every key whose rank r (the number of larger keys) is
+// below nkeep lands at out[r].  Each key goes to one of kBuckets buckets by
+// a monotone function of its quotient (fl((q - qmin) * scale), truncated),
+// so every key of a higher bucket is larger; counts per bucket (LDS
+// atomics), a descending scan for each bucket's start, the keys scattered
+// to their buckets in place, and each key ranked within its own bucket
+// only.  A few barriers and a handful of reads a key, where binary searches
+// over sorted lists cost dependent reads at conflicting addresses.  keys is
+// reordered; cnt holds kBuckets ints of scratch.  Correct for any keys;
+// massive ties (one bucket holding most keys) only cost time.
+constexpr int kBuckets = 2 * kBlock;
+template <typename SM>
+__device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int* cnt, SM& sm) {
+    constexpr int kPer = kUni / kBlock;   // keys per thread
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+#pragma unroll
+    for (int u = 0; u < kBuckets / kBlock; ++u) cnt[t * (kBuckets / kBlock) + u] = 0;
+    uint64_t k[kPer];
+    float qhi = -__builtin_huge_valf(), qlo_neg = -__builtin_huge_valf();
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = t + u * kBlock;
+        k[u] = i < n ? keys[i] : 0ull;
+        if (i < n) {
+            const float q = ckey_val(k[u]);
+            qhi = fmaxf(qhi, q);
+            qlo_neg = fmaxf(qlo_neg, -q);
+        }
+    }
+    qhi = wave_max_f32_dpp(qhi);
+    qlo_neg = wave_max_f32_dpp(qlo_neg);
+    if (lane == 0) {
+        sm.wave_f[wv] = qhi;
+        sm.wave_k[wv] = __float_as_uint(qlo_neg);
+    }
+    lds_sync();
+    float qmax = sm.wave_f[0], qmin_neg = __uint_as_float((uint32_t)sm.wave_k[0]);
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) {
+        qmax = fmaxf(qmax, sm.wave_f[i]);
+        qmin_neg = fmaxf(qmin_neg, __uint_as_float((uint32_t)sm.wave_k[i]));
+    }
+    const float qmin = -qmin_neg;
+    const float span = qmax - qmin;
+    // a span that is 0, or not finite, puts every key in bucket 0
+    const float scale = (span > 0.0f && span <= FLT_MAX) ? (float)(kBuckets - 1) / span : 0.0f;
+    int b[kPer], slot[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = t + u * kBlock;
+        b[u] = 0;
+        slot[u] = 0;
+        if (i < n) {
+            const float f = (ckey_val(k[u]) - qmin) * scale;   // NaN (inf * 0) and below 0 -> bucket 0
+            b[u] = f >= (float)(kBuckets - 1) ? kBuckets - 1 : (f >= 1.0f ? (int)f : 0);
+            slot[u] = atomicAdd(&cnt[b[u]], 1);
+        }
+    }
+    lds_sync();
+    // descending exclusive scan: start[b] = keys in buckets above b
+    {
+        constexpr int kB = kBuckets / kBlock;   // buckets per thread
+        int cb[kB], loc = 0;
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            cb[u] = cnt[kBuckets - 1 - (t * kB + u)];
+            loc += cb[u];
+        }
+        int tot;
+        int st = block_excl_scan(loc, tot, sm);
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            cnt[kBuckets - 1 - (t * kB + u)] = st;
+            st += cb[u];
+        }
+    }
+    lds_sync();
+    // every key was read into registers above: scatter in place
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+        if (t + u * kBlock < n) keys[cnt[b[u]] + slot[u]] = k[u];
+    lds_sync();
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        if (t + u * kBlock < n) {
+            const int lo = cnt[b[u]], hi = b[u] > 0 ? cnt[b[u] - 1] : n;
+            int r = lo;
+            for (int j = lo; j < hi; ++j) r += keys[j] > k[u] ? 1 : 0;
+            if (r < nkeep) out[r] = k[u];
+        }
+    }
+}
+
 template <typename T, bool FAST>
 __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     constexpr int VEC = Elt<T>::kVec;
@@ -552,7 +646,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         }
         if (!anynf && !bad_params && (fallback || n > kCand)) {
             if (mode == MODE_TOPK) {
-                nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn, sm);
+                nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn.on, pn.rep_on, pn.fp_on, pn.rep,
+                                     pn.freq, pn.pres, pn.ov, sm);
                 sort_cand(nout, sm);
             } else {
                 flags |= FLAG_OVERFLOW;
@@ -834,9 +929,15 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             lds_sync();
             const int ng = sm.misc[6];
             const int total = sm.hist[ng];
-            for (int i = t; i < total; i += kBlock) {
+            // The list of staged entry i: the last g >= 1 whose start is at
+            // or below i (independent reads, not a dependent walk).
+            auto list_of = [&](int i) {
                 int lc = 0;
-                while (sm.hist[lc + 1] <= i) ++lc;
+                for (int g = 1; g < ng; ++g) lc += sm.hist[g] <= i ? 1 : 0;
+                return lc;
+            };
+            for (int i = t; i < total; i += kBlock) {
+                const int lc = list_of(i);
                 const int src = sm.list_src[lc];
                 const int jj = i - sm.hist[lc];
                 uni[i] = src < 0 ? srt[i]
@@ -845,17 +946,9 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             }
             lds_sync();
             const int nkeep = total < keep_cap ? total : keep_cap;
-            for (int i = t; i < total; i += kBlock) {
-                int lc = 0;
-                while (sm.hist[lc + 1] <= i) ++lc;
-                const uint64_t k = uni[i];
-                int rank = i - sm.hist[lc];
-                for (int o = 0; o < ng; ++o) {
-                    if (o == lc) continue;
-                    rank += count_greater(uni + sm.hist[o], sm.hist[o + 1] - sm.hist[o], k);
-                }
-                if (rank < nkeep) srt[rank] = k;
-            }
+            // The staged lists' keys ranked together (the bucket counts go
+            // to pbits, dead since the chunk phase).
+            bucket_rank(uni, total, nkeep, srt, (int*)sm.pbits, sm);
             c_next = sm.misc[7];
             n_acc = nkeep;
             lds_sync();

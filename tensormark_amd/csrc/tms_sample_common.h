@@ -235,12 +235,23 @@ __device__ float slow_value(const T* base, const uint32_t* mrow, int id, int e0,
 // where the threshold admits too many: a radix select over the keys of
 // v / T (8 bits per pass) with the chunk re-read from memory, then the
 // strictly greater entries and the lowest-id ties.  Writes sm.cand, unsorted;
-// returns the count (<= K).  `pn` is taken by value: a reference would put the
-// caller's Pen in scratch memory, and a kernel with any scratch launched its
-// workgroups measurably slower (B = 1024, V = 256000: 256 -> 244 us).
+// returns the count (<= K).  The penalties come as scalars: a Pen argument
+// (by reference, or by value once it holds a pointer) put the caller's Pen in
+// scratch memory, and a kernel with any scratch launched its workgroups
+// measurably slower (B = 1024, V = 256000: 256 -> 244 us).
 template <typename T, typename SM>
 __device__ __noinline__ int radix_slow(const T* base, const uint32_t* mrow, int e0, int e1, int K,
-                                       float temp, bool divide, Pen pn, SM& sm) {
+                                       float temp, bool divide, bool pen_on, bool pen_rep_on, bool pen_fp_on,
+                                       float pen_rep, float pen_freq, float pen_pres, const float* pen_ov,
+                                       SM& sm) {
+    Pen pn;
+    pn.on = pen_on;
+    pn.rep_on = pen_rep_on;
+    pn.fp_on = pen_fp_on;
+    pn.rep = pen_rep;
+    pn.freq = pen_freq;
+    pn.pres = pen_pres;
+    pn.ov = pen_ov;
     const int t = threadIdx.x;
     const float NEG_INF = -__builtin_huge_valf();
     uint32_t prefix = 0, pmask = 0;
