@@ -56,9 +56,8 @@ namespace tms {
 // reordered; cnt holds kBuckets ints of scratch.  Correct for any keys;
 // massive ties (one bucket holding most keys) only cost time.
 constexpr int kBuckets = 2 * kBlock;
-template <typename SM>
+template <int kPer, typename SM>   // keys per thread: n <= kPer * kBlock
 __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int* cnt, SM& sm) {
-    constexpr int kPer = kUni / kBlock;   // keys per thread
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
 #pragma unroll
     for (int u = 0; u < kBuckets / kBlock; ++u) cnt[t * (kBuckets / kBlock) + u] = 0;
@@ -136,6 +135,158 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
             if (r < nkeep) out[r] = k[u];
         }
     }
+}
+
+// The top-p tail from block prefix sums (every thread of the workgroup),
+// for n <= kToppCap entries pr[0..n) in LDS (srt, K, P as in tail_topp).
+// Thread t holds the entries [t * per, t * per + per), per =
+// ceil(n / kBlock) rounded up to odd (<= 5: an odd stride keeps the
+// threads' 8-byte reads on distinct banks), and a prefix is its sequential
+// partial sum within the thread, plus the exclusive scan of the thread
+// totals within its wave, plus the totals of the waves before it (added in
+// order).  Against the reference's sequential sums of the quotients
+// pr_j / D (tmsample.h:186-199): a prefix takes at most 15 roundings (4 in
+// the thread, 6 in the scan, 3 across the waves, 2 to combine), the scaling
+// two (a prefix times the rounded reciprocal of the divisor), our divisor
+// (a prefix) 15 and the reference's n - 1, its quotients and additions
+// 2n + 1, so the two differ by at most (3n + 32) * 2^-53 relative
+// (3104 * 2^-53 at n = 1024) plus subnormal units, inside the margin
+// kRelP = 4160 * 2^-53.  A cut or draw decided within the margin of its
+// threshold, and any call that returns per-entry probabilities, takes the
+// sequential tail_topp.  The min-p cut compares the same pr values, so it is
+// exact here.  The decisions (first index at or above a threshold,
+// definitely or within the margin) meet in LDS: four barriers in place of
+// one wave's serial chains.  Returns 0 when the row is written, 1 when the
+// answer needs the order past the held entries (the whole-row path), 2 when
+// only tail_topp can decide.  Every thread gets the same value.
+template <typename SM>
+__device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt, int n,
+                               int K, const double* pr, SM& sm) {
+    static_assert(kToppCap <= kBlock * 4, "thread blocks of at most 5 entries");
+    if (a.topk_cap && a.out_topk_probs) return 2;
+    if (n < K && a.topk_cap > n && a.out_topk_ids) return 1;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int per = ((n + kBlock - 1) / kBlock) | 1;
+    const int b0 = t * per;
+    double c[5];
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const int i = b0 + j;
+        acc += (j < per && i < n) ? pr[i] : 0.0;   // adding 0 is exact
+        c[j] = acc;
+    }
+    const double incl = wave_incl_scan_f64(acc);
+    double excl = __builtin_bit_cast(double, __shfl_up((unsigned long long)__builtin_bit_cast(uint64_t, incl), 1, 64));
+    if (lane == 0) excl = 0.0;
+    double* wt = (double*)sm.wave_k;   // the waves' totals
+    if (lane == 63) wt[wv] = incl;
+    lds_sync();
+    double base = 0.0, z = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const double v = wt[w];
+        if (w < wv) base += v;
+        z += v;
+    }
+#pragma unroll
+    for (int j = 0; j < 5; ++j) c[j] = base + (excl + c[j]);
+    constexpr double kRelP = (4.0 * kToppCap + 64.0) * 0x1p-53;
+    constexpr double kAbs = 1e-300;
+    constexpr int kNone = 1 << 30;
+    // this thread's first index i < lim whose prefix / D is >= thr,
+    // definitely (fd) or within the margin (fm)
+    auto first_ge = [&](double D, double thr, int lim) {
+        int fd = kNone, fm = kNone;
+        const double rD = 1.0 / D;
+#pragma unroll
+        for (int j = 4; j >= 0; --j) {
+            const int i = b0 + j;
+            if (j < per && i < lim) {
+                const double v = c[j] * rD;
+                const double m = (v + fabs(thr)) * kRelP + kAbs;
+                if (v > thr + m) fd = i;
+                else if (!(v < thr - m)) fm = i;
+            }
+        }
+        return make_int2(wave_min_nonneg(fd), wave_min_nonneg(fm));
+    };
+    // the block minima of up to three per-wave values, in slots of hist
+    auto block_min3 = [&](int s0, int3 v) {
+        if (lane == 0) {
+            sm.hist[s0 + wv] = v.x;
+            sm.hist[s0 + kWaves + wv] = v.y;
+            sm.hist[s0 + 2 * kWaves + wv] = v.z;
+        }
+        lds_sync();
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            v.x = min(v.x, sm.hist[s0 + w]);
+            v.y = min(v.y, sm.hist[s0 + kWaves + w]);
+            v.z = min(v.z, sm.hist[s0 + 2 * kWaves + w]);
+        }
+        return v;
+    };
+    const int2 f1 = first_ge(z, (double)P.top_p, n);
+    int fl = kNone;   // first index >= 1 with pr < min_p
+    const bool minp = P.min_p > 0.0f;
+    if (minp) {
+        const double mp = (double)P.min_p;
+#pragma unroll
+        for (int j = 4; j >= 0; --j) {
+            const int i = b0 + j;
+            if (j < per && i >= 1 && i < n && pr[i] < mp) fl = i;
+        }
+        fl = wave_min_nonneg(fl);
+    }
+    const int3 m1 = block_min3(0, make_int3(f1.x, f1.y, fl));
+    const int fd = m1.x, fm = m1.y;
+    fl = m1.z;
+    bool ok = fm > fd || (fm == kNone && fd == kNone);
+    int kp = fd < n ? fd + 1 : K;
+    if (ok && minp) {
+        if (fl >= n && n < kp && !((double)P.min_p > 4.3e-18)) return 1;   // as in tail_topp
+        const int m = min(fl, min(kp, n));
+        if (m < kp) kp = m;
+    }
+    const int keep = kp;
+    const int lim = keep < n ? keep : n;
+    int tokidx = 0;
+    if (ok && keep >= 2) {
+        // sum = the prefix at lim - 1, from the thread that holds it
+        const int e = lim - 1, le = e / per, je = e - le * per;
+        if (t == le) {
+            double mine = 0.0;
+#pragma unroll
+            for (int j = 0; j < 5; ++j) mine = j == je ? c[j] : mine;
+            sm.theta = __builtin_bit_cast(uint64_t, mine);   // free since the merge
+        }
+        uint32_t w0, w1;
+        row_uniform(a, row, P, w0, w1);
+        const double u = canonical(w0, w1);
+        lds_sync();
+        const double sum = __builtin_bit_cast(double, sm.theta);
+        // cp at keep - 1 is 1.0 exactly (> u): only indices before it are
+        // decided from the prefixes
+        const int dl = min(lim, keep - 1);
+        const int2 f2 = first_ge(sum, u, dl);
+        const int3 m2 = block_min3(3 * kWaves, make_int3(f2.x, f2.y, kNone));
+        const int gd = m2.x, gm = m2.y;
+        ok = gm > gd || (gm == kNone && gd == kNone);
+        tokidx = gd < dl ? gd : keep - 1;
+    }
+    if (!ok) return 2;
+    // tokidx >= n: the draw fell past the last entry that moves the sums
+    if (tokidx >= n) return 1;
+    if (t == 0) {
+        a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
+        a.out_status[row] = TMS_ROW_OK;
+        if (a.out_keep) a.out_keep[row] = keep;
+    }
+    if (a.topk_cap && a.out_topk_ids)
+        for (int i = t; i < a.topk_cap; i += kBlock)
+            a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i < n ? (int)ckey_id(srt[i]) : -1;
+    return 0;
 }
 
 template <typename T, bool FAST>
@@ -945,20 +1096,24 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                                      : ld_agent(&row_lists[(int64_t)src * kListStride + 1 + jj]));
             }
             lds_sync();
+            TMS_TR(11);
             const int nkeep = total < keep_cap ? total : keep_cap;
             // The staged lists' keys ranked together (the bucket counts go
             // to pbits, dead since the chunk phase).
-            bucket_rank(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+            if (total <= 2 * kBlock) bucket_rank<2>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+            else bucket_rank<kUni / kBlock>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+            TMS_TR(12);
             c_next = sm.misc[7];
             n_acc = nkeep;
             lds_sync();
         }
     }
     // Every word the other chunks wrote this call (headers, entries) goes
-    // back to zero for the next call; on a top-k row's success path waves
-    // 1-3 do it while wave 0 runs the tail.
+    // back to zero for the next call; on a top-k or top-p row's success path
+    // waves 1-3 do it while wave 0 runs the tail.
     TMS_TR(9);
-    const bool defer_zero = status == TMS_ROW_OK && mode == MODE_TOPK && !sm.misc[3];
+    const bool defer_zero = status == TMS_ROW_OK && (mode == MODE_TOPK || (mode == MODE_TOPP && !go_dense)) &&
+                            !sm.misc[3];
     if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
     TMS_TR(10);
     if (status != TMS_ROW_OK) {
@@ -1018,28 +1173,40 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         return;
     }
     // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
+    // The count of that prefix and every held entry's pr in one pass (pr
+    // past the prefix is never read).
+    double* pr = (double*)sm.big.m.uni;               // staging no longer needed
+    double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
     {
         int sig = 0;
-        for (int i = t; i < n; i += kBlock)
-            sig += ((double)ckey_val(srt[i]) - (double)mx >= -(double)kSigSpan) ? 1 : 0;
+        for (int i = t; i < n; i += kBlock) {
+            const double d = (double)ckey_val(srt[i]) - (double)mx;
+            sig += d >= -(double)kSigSpan ? 1 : 0;
+            pr[i] = exp(d);
+        }
         sig = wave_sum_dpp(sig);
         if (lane == 0) sm.wave_i[wv] = sig;
+        if (t == 0) sm.nvalid = 0;
         lds_sync();
         n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
         n = min(n, K);   // tmsample::sample sums over the top K only (tmsample.h:185-191)
-        lds_sync();
     }
-    double* pr = (double*)sm.big.m.uni;               // staging no longer needed
-    double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
-    for (int i = t; i < n; i += kBlock) pr[i] = exp((double)ckey_val(srt[i]) - (double)mx);
-    lds_sync();
-    if (t == 0) sm.nvalid = 0;
-    lds_sync();
-    if (wv == 0) {
-        const bool lost = tail_topp_fast(a, row, P, srt, n, K, pr, q);
-        if (lane == 0) sm.nvalid = lost;
-        TMS_TR(8);
+    TMS_TR(14);
+    const int tp = tail_topp_block(a, row, P, srt, n, K, pr, sm);
+    if (tp == 2) {
+        // the sequential tail decides (or returns the probabilities)
+        if (wv == 0) {
+            TMS_TV(16, 1);
+            const bool lost = tail_topp(a, row, P, srt, n, K, pr, q);
+            if (lane == 0) sm.nvalid = lost;
+        } else {
+            zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
+        }
+    } else {
+        if (t == 0) sm.nvalid = tp;
+        zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
     }
+    TMS_TR(8);
     lds_sync();
     // The answer needs the order past the held entries: the whole row.
     if (sm.nvalid) defer_dense(a, row);

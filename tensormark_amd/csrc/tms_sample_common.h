@@ -571,13 +571,14 @@ __device__ void tail_topk_exact(const KArgs& a, int row, const tms_row_params& P
 // Whether the reference's left-to-right prefix sums of quotients pr_j / D
 // decide "first index k < m whose prefix is >= thr" the same way as the
 // prefixes c (lane k in c0, lane k - 64 in c1) computed here as (tree
-// prefix sum of pr) / D', D' the tree's value of the divisor.  For n <= 128
-// non-negative terms: the tree prefixes carry at most 7 roundings per term
-// (a 6-step DPP scan plus one addition), the division one, the reference's
-// quotients and sequential additions 2n + 1, and the two divisors differ by
-// at most (n + 7) * 2^-53 relative, so the two differ by at most
-// (3n + 16) * 2^-53 relative (400 * 2^-53 at n = 128), plus a few subnormal
-// units; the margin below is 576 * 2^-53.  Returns false when some prefix up
+// prefix sum of pr) * fl(1 / D'), D' the tree's value of the divisor.  For
+// n <= 128 non-negative terms: the tree prefixes carry at most 7 roundings
+// per term (a 6-step DPP scan plus one addition), the scaling two (the
+// reciprocal and the product), the reference's quotients and sequential
+// additions 2n + 1, and the two divisors differ by at most (n + 7) * 2^-53
+// relative, so the two differ by at most (3n + 17) * 2^-53 relative
+// (401 * 2^-53 at n = 128), plus a few subnormal units; the margin below is
+// 576 * 2^-53.  Returns false when some prefix up
 // to the decision lies within the margin of thr (or thr is NaN): only the
 // sequential sums decide it.
 __device__ __forceinline__ bool decide_first_ge(double c0, double c1, double thr, int m, int& idx) {
@@ -619,7 +620,8 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
     const double z = readlane_f64(s1, 63);
     // cum = prefix of q = pr / z: from the prefixes of pr (decide_first_ge
     // bounds the difference from the reference's sums of quotients)
-    const double c0 = s0 / z, c1 = s1 / z;
+    const double rz = 1.0 / z;
+    const double c0 = s0 * rz, c1 = s1 * rz;
     int fi;
     bool ok = decide_first_ge(c0, c1, (double)P.top_p, n, fi);
     int kp = fi < n ? fi + 1 : K;
@@ -637,7 +639,8 @@ __device__ void tail_topk(const KArgs& a, int row, const tms_row_params& P, cons
         const int e = keep - 1;   // the sum runs over entries 0 .. keep - 1
         const double sum = e < 64 ? readlane_f64(s0, e) : readlane_f64(s1, e - 64);
         // cp = prefix of p = pr / sum, likewise from the prefixes of pr
-        ok = decide_first_ge(s0 / sum, s1 / sum, u, keep - 1, tokidx);
+        const double rs = 1.0 / sum;
+        ok = decide_first_ge(s0 * rs, s1 * rs, u, keep - 1, tokidx);
     }
     if (!ok) {
         TMS_TV(16, 1);
@@ -744,118 +747,6 @@ __device__ __forceinline__ int wave_min_nonneg(int v) {
     u = min(u, dpp_u32<0x142, 0xA, false>(kBig, u));
     u = min(u, dpp_u32<0x143, 0xC, false>(kBig, u));
     return __builtin_amdgcn_readlane((int)u, 63);
-}
-
-// The top-p tail from lane-block prefix sums, for n <= kToppCap entries
-// pr[0..n) in LDS (one wave; srt, K, P as in tail_topp).  Lane l holds the
-// entries [l * per, l * per + per), per = ceil(n / 64) <= 16, and a
-// prefix is its sequential partial sum within the lane plus the exclusive
-// scan of the lane totals.  Against the reference's sequential sums of the
-// quotients pr_j / D (tmsample.h:186-199): a prefix takes at most 22
-// roundings (15 in the lane, 6 in the scan, one addition), the division one,
-// our divisor (a prefix) 22 and the reference's n - 1, its quotients and
-// additions 2n + 1, so the two differ by at most (3n + 45) * 2^-53
-// relative (3117 * 2^-53 at n = 1024) plus subnormal units, inside the
-// margin kRelP = 4160 * 2^-53.  A cut or draw decided within the margin of
-// its threshold, and any call that returns per-entry probabilities, takes
-// the sequential tail_topp.  The min-p cut compares the same pr values, so
-// it is exact here.
-__device__ bool tail_topp_fast(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt,
-                               int n, int K, double* pr, double* q) {
-    static_assert(kToppCap <= 64 * 16, "lane blocks of at most 16 entries");
-    if (a.topk_cap && a.out_topk_probs) return tail_topp(a, row, P, srt, n, K, pr, q);
-    if (n < K && a.topk_cap > n && a.out_topk_ids) return true;
-    const int lane = threadIdx.x & 63;
-    const int per = (n + 63) >> 6;
-    const int b0 = lane * per;
-    double c[16];   // prefixes of this lane's entries (0 past n)
-    double acc = 0.0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int i = b0 + j;
-        acc += (j < per && i < n) ? pr[i] : 0.0;   // adding 0 is exact
-        c[j] = acc;
-    }
-    const double incl = wave_incl_scan_f64(acc);
-    double excl = __builtin_bit_cast(double, __shfl_up((unsigned long long)__builtin_bit_cast(uint64_t, incl), 1, 64));
-    if (lane == 0) excl = 0.0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) c[j] = excl + c[j];
-    const double z = readlane_f64(incl, 63);
-    constexpr double kRelP = (4.0 * kToppCap + 64.0) * 0x1p-53;
-    constexpr double kAbs = 1e-300;
-    constexpr int kNone = 1 << 30;
-    // First index i < lim whose prefix / D is >= thr: definitely (above the
-    // margin) or possibly (within it).  ok = false when a possible one comes
-    // no later than the first definite one.
-    auto first_ge = [&](double D, double thr, int lim, int& idx) {
-        int fd = kNone, fm = kNone;
-#pragma unroll
-        for (int j = 15; j >= 0; --j) {
-            const int i = b0 + j;
-            if (j < per && i < lim) {
-                const double v = c[j] / D;
-                const double m = (v + fabs(thr)) * kRelP + kAbs;
-                if (v > thr + m) fd = i;
-                else if (!(v < thr - m)) fm = i;
-            }
-        }
-        fd = wave_min_nonneg(fd);
-        fm = wave_min_nonneg(fm);
-        idx = fd;
-        return fm > fd || (fm == kNone && fd == kNone);
-    };
-    int fi;
-    bool ok = first_ge(z, (double)P.top_p, n, fi);
-    int kp = fi < n ? fi + 1 : K;
-    if (ok && P.min_p > 0.0f) {
-        const double mp = (double)P.min_p;
-        int fl = kNone;   // first index >= 1 with pr < mp
-#pragma unroll
-        for (int j = 15; j >= 0; --j) {
-            const int i = b0 + j;
-            if (j < per && i >= 1 && i < n && pr[i] < mp) fl = i;
-        }
-        fl = wave_min_nonneg(fl);
-        if (fl >= n && n < kp && !(mp > 4.3e-18)) return true;   // as in tail_topp
-        const int m = min(fl, min(kp, n));
-        if (m < kp) kp = m;
-    }
-    const int keep = kp;
-    const int lim = keep < n ? keep : n;
-    int tokidx = 0;
-    if (ok && keep >= 2) {
-        // sum = the prefix at lim - 1, from the lane that holds it
-        const int e = lim - 1, le = e / per, je = e - le * per;
-        double mine = 0.0;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) mine = j == je ? c[j] : mine;
-        const double sum = readlane_f64(mine, le);
-        uint32_t w0, w1;
-        row_uniform(a, row, P, w0, w1);
-        const double u = canonical(w0, w1);
-        // cp at keep - 1 is 1.0 exactly (> u): only indices before it are
-        // decided from the prefixes
-        const int dl = min(lim, keep - 1);
-        int fd;
-        ok = first_ge(sum, u, dl, fd);
-        tokidx = fd < dl ? fd : keep - 1;
-    }
-    if (!ok) {
-        TMS_TV(16, 1);
-        return tail_topp(a, row, P, srt, n, K, pr, q);
-    }
-    // tokidx >= n: the draw fell past the last entry that moves the sums
-    if (tokidx >= n) return true;
-    if (lane == 0) {
-        a.out_tokens[row] = (int)ckey_id(srt[tokidx]);
-        a.out_status[row] = TMS_ROW_OK;
-        if (a.out_keep) a.out_keep[row] = keep;
-    }
-    if (a.topk_cap && a.out_topk_ids)
-        for (int i = lane; i < a.topk_cap; i += 64)
-            a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i < n ? (int)ckey_id(srt[i]) : -1;
-    return false;
 }
 
 }  // namespace tms
