@@ -1193,6 +1193,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     }
     TMS_TR(14);
     const int tp = tail_topp_block(a, row, P, srt, n, K, pr, sm);
+    TMS_TR(15);
     if (tp == 2) {
         // the sequential tail decides (or returns the probabilities)
         if (wv == 0) {

@@ -432,13 +432,16 @@ __device__ __forceinline__ int count_gt_fixed(const uint64_t* L, int n, uint64_t
 // >= 0), so the top-p cut and the drawn index are counts of partial sums
 // below the threshold.
 // Zero the published lists of a row (header, entries and padding up to r of
-// every chunk), threads tid0 .. nthr-1 of the workgroup.
+// every chunk), threads tid0 .. nthr-1 of the workgroup: one index space of
+// S lists x W words (W the longest list's words), so the lengths are
+// independent reads rather than one list after another.
 __device__ __forceinline__ void zero_lists(uint64_t* row_lists, int S, int r, const int* list_n,
                                            int tid0, int nthr) {
-    for (int cc = 0; cc < S; ++cc) {
-        const int nw = 1 + max(list_n[cc], r);
-        for (int jj = tid0; jj < nw; jj += nthr)
-            st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
+    int W = 1 + r;
+    for (int cc = 0; cc < S; ++cc) W = max(W, 1 + list_n[cc]);
+    for (int idx = tid0; idx < S * W; idx += nthr) {
+        const int cc = idx / W, jj = idx - cc * W;
+        if (jj < 1 + max(list_n[cc], r)) st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
     }
 }
 
