@@ -163,8 +163,10 @@ def test_cfg3_full_size_fp16_vs_oracle(sampler, orc, cap):
 @pytest.mark.parametrize("n_allowed", [70, 700, 1000])
 def test_topp_rows_many_entries(sampler, orc, n_allowed):
     """Top-p rows (top_k = 0) holding up to 1000 entries within 40 of the
-    maximum, spread over the row's chunks: lane blocks of up to 16 entries in the prefix-sum tail, with
-    top-p, min-p and temperature varied per row and no per-entry outputs."""
+    maximum, spread over the row's chunks: the whole-list merge ranks them by
+    value buckets (2 or 8 keys a thread), and the tail sums thread blocks of
+    up to 5 entries; top-p, min-p and temperature varied per row, no
+    per-entry outputs."""
     rng = np.random.default_rng(n_allowed)
     B, V = 64, 60000   # 4 chunks: a chunk holds at most 512 candidates
     x = rng.normal(0.0, 1.5, (B, V)).astype(np.float32)
@@ -176,6 +178,28 @@ def test_topp_rows_many_entries(sampler, orc, n_allowed):
     p["top_p"] = rng.choice([0.3, 0.8, 0.95, 0.999, 1.0], size=B)
     p["min_p"] = rng.choice([0.0, 0.0, 0.01, 0.2], size=B)
     p["temperature"] = rng.choice([0.6, 1.0, 1.7], size=B)
+    want = orc.sample_batch(x, p, mask=mask)
+    g = run_gpu(sampler, x, p, mask=mask)
+    check(g, want)
+
+
+@pytest.mark.parametrize("grid", [0.5, 0.0])
+def test_topp_rows_bucket_ties(sampler, orc, grid):
+    """Top-p rows whose values sit on a coarse grid (many exact ties, so many
+    keys share a bucket and rank by lowest id within it), and rows where
+    every allowed value is equal (grid 0: one bucket holds every key)."""
+    rng = np.random.default_rng(31)
+    B, V = 24, 40000
+    x = rng.normal(0.0, 1.5, (B, V)).astype(np.float32)
+    x = np.round(x / grid) * grid if grid else np.full((B, V), 0.25, np.float32)
+    x = x.astype(np.float32)
+    bits = np.zeros((B, ((V + 31) // 32) * 32), bool)
+    for b in range(B):
+        bits[b, rng.choice(V, size=int(rng.integers(200, 900)), replace=False)] = True
+    mask = workloads.pack_bits(bits)
+    p = params_array(B, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(B) + 11)
+    p["top_p"] = rng.choice([0.5, 0.9, 1.0], size=B)
+    p["temperature"] = rng.choice([0.7, 1.0], size=B)
     want = orc.sample_batch(x, p, mask=mask)
     g = run_gpu(sampler, x, p, mask=mask)
     check(g, want)
