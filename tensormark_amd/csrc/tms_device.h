@@ -245,6 +245,32 @@ __device__ __forceinline__ double wave_incl_scan_f64(double v) {
     return v;
 }
 
+// Inclusive prefix sums of int64 across the wave (DPP; lanes without a
+// source add 0).
+__device__ __forceinline__ int64_t wave_incl_scan_i64_dpp(int64_t v) {
+#define TMS_ISCAN(CTRL, RM, BZ)                                                            \
+    {                                                                                      \
+        const uint64_t b = (uint64_t)v;                                                    \
+        const uint32_t lo = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)b);                        \
+        const uint32_t hi = dpp_u32<CTRL, RM, BZ>(0u, (uint32_t)(b >> 32));                \
+        v += (int64_t)(((uint64_t)hi << 32) | lo);                                         \
+    }
+    TMS_ISCAN(0x111, 0xF, true)
+    TMS_ISCAN(0x112, 0xF, true)
+    TMS_ISCAN(0x114, 0xF, true)
+    TMS_ISCAN(0x118, 0xF, true)
+    TMS_ISCAN(0x142, 0xA, false)
+    TMS_ISCAN(0x143, 0xC, false)
+#undef TMS_ISCAN
+    return v;
+}
+
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ int wave_sum_dpp(int v) {
     return __builtin_amdgcn_readlane(wave_incl_scan_i32(v), 63);
 }

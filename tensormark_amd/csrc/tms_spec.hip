@@ -29,6 +29,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/tmsample_hip.h"
 #include "tms_context.h"
 #include "tms_device.h"
@@ -57,7 +59,19 @@ struct SArgs {
     tms_spec_stat* stats;
     uint64_t* parts;
     uint32_t* tickets;   // [B][kCounterStride]: resolve parts, or rows of the row kernel
+#ifdef TMS_TRACE
+    uint64_t* trace;     // trace builds: 8 stamps per workgroup
+#endif
 };
+
+#ifdef TMS_TRACE
+#define SPEC_TR(i)                                                                                         \
+    do {                                                                                                   \
+        if (threadIdx.x == 0 && a.trace) a.trace[blockIdx.x * 8 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define SPEC_TR(i) ((void)0)
+#endif
 
 // LDS of a verify workgroup (up to 16 waves).
 struct SpecLds {
@@ -318,7 +332,14 @@ __device__ void accept_tests(const SArgs& a, int b, SpecLds& L, int& status, int
 }
 
 // Part p of sequence b's resolution.
-template <typename T>
+// WAIT (the whole grid resident at once, runs of at most kRunMax ids): every
+// workgroup keeps its part's weights in registers, reads every part's sums
+// (bounded wait), and the one whose part holds the draw's threshold locates
+// the token from its registers; the last reader (by a done counter) zeroes
+// the parts.  Otherwise the last arriver by ticket gathers the parts and
+// recomputes the weights of the part holding the threshold.
+constexpr int kRunMax = 16;
+template <typename T, bool WAIT>
 __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     const double* tab = L.tab;
     int64_t* shl = L.shl;
@@ -330,7 +351,9 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     const tms_row_params P = a.params[b];
     const uint32_t* dw = a.draws ? a.draws + (int64_t)b * (a.k + 1) * 2 : nullptr;
     int status, acc, rej;
+    SPEC_TR(0);
     accept_tests<T>(a, b, L, status, acc, rej);
+    SPEC_TR(1);
     if (status != TMS_ROW_OK) {
         if (p == 0 && t == 0) {
             a.out_acc[b] = 0;
@@ -351,7 +374,30 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     __syncthreads();   // exp table in LDS
     const int lo = p * a.Lp, hi = min(a.V, lo + a.Lp);
     int64_t wsum = 0, tsum = 0;
-    if (rej < 0) {
+    int64_t wr[kRunMax], er[kRunMax];   // WAIT: the run's draw and target weights
+    if constexpr (WAIT) {
+        // a contiguous run of ids per thread, every load issued at once
+        const int E = (hi - lo + kBlock - 1) / kBlock;
+        const int r_lo = min(hi, lo + t * E), r_hi = min(hi, r_lo + E);
+        float xt[kRunMax], xd[kRunMax];
+#pragma unroll
+        for (int j = 0; j < kRunMax; ++j) {
+            const int id = min(r_lo + j, hi - 1);
+            xt[j] = j < E ? Elt<T>::scalar(rt + id) : 0.0f;
+            xd[j] = (j < E && rej >= 0) ? Elt<T>::scalar(rd + id) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kRunMax; ++j) {
+            er[j] = 0;
+            wr[j] = 0;
+            if (r_lo + j < r_hi) {
+                er[j] = weight(xt[j], temp, mt, tab);
+                wr[j] = rej < 0 ? er[j] : residual(er[j], weight(xd[j], temp, md, tab), ts.Z, ds.Z);
+            }
+            tsum += er[j];
+            wsum += wr[j];
+        }
+    } else if (rej < 0) {
         for_range(rt, lo, hi, a.fast, [&](int, float v) { tsum += weight(v, temp, mt, tab); });
         wsum = tsum;
     } else {
@@ -364,20 +410,31 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     }
     wsum = block_sum_i64(wsum, shl);
     tsum = block_sum_i64(tsum, shl + kWaves);
+    SPEC_TR(2);
     uint64_t* pw = a.parts + ((int64_t)b * kSpecParts + p) * 2;
-    uint32_t ticket = 0;
-    if (t == 0) {
-        st_agent(&pw[0], kPartReady | (uint64_t)wsum);
-        st_agent(&pw[1], kPartReady | (uint64_t)tsum);
-        ticket = __hip_atomic_fetch_add(&a.tickets[b * kCounterStride], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        misc[0] = (int)ticket;
+    if constexpr (WAIT) {
+        if (t == 0) {
+            st_agent(&pw[0], kPartReady | (uint64_t)wsum);
+            st_agent(&pw[1], kPartReady | (uint64_t)tsum);
+        }
+    } else {
+        uint32_t ticket = 0;
+        if (t == 0) {
+            st_agent(&pw[0], kPartReady | (uint64_t)wsum);
+            st_agent(&pw[1], kPartReady | (uint64_t)tsum);
+            ticket = __hip_atomic_fetch_add(&a.tickets[b * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+            misc[0] = (int)ticket;
+        }
+        __syncthreads();
+        SPEC_TR(3);
+        if (misc[0] != a.P - 1) return;
+        // the last arriver: its ticket for the next call
+        if (t == 0) st_agent(&a.tickets[b * kCounterStride], 0u);
     }
-    __syncthreads();
-    if (misc[0] != a.P - 1) return;
 
-    // ---- the last arriver: gather the parts (bounded wait on their ready
-    //      bits), zero them and the ticket for the next call.
-    if (t == 0) st_agent(&a.tickets[b * kCounterStride], 0u);
+    // ---- gather the parts (bounded wait on their ready bits); the reader
+    //      that is last zeroes them for the next call.
     int timed_out = 0;
     if (t < a.P) {
         uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * 2;
@@ -391,39 +448,64 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
         timed_out = !((w & kPartReady) && (u & kPartReady));
         part_w[t] = (int64_t)(w & ~kPartReady);
         part_t[t] = (int64_t)(u & ~kPartReady);
-        st_agent(&q[0], (uint64_t)0);
-        st_agent(&q[1], (uint64_t)0);
+        if (!WAIT) {
+            st_agent(&q[0], (uint64_t)0);
+            st_agent(&q[1], (uint64_t)0);
+        }
     }
     timed_out = block_or(timed_out, misc);
-    if (timed_out) {
+    if constexpr (WAIT) {
+        // every word read: the last of the P readers (a relaxed counter; each
+        // adds after its loads returned) zeroes the parts and the counter
         if (t == 0) {
+            const uint32_t done = __hip_atomic_fetch_add(&a.tickets[b * kCounterStride], 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            misc[1] = done == (uint32_t)(a.P - 1) ? 1 : 0;
+        }
+        __syncthreads();
+        if (misc[1]) {
+            if (t < a.P) {
+                uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * 2;
+                st_agent(&q[0], (uint64_t)0);
+                st_agent(&q[1], (uint64_t)0);
+            }
+            if (t == 0) st_agent(&a.tickets[b * kCounterStride], 0u);
+        }
+    }
+    SPEC_TR(4);
+    if (timed_out) {
+        if (t == 0 && (!WAIT || p == 0)) {
             a.out_acc[b] = 0;
             a.out_tok[b] = -1;
             a.out_status[b] = TMS_ROW_INTERNAL;
         }
         return;
     }
-    // Residual mass 0 (p_t <= p_d everywhere on the grid): draw from p_t.
-    int64_t W = 0;
-    for (int i = 0; i < a.P; ++i) W += part_w[i];
+    // The parts' sums across the lanes of each wave (P <= 64), by integer
+    // scans: exact, so W, the threshold's part and the sum before it equal
+    // the sequential sums.  Residual mass 0 (p_t <= p_d everywhere on the
+    // grid): draw from p_t.
+    static_assert(kSpecParts <= 64, "one part per lane");
+    const int pl = t & 63;
+    const int64_t sw = wave_incl_scan_i64_dpp(pl < a.P ? part_w[pl] : 0);
+    const int64_t st = wave_incl_scan_i64_dpp(pl < a.P ? part_t[pl] : 0);
+    int64_t W = readlane_i64(sw, 63);
     const bool use_t = rej < 0 || W == 0;
-    if (use_t) {
-        W = 0;
-        for (int i = 0; i < a.P; ++i) W += part_t[i];
-    }
+    if (use_t) W = readlane_i64(st, 63);
     uint32_t w0, w1;
     if (dw) { w0 = dw[2 * a.k]; w1 = dw[2 * a.k + 1]; }
     else row_words(P.seed, P.offset, (uint32_t)a.k, w0, w1);
     const double uf = canonical(w0, w1);
     int64_t thr = (int64_t)floor(uf * (double)W);
     if (thr > W - 1) thr = W - 1;
-    int ps = a.P - 1;
-    int64_t base = 0;
-    for (int i = 0; i < a.P; ++i) {
-        const int64_t wi = use_t ? part_t[i] : part_w[i];
-        if (base + wi > thr) { ps = i; break; }
-        base += wi;
-    }
+    // the first part whose inclusive sum exceeds thr (the last one does:
+    // thr < W), and the sum of the parts before it
+    const int64_t sc = use_t ? st : sw;
+    const uint64_t over = __ballot(pl < a.P && sc > thr);
+    const int ps = over ? __ffsll((unsigned long long)over) - 1 : a.P - 1;
+    const int64_t base = ps > 0 ? readlane_i64(sc, ps - 1) : 0;
+    if (WAIT && ps != p) return;   // another workgroup holds the threshold's part
+    SPEC_TR(6);
     // The part's weights, a contiguous run of ids per thread.
     const int plo = ps * a.Lp, phi = min(a.V, plo + a.Lp);
     const int E = (phi - plo + kBlock - 1) / kBlock;
@@ -436,12 +518,18 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     };
     // Runs of up to kRunMax ids: every load issued at once (clamped
     // addresses), the weights kept in registers for the scan and the search;
-    // longer runs walk the ids one by one.
-    constexpr int kRunMax = 16;
-    const bool cached = E <= kRunMax;
+    // longer runs walk the ids one by one.  WAIT: this workgroup's own run
+    // weights, still in registers.
+    const bool cached = WAIT || E <= kRunMax;
     int64_t wc[kRunMax];
     int64_t mine = 0;
-    if (cached) {
+    if constexpr (WAIT) {
+#pragma unroll
+        for (int j = 0; j < kRunMax; ++j) {
+            wc[j] = use_t ? er[j] : wr[j];
+            mine += wc[j];
+        }
+    } else if (cached) {
         float xt[kRunMax], xd[kRunMax];
 #pragma unroll
         for (int j = 0; j < kRunMax; ++j) {
@@ -461,11 +549,13 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     } else {
         for (int id = my_lo; id < my_hi; ++id) mine += w_at(id);
     }
+    SPEC_TR(7);
     // Exclusive scan of the threads' sums.
     const int lane = t & 63, wv = t >> 6;
     const int64_t inc = wave_incl_scan_i64(mine);
     if (lane == 63) shl[wv] = inc;
     __syncthreads();
+    SPEC_TR(5);
     int64_t pre = base;
     for (int i = 0; i < wv; ++i) pre += shl[i];
     pre += inc - mine;
@@ -495,11 +585,19 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
 }
 
 
-template <typename T>
+#ifdef TMS_TRACE
+static uint64_t* g_spec_trace;
+extern "C" int tms_spec_trace_set(uint64_t* buf) {
+    g_spec_trace = buf;
+    return 0;
+}
+#endif
+
+template <typename T, bool WAIT>
 __global__ __launch_bounds__(kBlock) void spec_resolve_kernel(SArgs a) {
     __shared__ SpecLds L;
     load_exp_table(L.tab);
-    resolve_part<T>(a, blockIdx.x / a.P, blockIdx.x % a.P, L);
+    resolve_part<T, WAIT>(a, blockIdx.x / a.P, blockIdx.x % a.P, L);
 }
 
 // Row statistics for 16-byte aligned rows of at most kRowT x NS vectors:
@@ -557,6 +655,28 @@ void spec_row_kernel(SArgs a) {
 
 }  // namespace tms
 
+// Whether a resolve grid of n workgroups is resident at once on the current
+// device (occupancy of the waiting form x compute units, looked up once per
+// device and type): the waiting form's workgroups wait on each other.
+template <typename T>
+static bool resolve_resident(int n) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cap[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    int c = cap[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, tms::spec_resolve_kernel<T, true>, tms::kBlock, 0) !=
+                hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return false;
+        c = per_cu * cus > 0 ? per_cu * cus : -1;
+        cap[dev].store(c, std::memory_order_relaxed);
+    }
+    return c > 0 && n <= c;
+}
+
 extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStream_t stream) {
     if (!ctx || !a || !a->target_logits || !a->draft_logits || !a->draft_tokens || !a->params ||
         !a->out_accepted || !a->out_token || !a->out_status)
@@ -594,6 +714,9 @@ extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStre
     s.stats = ctx->spec_stats;
     s.parts = ctx->spec_parts;
     s.tickets = ctx->spec_tickets;
+#ifdef TMS_TRACE
+    s.trace = tms::g_spec_trace;
+#endif
     // 16-byte aligned rows of at most kRowT x 16 vectors (fp32) or x 4
     // (fp16, bf16: 8 spill): the row kernel (two workgroups per CU up to 8
     // vectors a thread); others: the per-row statistics.  Then the resolve.
@@ -616,7 +739,10 @@ extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStre
         } else {                                                                           \
             hipLaunchKernelGGL(tms::spec_stats_kernel<T>, g1, block, 0, stream, s);        \
         }                                                                                  \
-        hipLaunchKernelGGL(tms::spec_resolve_kernel<T>, g2, block, 0, stream, s);          \
+        if (resolve_resident<T>(a->batch * s.P) && (s.Lp + tms::kBlock - 1) / tms::kBlock <= tms::kRunMax) \
+            hipLaunchKernelGGL((tms::spec_resolve_kernel<T, true>), g2, block, 0, stream, s);  \
+        else                                                                               \
+            hipLaunchKernelGGL((tms::spec_resolve_kernel<T, false>), g2, block, 0, stream, s); \
     } while (0)
     switch (a->dtype) {
         case TMS_DTYPE_F32: TMS_SPEC_LAUNCH(float, 8, 16); break;
