@@ -44,6 +44,36 @@
 
 namespace tms {
 
+// Every thread of the workgroup: out[r] = keys[i] for every i < n, r the
+// number of larger keys (keys 16-byte aligned, readable up to n + 16).  P
+// neighbouring lanes share a key (P = kBlock / n rounded down to a power of
+// two, at most 8), each counting the larger keys in its share of the list in
+// 16-byte reads; the shares meet by DPP within the group.  Equal keys (the
+// zero keys of dropped top-p entries) land on one slot.
+__device__ __forceinline__ void rank_all(const uint64_t* keys, int n, uint64_t* out) {
+    const int t = threadIdx.x;
+    int P = 8;
+    while (P > 1 && P * n > kBlock) P >>= 1;
+    const int L = ((n + P - 1) / P + 1) & ~1;
+    for (int b0 = 0; b0 < n; b0 += kBlock / P) {
+        const int i = b0 + t / P, part = t & (P - 1);
+        const uint64_t k = i < n ? keys[i] : ~0ull;
+        const ulonglong2* c2 = (const ulonglong2*)(keys + part * L);
+        int cnt = 0;
+#pragma unroll 4
+        for (int q = 0; q < (L >> 1); ++q) {
+            const ulonglong2 y = c2[q];
+            const int j = part * L + 2 * q;
+            cnt += (j < n && y.x > k ? 1 : 0) + (j + 1 < n && y.y > k ? 1 : 0);
+        }
+        uint32_t u = (uint32_t)cnt;
+        if (P >= 2) u += dpp_u32<0xB1, 0xF, false>(0u, u);    // quad_perm [1, 0, 3, 2]
+        if (P >= 4) u += dpp_u32<0x4E, 0xF, false>(0u, u);    // quad_perm [2, 3, 0, 1]
+        if (P >= 8) u += dpp_u32<0x141, 0xF, false>(0u, u);   // row_half_mirror
+        if (part == 0 && i < n) out[u] = k;
+    }
+}
+
 // Ranks of the n distinct keys keys[0..n) (n <= kUni, any order; the
 // whole workgroup): every key whose rank r (the number of larger keys) is
 // below nkeep lands at out[r].  Each key goes to one of kBuckets buckets by
@@ -779,20 +809,13 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                     if (lane == 0) sm.wave_i[wv] = nv;
                 }
                 lds_sync();
+                TMS_TR(17);
+                TMS_TV(19, n + 1);
                 if (mode == MODE_TOPP) nout = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
                 else nout = n < K ? n : K;
-                for (int i = t; i < n; i += kBlock) {
-                    const uint64_t k = keys[i];
-                    int r0 = 0, r1 = 0;
-                    int jj = 0;
-                    for (; jj + 1 < n; jj += 2) {
-                        r0 += keys[jj] > k ? 1 : 0;
-                        r1 += keys[jj + 1] > k ? 1 : 0;
-                    }
-                    if (jj < n) r0 += keys[jj] > k ? 1 : 0;
-                    sm.cand[r0 + r1] = k;
-                }
+                rank_all(keys, n, sm.cand);
                 lds_sync();
+                TMS_TR(18);
             }
         }
         if (!anynf && !bad_params && (fallback || n > kCand)) {
