@@ -653,6 +653,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                                                     (double)temp);
             if (thr == NEG_INF) thr = -FLT_MAX;
         }
+        TMS_TR(20);
         int n = 0;
         if (!anynf && !bad_params && !fallback) {
             // Each wave compacts its candidates with ballots into its own
@@ -784,6 +785,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
 #pragma unroll
                 for (int w = 1; w < kWaves; ++w) cw[w] = 0;
             }
+            TMS_TR(21);
             if (n <= kCand) {
                 // Dense pass (the window counts are dead now): divide the
                 // candidates, form their keys contiguously in uni; top-p drops
