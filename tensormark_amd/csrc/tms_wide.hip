@@ -1,35 +1,37 @@
 // tms_wide.hip -- the sampler kernel for batches whose rows are all greedy or
 // top-k with k <= 128 (the host picks it from the caller's row-kind hint),
-// with 1024-thread workgroups.
+// with 1024-thread workgroups whose grid is resident at once.
 //
 // One launch per call.  Row b is cut into S <= 16 chunks; workgroup (b, c)
-// streams chunk c once: 1024 threads x 4 nontemporal 16-byte loads each, so a
-// CU holds two workgroups (32 waves) and keeps enough bytes in flight to run
-// the stream near the HBM rate (a bare stream of 33 MB measured 8.7 us with
-// 512 x 256-thread workgroups and 5.9 us with 512 x 1024).
+// streams chunk c once, each thread kSlots nontemporal 16-byte loads: 8 for
+// fp32 rows at one workgroup per CU (config 2: S = 4), else 4 at two per CU.
+// A bare stream of 33 MB measured 8.7 us with 512 x 256-thread workgroups and
+// 5.9 us with 512 x 1024.
 //
 //   window    while the stream is in flight: the row's history ids that fall
-//             in the chunk are set in an LDS bitmap and listed; the first
-//             position holding an id owns it, counts its occurrences and
-//             loads its logit and mask bit (tmsample.h:52-63 compounding,
-//             then frequency/presence).  The stream leaves those ids out; the
-//             owners bring them back penalised.
+//             in the chunk go into an LDS bitmap and a hash table; the first
+//             position holding an id owns it and counts its occurrences.  The
+//             stream leaves those ids out; after the bound the owners bring
+//             them back penalised (tmsample.h:52-63 compounding, then
+//             frequency/presence).
 //   pass 1    per 16-byte slot: mask bit (and not a window id) -> value,
 //             else -inf; the thread's maximum; NaN / +inf flagged.
-//   bound     each wave takes its 8 (or fewer) largest thread maxima; the
-//             K-th largest of those 16 lists bounds the chunk's K-th value
-//             from below (K thread maxima, each a distinct entry, reach it).
+//   bound     the maxima of 128 groups of lanes (DPP); wave 0 bisects for the
+//             K-th largest, which bounds the chunk's K-th value from below (K
+//             groups, each with a distinct entry, reach it); wave 1 does the
+//             same for ceil(K / S) groups, for the merger's pruning.
 //   select    every entry whose v / T can reach the bound's quotient is a
-//             candidate (the division runs on candidates only); candidates
-//             are ranked by counting, and the chunk's sorted top min(n, K)
-//             keys (v / T, then lowest id) are published.  A chunk with more
-//             than 1024 candidates (massive ties) takes an exact radix select
-//             over the keys instead.
+//             candidate (the division runs on candidates only): hot lanes
+//             stage their words in LDS and each wave appends its takes.  Up
+//             to 128 candidates are published unranked; more are ranked and
+//             the top K published; over 1024 (massive ties) take an exact
+//             radix select over the keys.  The list header carries both
+//             bounds.
 //   merge     the last chunk of the row to take a ticket reads the other
 //             lists (a word still in flight reads 0 and is read again; the
-//             merger returns every word it read to 0), ranks each key by its
-//             position in its own list plus binary searches in the others,
-//             and runs the fp64 tail of tmsample::sample
+//             merger returns every word it read to 0), keeps the keys at or
+//             above the quotient of the larger of the two bounds, ranks them
+//             together, and runs the fp64 tail of tmsample::sample
 //             (tensormark/tmsample.h:184-199) on one wave.
 #include "tms_sample_common.h"
 
