@@ -5,7 +5,8 @@
 // loads into registers (64 values per thread), applies the grammar mask and
 // the history penalties there, and reduces the chunk to a short sorted
 // candidate list.  The last workgroup of the row to finish its stream merges
-// the S lists and runs the sequential fp64 tail of tmsample::sample
+// the S lists (top-k rows from a pruned sample of them; whole lists ranked by
+// value buckets otherwise) and runs the fp64 tail of tmsample::sample
 // (tensormark/tmsample.h:184-199): softmax over the top-k, top-p and min-p
 // cuts, and the inverse-CDF draw.
 //
@@ -18,8 +19,8 @@
 //           when the bound admits too many.
 //   top-p   K > kTopkFast (top_k = 0 or large): every chunk entry whose
 //           probability can change the fp64 sums, i.e. v / T within 40 of
-//           the chunk maximum (exp(-40) < 2^-57); rows with more than the
-//           capacity report TMS_ROW_UNSUPPORTED.
+//           the chunk maximum (exp(-40) < 2^-57); rows past the capacity
+//           go to the whole-row pass (tms_dense.hip).
 //
 // Timeline of a workgroup: the stream's loads are the kernel's first
 // instructions and are issued unconditionally (clamped addresses, an all-ones
