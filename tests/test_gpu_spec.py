@@ -169,3 +169,23 @@ def test_spec_back_to_back_different_batches(orc, sampler):
         gpu = run_spec(sampler, c["target"], c["draft"], c["tokens"], c["params"])
         words = philox_words(orc, c["params"], c["draft"].shape[1])
         check_spec(orc, gpu, c["target"], c["draft"], c["tokens"], c["params"], words)
+
+
+@pytest.mark.parametrize("B,V", [(24, 140000), (4, 262144)])
+def test_spec_resolve_ticket_form(orc, sampler, B, V):
+    """Resolve grids that are not resident at once (24 sequences x 64 parts)
+    and part runs past 16 ids a thread (V = 262144: 4,096 ids a part) take
+    the ticket form, whose last arriver recomputes the threshold's part;
+    config 4 itself takes the waiting form.  Rows this long also take the
+    two-pass statistics kernel."""
+    rng = np.random.default_rng(B)
+    k = 2
+    target = rng.normal(0.0, 2.0, (B, k + 1, V)).astype(np.float32)
+    draft = (target[:, :k] + rng.normal(0.0, 0.5, (B, k, V))).astype(np.float32)
+    tokens = workloads.softmax_draws(rng, draft)
+    params = params_array(B, temperature=1.0, top_k=0, top_p=1.0, seed=np.arange(B) + 3)
+    params["temperature"] = rng.choice([0.8, 1.0], size=B)
+    gpu = run_spec(sampler, target, draft, tokens, params)
+    words = philox_words(orc, params, k)
+    check_spec(orc, gpu, target, draft, tokens, params, words)
+    assert (gpu["status"] == 0).all()
