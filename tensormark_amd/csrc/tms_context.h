@@ -14,6 +14,7 @@
 namespace tms {
 constexpr int kSpecMaxK = 16;      // draft tokens per sequence
 constexpr int kSpecParts = 64;     // vocabulary parts of the residual draw
+constexpr int kPartWords = 3;      // u64 per part: weight sum, target sum, the bonus row's part max
 constexpr int kCounterStride = 64; // u32 between per-row arrival counters: one 256-byte line
                                    // each, so the rows' atomics do not queue on one line
 }  // namespace tms
@@ -40,7 +41,7 @@ struct tms_context {
     uint64_t* lists;           // [max_batch][max_chunks][kListStride] chunk candidate lists
     uint64_t* tlists;          // [max_batch][min(max_chunks, 16)][1280] top-k kernel lists
     uint32_t* spec_tickets;    // [max_batch][kCounterStride] verify arrival counters (word 0)
-    uint64_t* spec_parts;      // [max_batch][kSpecParts][2] published partial sums
+    uint64_t* spec_parts;      // [max_batch][kSpecParts][kPartWords] published partial sums
     tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]
     uint32_t* dqueue;          // whole-row pass queue: 3 counters, then [max_batch] rows
     int32_t* ov_n;             // [max_batch] history pre-pass: list lengths (-1: overflow)

@@ -1291,7 +1291,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_l = off_ones + 256 * ((ones_words * 4 + 255) / 256);
     const size_t off_st = off_l + nc * tms::kListStride * sizeof(uint64_t);
     const size_t off_sp = off_st + nb * tms::kCounterStride * 4;   // one 256-byte line per ticket
-    const size_t off_ss = off_sp + nb * tms::kSpecParts * 2 * sizeof(uint64_t);
+    const size_t off_ss = off_sp + nb * tms::kSpecParts * tms::kPartWords * sizeof(uint64_t);
     const size_t off_tl = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
     const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kLeanMaxChunksHost);
     const size_t off_dq = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);

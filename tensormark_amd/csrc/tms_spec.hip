@@ -50,6 +50,7 @@ struct SArgs {
     int B, k, V;
     bool fast;   // rows 16-byte aligned and V a multiple of the vector width
     int P, Lp;   // vocabulary parts of the two-launch resolve and their length
+    bool lazy;   // the row kernel leaves the bonus rows (target row k) to the resolve
     const int32_t* tokens;
     const tms_row_params* params;
     const uint32_t* draws;
@@ -328,7 +329,7 @@ __device__ void accept_tests(const SArgs& a, int b, SpecLds& L, int& status, int
         rej = i;
         break;
     }
-    if (rej < 0 && L.srow[a.k].status) status = L.srow[a.k].status;
+    if (rej < 0 && !a.lazy && L.srow[a.k].status) status = L.srow[a.k].status;
 }
 
 // Part p of sequence b's resolution.
@@ -386,12 +387,80 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
             xt[j] = j < E ? Elt<T>::scalar(rt + id) : 0.0f;
             xd[j] = (j < E && rej >= 0) ? Elt<T>::scalar(rd + id) : 0.0f;
         }
+        double mtu = mt;
+        if (a.lazy && rej < 0) {
+            // The bonus row's statistics (the row kernel left them): each
+            // part's max of v / T and NaN / +inf flag, exchanged between the
+            // sequence's workgroups; the status rules of the statistics
+            // kernels (tmo_spec_weights).
+            float pm = -__builtin_huge_valf();
+            int pnf = 0;
+#pragma unroll
+            for (int j = 0; j < kRunMax; ++j) {
+                if (r_lo + j < r_hi) {
+                    const float v = xt[j];
+                    pnf |= (__builtin_isnan(v) || v == __builtin_huge_valf()) ? 1 : 0;
+                    pm = fmaxf(pm, scaled(v, temp));
+                }
+            }
+            pm = block_max_f32(pm, L.shf);
+            pnf = block_or(pnf, misc);
+            uint64_t* mw = a.parts + ((int64_t)b * kSpecParts + p) * kPartWords + 2;
+            if (t == 0) st_agent(mw, kPartReady | ((uint64_t)pnf << 32) | okey(pm));
+            int bad = 0;
+            uint32_t km = 0;
+            int knf = 0;
+            if (t < a.P) {
+                const uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * kPartWords + 2;
+                uint64_t h = 0;
+                for (int it = 0; it < kPartPoll; ++it) {
+                    h = ld_agent(q);
+                    if (h & kPartReady) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                bad = (h & kPartReady) ? 0 : 1;
+                km = (uint32_t)h;
+                knf = (int)((h >> 32) & 1u);
+            }
+            // the bonus maxima's readers: the last zeroes the words and its counter
+            km = (uint32_t)wave_max_u64(km);
+            if ((t & 63) == 0) L.shl[t >> 6] = (int64_t)km;
+            bad = block_or(bad, misc);
+            knf = block_or(knf, misc);
+            if (t == 0) {
+                const uint32_t done = __hip_atomic_fetch_add(&a.tickets[b * kCounterStride + 1], 1u,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                misc[2] = done == (uint32_t)(a.P - 1) ? 1 : 0;
+            }
+            __syncthreads();
+            uint32_t kmax = (uint32_t)L.shl[0];
+            for (int w = 1; w < kWaves; ++w) kmax = max(kmax, (uint32_t)L.shl[w]);
+            if (misc[2]) {
+                if (t < a.P) st_agent(a.parts + ((int64_t)b * kSpecParts + t) * kPartWords + 2, (uint64_t)0);
+                if (t == 0) st_agent(&a.tickets[b * kCounterStride + 1], 0u);
+            }
+            const float gm = okey_inv(kmax);
+            int st = TMS_ROW_OK;
+            if (bad) st = TMS_ROW_INTERNAL;
+            else if (knf) st = TMS_ROW_NONFINITE;
+            else if (gm == -__builtin_huge_valf()) st = TMS_ROW_ALL_MASKED;
+            else if (gm == __builtin_huge_valf()) st = TMS_ROW_NONFINITE;
+            if (st != TMS_ROW_OK) {
+                if (p == 0 && t == 0) {
+                    a.out_acc[b] = 0;
+                    a.out_tok[b] = -1;
+                    a.out_status[b] = st;
+                }
+                return;   // every workgroup of the sequence: no parts published
+            }
+            mtu = (double)gm;
+        }
 #pragma unroll
         for (int j = 0; j < kRunMax; ++j) {
             er[j] = 0;
             wr[j] = 0;
             if (r_lo + j < r_hi) {
-                er[j] = weight(xt[j], temp, mt, tab);
+                er[j] = weight(xt[j], temp, mtu, tab);
                 wr[j] = rej < 0 ? er[j] : residual(er[j], weight(xd[j], temp, md, tab), ts.Z, ds.Z);
             }
             tsum += er[j];
@@ -411,7 +480,7 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     wsum = block_sum_i64(wsum, shl);
     tsum = block_sum_i64(tsum, shl + kWaves);
     SPEC_TR(2);
-    uint64_t* pw = a.parts + ((int64_t)b * kSpecParts + p) * 2;
+    uint64_t* pw = a.parts + ((int64_t)b * kSpecParts + p) * kPartWords;
     if constexpr (WAIT) {
         if (t == 0) {
             st_agent(&pw[0], kPartReady | (uint64_t)wsum);
@@ -437,7 +506,7 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     //      that is last zeroes them for the next call.
     int timed_out = 0;
     if (t < a.P) {
-        uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * 2;
+        uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * kPartWords;
         uint64_t w = 0, u = 0;
         for (int it = 0; it < kPartPoll; ++it) {
             w = ld_agent(&q[0]);
@@ -465,7 +534,7 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
         __syncthreads();
         if (misc[1]) {
             if (t < a.P) {
-                uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * 2;
+                uint64_t* q = a.parts + ((int64_t)b * kSpecParts + t) * kPartWords;
                 st_agent(&q[0], (uint64_t)0);
                 st_agent(&q[1], (uint64_t)0);
             }
@@ -613,9 +682,12 @@ void spec_row_kernel(SArgs a) {
     __shared__ SpecLds L;
     load_exp_table(L.tab);
     const int t = threadIdx.x;
-    const int R = 2 * a.k + 1;
+    // lazy: 2k rows a sequence (the bonus row k left to the resolve)
+    const int R = a.lazy ? 2 * a.k : 2 * a.k + 1;
     const int g = blockIdx.x;
-    const int b = g / R, i = g - b * R;
+    const int b = g / R;
+    int i = g - b * R;
+    if (a.lazy && i >= a.k) ++i;
     const T* row = spec_row<T>(a, b, i);
     const float temp = a.params[b].temperature;
     const bool div = temp != 1.0f;
@@ -645,7 +717,7 @@ void spec_row_kernel(SArgs a) {
             const int x = a.tokens[(int64_t)b * a.k + di];
             if (x >= 0 && x < a.V) ex = weight(Elt<T>::scalar(row + x), temp, md, L.tab);
         }
-        uint64_t* w = (uint64_t*)(a.stats + g);
+        uint64_t* w = (uint64_t*)(a.stats + (int64_t)b * (2 * a.k + 1) + i);
         st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)st << 32));
         st_agent(&w[1], (uint64_t)z);
         st_agent(&w[2], (uint64_t)ex);
@@ -725,10 +797,18 @@ extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStre
     const int max_ns = esz == 4 ? 16 : 4;
     const int row_ns = (!s.fast || slots > max_ns) ? 0 : slots <= 4 ? 4 : slots <= 8 ? 8 : 16;
     const dim3 block(tms::kBlock);
-    const dim3 g1((unsigned)(a->batch * R)), g2((unsigned)(a->batch * s.P));
+    const dim3 g2((unsigned)(a->batch * s.P));
     const dim3 brow(tms::kRowT);
+    // The waiting resolve (its grid resident at once, runs of at most
+    // kRunMax ids) takes the bonus rows' statistics itself when the row
+    // kernel runs: 2k rows a sequence there (config 4: 512 rows, one round
+    // of two workgroups per CU, in place of 544).
 #define TMS_SPEC_LAUNCH(T, NS2, NS3)                                                       \
     do {                                                                                   \
+        const bool wait = resolve_resident<T>(a->batch * s.P) &&                          \
+                          (s.Lp + tms::kBlock - 1) / tms::kBlock <= tms::kRunMax;          \
+        s.lazy = wait && row_ns > 0;                                                       \
+        const dim3 g1((unsigned)(a->batch * (s.lazy ? R - 1 : R)));                        \
         if (row_ns > 0) {                                                                  \
             if (row_ns == 4)                                                               \
                 hipLaunchKernelGGL((tms::spec_row_kernel<T, 4>), g1, brow, 0, stream, s);  \
@@ -739,7 +819,7 @@ extern "C" int tms_spec_verify(tms_context* ctx, const tms_spec_args* a, hipStre
         } else {                                                                           \
             hipLaunchKernelGGL(tms::spec_stats_kernel<T>, g1, block, 0, stream, s);        \
         }                                                                                  \
-        if (resolve_resident<T>(a->batch * s.P) && (s.Lp + tms::kBlock - 1) / tms::kBlock <= tms::kRunMax) \
+        if (wait)                                                                          \
             hipLaunchKernelGGL((tms::spec_resolve_kernel<T, true>), g2, block, 0, stream, s);  \
         else                                                                               \
             hipLaunchKernelGGL((tms::spec_resolve_kernel<T, false>), g2, block, 0, stream, s); \

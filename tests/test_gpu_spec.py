@@ -189,3 +189,27 @@ def test_spec_resolve_ticket_form(orc, sampler, B, V):
     words = philox_words(orc, params, k)
     check_spec(orc, gpu, target, draft, tokens, params, words)
     assert (gpu["status"] == 0).all()
+
+
+def test_spec_bonus_row_statistics_in_the_resolve(orc, sampler):
+    """The resolve forms the bonus row's statistics itself (every part's
+    maximum exchanged between the sequence's workgroups; V = 6000: three
+    parts): an all-masked bonus row after every draft is accepted, a NaN
+    in a bonus row that a rejection leaves unused, a NaN in the last part of
+    an accepted sequence's bonus row, and plain accepted sequences."""
+    rng = np.random.default_rng(47)
+    B, k, V = 6, 3, 6000
+    target = rng.normal(0, 1.5, size=(B, k + 1, V)).astype(np.float32)
+    draft = target[:, :k].copy()                 # equal: every draft is accepted
+    draft[1] = (draft[1] + rng.normal(0, 4.0, size=(k, V))).astype(np.float32)
+    tokens = workloads.softmax_draws(rng, draft)
+    params = params_array(B, temperature=1.0, seed=np.arange(B, dtype=np.uint64) + 9)
+    params["temperature"][3] = 0.7
+    target[0, k, :] = -np.inf                    # all-masked bonus row
+    target[1, k, 100] = np.nan                   # unused when a draft is rejected
+    target[2, k, V - 7] = np.nan                 # last part of the bonus row
+    gpu = run_spec(sampler, target, draft, tokens, params)
+    words = philox_words(orc, params, k)
+    check_spec(orc, gpu, target, draft, tokens, params, words)
+    assert gpu["status"][0] == 2 and gpu["status"][2] == 3
+    assert (gpu["status"][3:] == 0).all() and (gpu["accepted"][3:] == k).all()
