@@ -422,9 +422,12 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
                 km = (uint32_t)h;
                 knf = (int)((h >> 32) & 1u);
             }
-            // the bonus maxima's readers: the last zeroes the words and its counter
+            // the bonus maxima's readers: the last zeroes the words and its
+            // counter.  The waves' maxima meet in part_w, whose next writes
+            // (the part sums' gather) come after the sums' barriers; shl is
+            // the sums' own scratch.
             km = (uint32_t)wave_max_u64(km);
-            if ((t & 63) == 0) L.shl[t >> 6] = (int64_t)km;
+            if ((t & 63) == 0) part_w[t >> 6] = (int64_t)km;
             bad = block_or(bad, misc);
             knf = block_or(knf, misc);
             if (t == 0) {
@@ -433,8 +436,8 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
                 misc[2] = done == (uint32_t)(a.P - 1) ? 1 : 0;
             }
             __syncthreads();
-            uint32_t kmax = (uint32_t)L.shl[0];
-            for (int w = 1; w < kWaves; ++w) kmax = max(kmax, (uint32_t)L.shl[w]);
+            uint32_t kmax = (uint32_t)part_w[0];
+            for (int w = 1; w < kWaves; ++w) kmax = max(kmax, (uint32_t)part_w[w]);
             if (misc[2]) {
                 if (t < a.P) st_agent(a.parts + ((int64_t)b * kSpecParts + t) * kPartWords + 2, (uint64_t)0);
                 if (t == 0) st_agent(&a.tickets[b * kCounterStride + 1], 0u);
