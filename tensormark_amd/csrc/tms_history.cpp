@@ -10,6 +10,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <utility>
 #include <vector>
 
@@ -57,6 +58,14 @@ extern "C" void tms_host_no_repeat_ngram(float* logits, int V, const int32_t* re
 // with the window's tail for L >= allowed_length ids (never across a breaker
 // id), subtract multiplier * base^(L - allowed_length) from the id that
 // followed the earlier run.
+//
+// Every position's agreement comes from one linear pass: with the window
+// reversed (r[j] = id at last - j), the agreement of the run ending at i
+// with the tail is the longest common prefix of r and r[last - i ..], which
+// the Z-function gives for every shift at once.  Each breaker occurrence
+// becomes a code of its own (below every id), so no match extends across
+// one.  The penalties are applied in ascending position order, as the
+// reference applies them.
 extern "C" void tms_host_dry(float* logits, int V, const int32_t* recent, int n_recent,
                              float multiplier, float base, int allowed_length, int penalty_last_n,
                              const unsigned char* is_breaker) {
@@ -65,15 +74,27 @@ extern "C" void tms_host_dry(float* logits, int V, const int32_t* recent, int n_
     if (n_recent < allowed_length + 1 || n < allowed_length + 1) return;
     const int32_t* w = recent + (n_recent - n);
     const int last = n - 1;
+    auto breaker = [&](int32_t id) { return is_breaker && id >= 0 && id < V && is_breaker[id]; };
+    std::vector<int64_t> r((size_t)n);
+    for (int j = 0; j < n; ++j) {
+        const int32_t id = w[last - j];
+        r[(size_t)j] = breaker(id) ? INT64_MIN + j : (int64_t)id;
+    }
+    std::vector<int> z((size_t)n, 0);   // z[d]: common prefix of r and r[d..]
+    for (int d = 1, lo = 0, hi = 0; d < n; ++d) {
+        int k = d < hi ? std::min(hi - d, z[(size_t)(d - lo)]) : 0;
+        while (d + k < n && r[(size_t)k] == r[(size_t)(d + k)]) ++k;
+        z[(size_t)d] = k;
+        if (d + k > hi) {
+            lo = d;
+            hi = d + k;
+        }
+    }
     for (int i = 0; i < last; ++i) {
-        int L = 0;
-        while (L <= i && w[i - L] == w[last - L] &&
-               !(is_breaker && (is_breaker[w[i - L]] || is_breaker[w[last - L]])))
-            ++L;
+        const int L = z[(size_t)(last - i)];
         if (L < allowed_length) continue;
-        const int next = w[i + 1];
-        if (next < 0 || next >= V) continue;
-        if (is_breaker && is_breaker[next]) continue;
+        const int32_t next = w[i + 1];
+        if (next < 0 || next >= V || breaker(next)) continue;
         logits[next] -= multiplier * tms_dry_scale(base, L - allowed_length);
     }
 }
