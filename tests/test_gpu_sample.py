@@ -205,6 +205,32 @@ def test_topp_rows_bucket_ties(sampler, orc, grid):
     check(g, want)
 
 
+def test_topk_128_tie_heavy_rows(sampler, orc):
+    """top_k = 128 rows built to stress the wide kernel's chunk paths: values
+    on a coarse grid (more than 128 candidates a chunk: the chunk ranks and
+    publishes its top K), all-equal rows (more than 1024: the exact radix
+    select), and rows with a few peaks; V = 200000 fp32 is seven chunks of
+    the 8-slot form.  The top-k ids come back in rank order."""
+    rng = np.random.default_rng(53)
+    B, V = 24, 200000
+    x = rng.normal(0.0, 1.0, (B, V)).astype(np.float32)
+    kind = np.arange(B) % 3
+    for b in range(B):
+        if kind[b] == 0:
+            x[b] = np.round(x[b] * 2.0) / 2.0
+        elif kind[b] == 1:
+            x[b] = 0.5
+        else:
+            x[b, rng.choice(V, 40, replace=False)] += 6.0
+    p = params_array(B, temperature=1.0, top_k=128, top_p=1.0, seed=np.arange(B) + 17)
+    p["temperature"] = rng.choice([0.7, 1.0, 1.3], size=B)
+    p["top_p"] = rng.choice([0.5, 0.95, 1.0], size=B)
+    p["greedy"] = (np.arange(B) % 8 == 7).astype(np.int32)
+    want = orc.sample_batch(x, p, topk_cap=128)
+    g = run_gpu(sampler, x, p, topk_cap=128)
+    check(g, want, 128)
+
+
 def test_cfg5_rows_bf16_vs_oracle(sampler, orc):
     w = workloads.cfg5(B=48)
     bits = workloads.to_bf16_bits(w["logits"])
