@@ -465,7 +465,9 @@ int tms_embed_gather(const void* table, int dtype, int64_t rows, int64_t dim, co
  * tuples packed as 6 words each and write 4 words each; evaluate the device
  * double exp on n inputs (which = 0: the HIP math library, 1: the
  * library's own exp used by tms_spec_verify, 2: tms_spec_verify's weight
- * q44(exp(x)) for x <= 0 as a double, the integer count of 2^-44 units).
+ * q44(exp(x)) for x <= 0 as a double, the integer count of 2^-44 units;
+ * 3: the quotients in[2i] / in[2i + 1] by tms_spec_verify's division from
+ * a reciprocal, into out[i] for i < n / 2).
  */
 int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipStream_t stream);
 /* Checks of the device ordering the cross-workgroup protocols rely on

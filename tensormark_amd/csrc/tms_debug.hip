@@ -1,5 +1,5 @@
-// tms_debug.hip -- test hooks: run the device Philox and the device double
-// exp on caller inputs so the tests can pin them against the host checker,
+// tms_debug.hip -- test hooks: run the device Philox, the device double
+// exp and the reciprocal-based division on caller inputs so the tests can pin them against the host checker,
 // and check the ordering properties of the device that the library's
 // cross-workgroup protocols rely on.
 
@@ -28,6 +28,10 @@ __global__ void exp_kernel(const double* in, double* out, int n, int which) {
     if (threadIdx.x < 64) tab[threadIdx.x] = kExpTab[threadIdx.x];
     __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (which == 3) {   // quotients of the pairs (in[2i], in[2i + 1]) into out[i]
+        if (2 * i + 1 < n) out[i] = div_rn(in[2 * i], in[2 * i + 1], 1.0 / in[2 * i + 1]);
+        return;
+    }
     if (i >= n) return;
     out[i] = which == 2 ? (double)q44_exp_nonpos(in[i], tab) : which ? exp64(in[i], tab) : exp(in[i]);
 }
@@ -173,7 +177,7 @@ extern "C" int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipS
 }
 
 extern "C" int tms_debug_exp(const double* in, double* out, int n, int which, hipStream_t stream) {
-    if (!in || !out || n < 0 || which < 0 || which > 2) return TMS_ERR_INVALID_ARG;
+    if (!in || !out || n < 0 || which < 0 || which > 3) return TMS_ERR_INVALID_ARG;
     if (n == 0) return TMS_OK;
     hipLaunchKernelGGL(tms::exp_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, in, out, n, which);
     return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;

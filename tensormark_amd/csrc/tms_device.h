@@ -140,14 +140,16 @@ __device__ __forceinline__ int64_t q44(double y) {
     return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
-// q44(exp64(x)) for x <= 0, bit-identical to the pair above.  Below -40 the
-// weight is 0: exp64(x) < e^-40 < 2^-57, which rounds to 0 on the 2^-44
-// grid.  On [-40, 0] exp64 takes none of its special cases (2^m is normal,
-// m >= -58), and its final scaling by 2^m and q44's by 2^44 are both exact,
-// so they fold into one multiplication by 2^(m + 44).  A NaN gives 0.
-__device__ __forceinline__ int64_t q44_exp_nonpos(double x, const double* tab) {
-    const bool zero = !(x >= -40.0);
-    const double xc = zero ? 0.0 : x;
+// q44(exp64(x)) for x <= 0, bit-identical to the pair above, as a double
+// holding the whole number (at most 2^44, so sums of up to 128 of them stay
+// exact and below 2^52).  Below -40 the weight is 0: exp64(x) < e^-40 < 2^-57, which rounds
+// to 0 on the 2^-44 grid; the argument is clamped at -41, where the same
+// holds, so no select is needed (a NaN clamps to -41 too).  On [-41, 0]
+// exp64 takes none of its special cases (2^m is normal, m >= -60), and its
+// final scaling by 2^m and q44's by 2^44 are both exact, so they fold into
+// one ldexp by m + 44.
+__device__ __forceinline__ double q44_exp_nonpos_f(double x, const double* tab) {
+    const double xc = fmax(x, -41.0);
     const double kd = floor(xc * 0x1.71547652b82fep+6 + 0.5);
     double r = fma(-kd, 0x1.62e42fefa39efp-7, xc);
     r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
@@ -159,10 +161,28 @@ __device__ __forceinline__ int64_t q44_exp_nonpos(double x, const double* tab) {
     p = fma(p, r, 1.0);
     const int ki = (int)kd;
     const double y = tab[ki & 63] * p;
-    const double s = __longlong_as_double((long long)((ki >> 6) + 44 + 1023) << 52);
-    const double f = floor(y * s + 0.5);
-    const int64_t w = __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
-    return zero ? 0 : w;
+    return floor(ldexp(y, (ki >> 6) + 44) + 0.5);
+}
+
+// a / b correctly rounded, given y = RN(1/b) (one division per divisor in
+// place of one per element).  q0 = RN(a * y) is within 1.5 ulp of a / b; the
+// remainder a - b * q0 is exact by fma, and q1 = RN(q0 + r0 * y) is within
+// an ulp (faithful); from a faithful quotient and the correctly rounded
+// reciprocal, one more correction returns RN(a / b) (Markstein, IBM J. Res.
+// Dev. 34(1), 1990).  For finite a, b whose quotient, remainders and
+// reciprocal neither overflow nor fall below the normal range.
+__device__ __forceinline__ double div_rn(double a, double b, double y) {
+    double q = a * y;
+    double r = fma(-b, q, a);
+    q = fma(r, y, q);
+    r = fma(-b, q, a);
+    return fma(r, y, q);
+}
+
+// The same weight as an int64 (the bit-pattern difference of q44).
+__device__ __forceinline__ int64_t q44_exp_nonpos(double x, const double* tab) {
+    const double f = q44_exp_nonpos_f(x, tab);
+    return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
 // ------------------------------------------------------------ reductions

@@ -187,12 +187,29 @@ __device__ __forceinline__ int64_t weight(float v, float temp, double m, const d
     return q44_exp_nonpos((double)scaled<DIV>(v, temp) - m, tab);
 }
 
-// Residual weight q44(max(p_t - p_d, 0)) from the two rows' weights.
-__device__ __forceinline__ int64_t residual(int64_t et, int64_t ed, int64_t Zt, int64_t Zd) {
-    const double pt = (double)et / (double)Zt;
-    const double pd = (double)ed / (double)Zd;
-    const double d = pt - pd;
-    return d > 0.0 ? q44(d) : 0;
+// The same weight as a double holding the whole number.
+template <bool DIV = true>
+__device__ __forceinline__ double weight_f(float v, float temp, double m, const double* tab) {
+    return q44_exp_nonpos_f((double)scaled<DIV>(v, temp) - m, tab);
+}
+
+// Residual weight q44(max(p_t - p_d, 0)) from the two rows' weights (whole
+// numbers as doubles), p = e / (double)Z.  The divisors' reciprocals are
+// formed once (Resid), and div_rn returns the correctly rounded quotients,
+// the same as dividing per element.  Z >= 2^44 for a row that reaches here
+// (its maximum has weight 2^44), so nothing overflows or is subnormal.
+struct Resid {
+    double zt, zd, yt, yd;
+    __device__ __forceinline__ Resid(int64_t Zt, int64_t Zd)
+        : zt((double)Zt), zd((double)Zd), yt(1.0 / (double)Zt), yd(1.0 / (double)Zd) {}
+    __device__ __forceinline__ int64_t operator()(double et, double ed) const {
+        const double d = div_rn(et, zt, yt) - div_rn(ed, zd, yd);
+        return d > 0.0 ? q44(d) : 0;
+    }
+};
+
+__device__ __forceinline__ int64_t as_i64(double f) {
+    return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
 template <typename T>
@@ -266,17 +283,20 @@ template <typename T, int NS, int NT, bool DIV>
 __device__ __forceinline__ int64_t row_z(const uint4 (&q)[NS], int nv, float temp, double md, const double* tab) {
     constexpr int VEC = Elt<T>::kVec;
     const int t = threadIdx.x;
-    int64_t z = 0;
+    // whole numbers of at most 2^44 each, at most 128 of them: the double
+    // sum is exact
+    static_assert(NS * VEC <= 128, "exact double sum");
+    double z = 0.0;
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) {
         float x[VEC];
         Elt<T>::widen(q[sl], x);
         if (t + sl * NT < nv) {
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) z += weight<DIV>(x[e], temp, md, tab);
+            for (int e = 0; e < VEC; ++e) z += q44_exp_nonpos_f((double)scaled<DIV>(x[e], temp) - md, tab);
         }
     }
-    return z;
+    return __double_as_longlong(z + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
 // The sequence's statistics, draft tokens and accept uniforms staged in LDS
@@ -372,6 +392,7 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     const tms_spec_stat ds = rej < 0 ? ts : srow[a.k + 1 + rej];
     const float temp = P.temperature;
     const double mt = (double)ts.m, md = (double)ds.m;
+    const Resid res(ts.Z, ds.Z);
     __syncthreads();   // exp table in LDS
     const int lo = p * a.Lp, hi = min(a.V, lo + a.Lp);
     int64_t wsum = 0, tsum = 0;
@@ -463,8 +484,9 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
             er[j] = 0;
             wr[j] = 0;
             if (r_lo + j < r_hi) {
-                er[j] = weight(xt[j], temp, mtu, tab);
-                wr[j] = rej < 0 ? er[j] : residual(er[j], weight(xd[j], temp, md, tab), ts.Z, ds.Z);
+                const double etf = weight_f(xt[j], temp, mtu, tab);
+                er[j] = as_i64(etf);
+                wr[j] = rej < 0 ? er[j] : res(etf, weight_f(xd[j], temp, md, tab));
             }
             tsum += er[j];
             wsum += wr[j];
@@ -474,10 +496,9 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
         wsum = tsum;
     } else {
         for_range2(rt, rd, lo, hi, a.fast, [&](int, float vt, float vd) {
-            const int64_t et = weight(vt, temp, mt, tab);
-            const int64_t ed = weight(vd, temp, md, tab);
-            tsum += et;
-            wsum += residual(et, ed, ts.Z, ds.Z);
+            const double et = weight_f(vt, temp, mt, tab);
+            tsum += as_i64(et);
+            wsum += res(et, weight_f(vd, temp, md, tab));
         });
     }
     wsum = block_sum_i64(wsum, shl);
@@ -583,10 +604,9 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
     const int E = (phi - plo + kBlock - 1) / kBlock;
     const int my_lo = min(phi, plo + t * E), my_hi = min(phi, my_lo + E);
     auto w_at = [&](int id) -> int64_t {
-        const int64_t et = weight(Elt<T>::scalar(rt + id), temp, mt, tab);
-        if (use_t) return et;
-        const int64_t ed = weight(Elt<T>::scalar(rd + id), temp, md, tab);
-        return residual(et, ed, ts.Z, ds.Z);
+        const double et = weight_f(Elt<T>::scalar(rt + id), temp, mt, tab);
+        if (use_t) return as_i64(et);
+        return res(et, weight_f(Elt<T>::scalar(rd + id), temp, md, tab));
     };
     // Runs of up to kRunMax ids: every load issued at once (clamped
     // addresses), the weights kept in registers for the scan and the search;
@@ -613,8 +633,8 @@ __device__ void resolve_part(const SArgs& a, int b, int p, SpecLds& L) {
         for (int j = 0; j < kRunMax; ++j) {
             wc[j] = 0;
             if (my_lo + j < my_hi) {
-                const int64_t et = weight(xt[j], temp, mt, tab);
-                wc[j] = use_t ? et : residual(et, weight(xd[j], temp, md, tab), ts.Z, ds.Z);
+                const double et = weight_f(xt[j], temp, mt, tab);
+                wc[j] = use_t ? as_i64(et) : res(et, weight_f(xd[j], temp, md, tab));
             }
             mine += wc[j];
         }

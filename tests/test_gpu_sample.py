@@ -81,6 +81,30 @@ def test_exp64_device_bitwise_equals_oracle(orc):
     assert np.array_equal(y.view(np.uint64), want.view(np.uint64))
 
 
+def test_reciprocal_division_is_correctly_rounded():
+    """The verify residual divides by a row's Z through its reciprocal and
+    two fma corrections; the quotients equal IEEE division (numpy's a / b)
+    bit for bit: the residual's operands (whole numbers up to 2^44 over Z in
+    [2^44, 2^61)), divisors next to powers of two, and general doubles."""
+    import torch
+
+    from tensormark_amd.sampler import debug_exp
+
+    rng = np.random.default_rng(5)
+    n = 1 << 20
+    a = np.floor(rng.random(n) * 2.0 ** rng.integers(0, 45, n))
+    b = np.floor(2.0 ** rng.uniform(44, 61, n))
+    near = rng.random(n) < 0.25
+    b[near] = 2.0 ** rng.integers(45, 61, int(near.sum())) - rng.integers(1, 1000, int(near.sum())) * 2.0 ** 8
+    g = rng.random(n) < 0.25
+    a[g] = np.exp(rng.uniform(-300, 300, int(g.sum())))
+    b[g] = np.exp(rng.uniform(-300, 300, int(g.sum())))
+    x = np.empty(2 * n)
+    x[0::2], x[1::2] = a, b
+    y = debug_exp(torch.from_numpy(x).to("cuda:0"), 3).cpu().numpy()[:n]
+    assert np.array_equal(y, a / b)
+
+
 def test_q44_weight_fast_path_bitwise_equals_oracle(orc):
     """The verify weight q44(exp64(x)) for x <= 0 through the device's folded
     form equals the oracle's two-step form bit for bit, including the -40
