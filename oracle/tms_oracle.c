@@ -453,7 +453,7 @@ double tmo_exp64(double x) {
     if (isnan(x)) return x;
     if (x < -746.0) return 0.0;
     if (x > 709.782712893384) return INFINITY;
-    const double kd = floor(x * 0x1.71547652b82fep+6 + 0.5);
+    const double kd = nearbyint(x * 0x1.71547652b82fep+6);   /* ties to even */
     double r = fma(-kd, 0x1.62e42fefa39efp-7, x);
     r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
     double p = 1.0 / 120;
@@ -478,9 +478,10 @@ double tmo_exp64(double x) {
     return y * s.d;
 }
 
-/* Weights on a 2^-44 grid: round(y * 2^44), half up. */
+/* Weights on a 2^-44 grid: y * 2^44 rounded to the nearest whole number,
+ * ties to even (one IEEE operation on the device). */
 int64_t tmo_q44(double y) {
-    return (int64_t)floor(y * 17592186044416.0 + 0.5);
+    return (int64_t)nearbyint(y * 17592186044416.0);
 }
 
 /* Softmax weights of one row: lg = v / T, m = max lg,

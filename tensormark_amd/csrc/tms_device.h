@@ -108,7 +108,7 @@ __device__ __forceinline__ double exp64(double x, const double* tab) {
     if (x != x) return x;
     if (x < -746.0) return 0.0;
     if (x > 709.782712893384) return __builtin_huge_val();
-    const double kd = floor(x * 0x1.71547652b82fep+6 + 0.5);
+    const double kd = rint(x * 0x1.71547652b82fep+6);
     double r = fma(-kd, 0x1.62e42fefa39efp-7, x);
     r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
     double p = 1.0 / 120;
@@ -131,12 +131,12 @@ __device__ __forceinline__ double exp64(double x, const double* tab) {
     return y * __longlong_as_double((long long)(m + 1023) << 52);
 }
 
-// y in [0, 1] (a probability): floor(y * 2^44 + 0.5) is a whole number
-// below 2^52, so adding 2^52 holds it exactly in the mantissa, and the
+// y in [0, 1] (a probability): rint(y * 2^44), the nearest multiple of
+// 2^-44 in units of 2^-44 (ties to even), is a whole number below 2^52, so adding 2^52 holds it exactly in the mantissa, and the
 // difference of the bit patterns is that integer (two operations, where a
 // general double -> int64 conversion takes several).
 __device__ __forceinline__ int64_t q44(double y) {
-    const double f = floor(y * 17592186044416.0 + 0.5);
+    const double f = rint(y * 17592186044416.0);
     return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
 }
 
@@ -150,7 +150,7 @@ __device__ __forceinline__ int64_t q44(double y) {
 // one ldexp by m + 44.
 __device__ __forceinline__ double q44_exp_nonpos_f(double x, const double* tab) {
     const double xc = fmax(x, -41.0);
-    const double kd = floor(xc * 0x1.71547652b82fep+6 + 0.5);
+    const double kd = rint(xc * 0x1.71547652b82fep+6);
     double r = fma(-kd, 0x1.62e42fefa39efp-7, xc);
     r = fma(-kd, 0x1.abc9e3b39803fp-62, r);
     double p = 1.0 / 120;
@@ -161,7 +161,7 @@ __device__ __forceinline__ double q44_exp_nonpos_f(double x, const double* tab) 
     p = fma(p, r, 1.0);
     const int ki = (int)kd;
     const double y = tab[ki & 63] * p;
-    return floor(ldexp(y, (ki >> 6) + 44) + 0.5);
+    return rint(ldexp(y, (ki >> 6) + 44));
 }
 
 // a / b correctly rounded, given y = RN(1/b) (one division per divisor in
