@@ -51,6 +51,7 @@ constexpr int kHot = 8;             // lanes a wave examines from LDS (more: eve
 constexpr int kCap = 1024;          // chunk candidates held in LDS
 constexpr int kPad = 256;           // slack after a ranked list (rank_place reads past it)
 constexpr int kList = 128;          // a chunk's candidates published unranked up to this many
+constexpr int kMW = 4;             // waves of the merge after the compaction (one a SIMD)
 static_assert(kLStride >= 1 + kKMax && kLStride >= 1 + kList && kList >= kKMax && kList <= 128, "list layout");
 
 // Header word: ready bit, flags (bits 48-55), list length (bits 32-47),
@@ -805,6 +806,11 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     if (t == 0 && S > 1) st_agent(&a.counters[row * kCounterStride], 0u);
     if (wv < S && lane == 0) sm.mn[wv] = ncc;
     lds_sync();
+    // From here the merge runs on waves 0 .. max(S, 4) - 1 (the list holders
+    // for the compaction, four for the rank), then on waves 0 .. 3: the
+    // others leave, so each instruction of the merge is issued by at most a
+    // wave or so a SIMD instead of four.
+    if (wv >= (S > kMW ? S : kMW)) return;
 
     WTR(7);
     WSTOP(5, (float)(key0 + key1));
@@ -840,7 +846,8 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
             a.out_status[row] = status;
             if (a.out_keep) a.out_keep[row] = 0;
         }
-        for (int i = t; i < a.topk_cap; i += kT) {
+        for (int i = t; i < a.topk_cap; i += kMW * 64) {
+            if (t >= kMW * 64) break;
             if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = -1;
             if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = 0.0f;
         }
@@ -880,11 +887,12 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         }
         WSTOP(51, (float)(b0 + b1));
         lds_sync();
+        if (wv >= kMW) return;
         const int nsurv = sm.nsurv;
         WTR(13);
         WTV(14, nsurv);
         WSTOP(52, (float)nsurv);
-        rank_place<kT>(sm.u.surv, nsurv, K, sm.srt);
+        rank_place<kMW * 64>(sm.u.surv, nsurv, K, sm.srt);
     }
     lds_sync();
     WTR(8);
@@ -898,7 +906,7 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
             a.out_status[row] = TMS_ROW_OK;
             if (a.out_keep) a.out_keep[row] = 0;
         }
-        for (int i = t; i < a.topk_cap; i += kT) {
+        for (int i = t; i < a.topk_cap; i += kMW * 64) {
             if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
             if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
         }
