@@ -133,12 +133,18 @@ struct Smem {
         } m;
     } big;
     uint64_t cand[kCand];
-    uint32_t tkey[kBlock];         // order keys of the thread maxima
-    uint32_t pbits[2 * kBlock];    // per thread: its penalised entries (bit = slot * VEC + e)
+    // One region for two phases (lds_syncs between them): pbits, per thread
+    // its penalised entries (bit = slot * VEC + e), read once after the
+    // window and reused by the merge's buckets; tkey, the order keys of the
+    // thread maxima, during the selection.  Keeping the workgroup's LDS at
+    // most 40 KB lets four workgroups share a CU.
+    union {
+        uint32_t pbits[2 * kBlock];
+        uint32_t tkey[kBlock];
+    };
     int wave_i[kWaves];
     uint64_t wave_k[kWaves];
     float wave_f[kWaves];
-    int list_off[kMaxChunks + 2];
     int list_src[kMaxChunks + 1];
     int list_n[kMaxChunks];        // entries of each chunk list
     int list_s[kMaxChunks];        // survivors of each chunk list
