@@ -582,6 +582,38 @@ def test_topk_kernel_error_rows(sampler, orc):
     assert np.array_equal(out["tokens"].cpu().numpy(), want2["tokens"])
 
 
+def test_wide_kernel_rows_with_a_wide_topk_cap(sampler, orc):
+    """The wide top-k kernel (config 2's shape under the ROWS_TOPK promise)
+    with per-row outputs wider than its merge waves (topk_cap 300 > 256
+    threads): error rows (temperature 0, all masked, NaN) fill every output
+    with -1 / 0, greedy rows put their one id first, sampled rows match the
+    oracle over all 300 entries."""
+    import torch
+
+    from tensormark_amd.sampler import ROWS_TOPK
+
+    rng = np.random.default_rng(31)
+    B, V, cap = 64, 128256, 300
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    x[5, 70000] = np.nan
+    p = params_array(B, temperature=0.8, top_k=40, top_p=0.95, seed=np.arange(B) + 900)
+    p["top_k"] = np.where(np.arange(B) % 3 == 0, 128, 40)
+    p["greedy"] = (np.arange(B) % 8 == 1).astype(np.int32)
+    p["temperature"][2] = 0.0
+    mask = np.full((B, (V + 31) // 32), 0xFFFFFFFF, np.uint32)
+    mask[9] = 0
+    out = sampler.sample(torch.from_numpy(x).to("cuda:0"), p,
+                         mask=torch.from_numpy(mask.view(np.int32)).to("cuda:0"), topk_cap=cap,
+                         row_kinds=ROWS_TOPK)
+    torch.cuda.synchronize()
+    gpu = {k: v.cpu().numpy() for k, v in out.items()}
+    want = orc.sample_batch(x, p, mask=mask, topk_cap=cap)
+    assert gpu["status"][2] == 1 and gpu["status"][9] == 2 and gpu["status"][5] == 3
+    for b in (2, 5, 9):
+        assert (gpu["topk_ids"][b] == -1).all() and (gpu["topk_probs"][b] == 0).all()
+    check(gpu, want, cap)
+
+
 def test_tie_fixture_rows(sampler, orc):
     """Rows full of exact ties (tests/golden/tie_golden.npz): the device gives
     the oracle's lowest-id-first order, keep and draws, in groups of equal
