@@ -132,9 +132,10 @@ __device__ __forceinline__ double exp64(double x, const double* tab) {
 }
 
 // y in [0, 1] (a probability): rint(y * 2^44), the nearest multiple of
-// 2^-44 in units of 2^-44 (ties to even), is a whole number below 2^52, so adding 2^52 holds it exactly in the mantissa, and the
-// difference of the bit patterns is that integer (two operations, where a
-// general double -> int64 conversion takes several).
+// 2^-44 in units of 2^-44 (ties to even), is a whole number below 2^52, so
+// adding 2^52 holds it exactly in the mantissa, and the difference of the
+// bit patterns is that integer (two operations, where a general double ->
+// int64 conversion takes several).
 __device__ __forceinline__ int64_t q44(double y) {
     const double f = rint(y * 17592186044416.0);
     return __double_as_longlong(f + 0x1p52) - __double_as_longlong(0x1p52);
@@ -142,8 +143,8 @@ __device__ __forceinline__ int64_t q44(double y) {
 
 // q44(exp64(x)) for x <= 0, bit-identical to the pair above, as a double
 // holding the whole number (at most 2^44, so sums of up to 128 of them stay
-// exact and below 2^52).  Below -40 the weight is 0: exp64(x) < e^-40 < 2^-57, which rounds
-// to 0 on the 2^-44 grid; the argument is clamped at -41, where the same
+// exact and below 2^52).  Below -40 the weight is 0: exp64(x) < e^-40 <
+// 2^-57, which rounds to 0 on the 2^-44 grid; the argument is clamped at -41, where the same
 // holds, so no select is needed (a NaN clamps to -41 too).  On [-41, 0]
 // exp64 takes none of its special cases (2^m is normal, m >= -60), and its
 // final scaling by 2^m and q44's by 2^44 are both exact, so they fold into
