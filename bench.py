@@ -41,6 +41,7 @@ PEAK_HBM = 8.0e12
 # BASELINE.json's metric is quoted on config 2; the other configs are named the
 # same way for their own shapes.
 METRICS = {
+    1: "sampled rows/sec at B=1, V=32000, fp32 logits (single-row latency)",
     2: "sampled rows/sec and HBM GB/s (% of peak) at B=64, V=128256, fp32 logits",
     3: "sampled rows/sec and HBM GB/s (% of peak) at B=128, V=151936, fp16 logits",
     4: "verified sequences/sec and HBM GB/s (% of peak) at B=32, k=8, V=32000, fp32 logits",
@@ -53,7 +54,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-rotate", action="store_true",
                     help="reuse one input batch (cache-resident after the first launch)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -71,6 +72,11 @@ def parse():
 def workload(cfg):
     from tensormark_amd import workloads
 
+    if cfg == 1:
+        w = workloads.cfg1()
+        bytes_ = w["logits"].nbytes + w["recent"].nbytes
+        return w, "f32", bytes_, ("cfg1: B=1 V=32000 fp32, repetition 1.1/64 + top-k 40 + top-p 0.95, "
+                                  "one row a call")
     if cfg == 2:
         w = workloads.cfg2(with_mask=True)
         B, V = w["logits"].shape
@@ -151,7 +157,11 @@ def cpu_baseline(w, cfg):
     ref = oracle.reference()
     if ref is None:
         return None
-    if cfg == 2:
+    if cfg == 1:
+        x = w["logits"]
+        groups = [(x, dict(recent=w["recent"], window=64, penalty=1.1), (0.8, 40, 0.95, False))]
+        what = "apply_repeat_penalty 1.1/64 -> sample T=0.8 k=40 p=0.95, one row"
+    elif cfg == 2:
         x = w["logits"]
         groups = [(x, dict(recent=w["recent"], window=256, penalty=1.1, mask=w["mask"]),
                    (0.7, 40, 0.95, False))]
@@ -190,9 +200,14 @@ def cpu_baseline(w, cfg):
             return tot
         return run
 
+    if B == 1:
+        threads = 1   # one row: one thread does all of it
     dt, reps = _timed(run_all(threads))
-    dt1 = run_all(1, rows=4)(5)
-    n1 = 4 * len(groups)
+    # the one-thread figure: up to 16 rows of each group, median of enough
+    # passes for about 3 s of work
+    n1 = min(B, 16)
+    dt1, reps1 = _timed(run_all(1, rows=n1), budget=3.0)
+    n1 *= len(groups)
     return {
         "value": round(B / dt, 1),
         "unit": "rows/s",
@@ -203,10 +218,41 @@ def cpu_baseline(w, cfg):
         "nproc": nproc,
         "sample": (f"the reference tmsample.h compiled -O3 ({what}) over the same {B} x {V} rows, "
                    f"rows dealt to {threads} threads (the GPU box's CPU share; nproc {nproc}), "
-                   f"median of {reps} passes; one_core: {n1} rows on 1 thread, median of 5; "
+                   f"median of {reps} passes; one_core: {n1} rows on 1 thread, median of {reps1} passes; "
                    f"{time.perf_counter() - t0:.1f} s wall in all; frequency/presence/min-p are "
                    f"absent from the reference"),
     }
+
+
+def verify(w, cfg, out):
+    """The last timed launch's outputs against the oracle's answer for the
+    same inputs (every row): tokens, keep counts and status (configs 1-3, 5),
+    accepted lengths, tokens and status (config 4).  Returns (ok, note)."""
+    import oracle
+
+    orc = oracle.oracle()
+    got = {k: v.cpu().numpy() for k, v in out.items()}
+    if cfg == 4:
+        tg, dr, tok, prm = w["target"], w["draft"], w["tokens"], w["params"]
+        B, k = tok.shape
+        bad = 0
+        for b in range(B):
+            words = np.array([orc.row_words(int(prm["seed"][b]), int(prm["offset"][b]), i)
+                              for i in range(k + 1)], np.uint32)
+            st, acc, t = orc.spec_verify_seq(tg[b], dr[b], tok[b], float(prm["temperature"][b]), words)
+            bad += int(got["accepted"][b] != acc or got["token"][b] != t or got["status"][b] != st)
+        return bad == 0, f"{B - bad} of {B} sequences equal the oracle's (accepted length, token)"
+    x = w["logits"]
+    if cfg == 3:
+        x = x.astype(np.float32)
+    elif cfg == 5:
+        from tensormark_amd import workloads
+
+        x = workloads.bf16_bits_to_f32(x)
+    want = orc.sample_batch(x, w["params"], recent=w.get("recent"), mask=w.get("mask"))
+    ok = ((got["tokens"] == want["tokens"]) & (got["keep"] == want["keep"]) &
+          (got["status"] == want["status"]))
+    return bool(ok.all()), f"{int(ok.sum())} of {len(ok)} rows equal the oracle's (token, keep, status)"
 
 
 def measure_traffic(args):
@@ -394,6 +440,7 @@ def main():
     rows_per_s = B / (ms * 1e-3)   # config 4: sequences verified per second
     achieved = algo_bytes / (ms * 1e-3)
     cpu = None if args.no_cpu else cpu_baseline(w, args.config)
+    verified, verify_note = (None, "not checked (--no-cpu)") if args.no_cpu else verify(w, args.config, out)
     line = {
         "metric": METRICS[args.config],
         "value": round(rows_per_s, 1),
@@ -421,6 +468,8 @@ def main():
             "traffic_source": traffic_note,
         },
         "cpu_baseline": cpu,
+        "verified": verified,
+        "verify_note": verify_note,
     }
     print(json.dumps(line), flush=True)
     s.close()

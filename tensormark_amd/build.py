@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtmsample_hip.so")
-SOURCES = ["tms_sample.hip", "tms_topk.hip", "tms_wide.hip", "tms_dense.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
+SOURCES = ["tms_sample.hip", "tms_wide.hip", "tms_dense.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
 
 # -ffp-contract=off keeps every a*b+c as two rounded operations, so the
 # device arithmetic matches the host checker bit for bit.  Packed-FP32 ops
@@ -32,12 +32,11 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
 ]
 
-# Per-file flags.  The top-k kernels take their row ticket as soon as the
-# stream is in and use the result only after publishing; the atomic
+# Per-file flags.  The wide top-k kernel takes its row ticket as soon as
+# the stream is in and uses the result only after publishing; the atomic
 # optimizer would rewrite that single-lane atomic into a wave-wide one whose
 # result is broadcast at once, waiting out the round trip there.
 FILE_FLAGS = {
-    "tms_topk.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
     "tms_wide.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
 }
 

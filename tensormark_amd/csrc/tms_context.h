@@ -39,7 +39,7 @@ struct tms_context {
     uint32_t* counters;        // [max_batch][kCounterStride] sampler arrival counters (word 0)
     uint32_t* ones;            // all-ones mask row, for calls without a grammar mask
     uint64_t* lists;           // [max_batch][max_chunks][kListStride] chunk candidate lists
-    uint64_t* tlists;          // [max_batch][min(max_chunks, 16)][1280] top-k kernel lists
+    uint64_t* tlists;          // [max_batch][min(max_chunks, 16)][136] wide top-k kernel lists
     uint32_t* spec_tickets;    // [max_batch][kCounterStride] verify arrival counters (word 0)
     uint64_t* spec_parts;      // [max_batch][kSpecParts][kPartWords] published partial sums
     tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]

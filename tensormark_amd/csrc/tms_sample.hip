@@ -1293,8 +1293,8 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_sp = off_st + nb * tms::kCounterStride * 4;   // one 256-byte line per ticket
     const size_t off_ss = off_sp + nb * tms::kSpecParts * tms::kPartWords * sizeof(uint64_t);
     const size_t off_tl = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
-    const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kLeanMaxChunksHost);
-    const size_t off_dq = off_tl + nb * tl_chunks * tms::kTopkListStride * sizeof(uint64_t);
+    const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kWideMaxChunksHost);
+    const size_t off_dq = off_tl + nb * tl_chunks * tms::kWideListStride * sizeof(uint64_t);
     const size_t off_hn = off_dq + 256 * (((tms::kDenseQueueHead + nb) * sizeof(uint32_t) + 255) / 256);
     const size_t off_hi = off_hn + 256 * ((nb * sizeof(int32_t) + 255) / 256);
     const size_t off_hv = off_hi + nb * tms::kHistMax * sizeof(int32_t);
@@ -1437,10 +1437,8 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
     k.counters = w.counters;
     k.lists = w.lists;
     k.tlists = w.tlists;
-    // The whole-row pass follows any call without the top-k promise, and a
-    // top-k call whose windows can overflow the top-k kernel's penalised-entry
-    // lists (more than kCand window ids).
-    const bool dense_pass = a->row_kinds == TMS_ROWS_ANY || (a->recent && a->recent_stride > tms::kCand);
+    // The whole-row pass follows any call without the top-k promise.
+    const bool dense_pass = a->row_kinds == TMS_ROWS_ANY;
     k.dense = dense_pass ? w.dense : nullptr;
     k.dense_stride = w.max_vocab;
     k.dqueue = w.dqueue;
@@ -1512,25 +1510,10 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
             }
         }
     }
-    if (a->row_kinds == TMS_ROWS_TOPK) {
-        // Every row greedy or top-k <= 128 (the caller's promise): the top-k
-        // kernel, with chunks of CE ids, CE a multiple of 32 so each chunk
-        // starts on a mask word, when the row fits its list staging and the
-        // grid is resident at once.  Its lists carry 3 keys per thread, so a
-        // larger grid (many rows in several waves of workgroups) spends more
-        // on list traffic than the selection it skips: B = 1024, V = 256000
-        // bf16 ran 363 us there against 278 us in the general kernel.
-        const int ce = (per + 31) / 32 * 32;
-        const int s_lean = (a->vocab + ce - 1) / ce;
-        if (s_lean <= tms::kLeanMaxChunksHost && a->batch * s_lean <= tms::kTopkMaxGrid) {
-            tms::KArgs kl = k;
-            kl.CE = ce;
-            kl.S = s_lean;
-            const int rc = tms_launch_topk(kl, a->dtype, fast, a->batch, stream);
-            if (rc != TMS_OK || !dense_pass) return rc;
-            return tms_launch_dense(kl, a->dtype, dense_grid, stream);
-        }
-    }
+    // Everything else, including top-k batches whose grid does not fit the
+    // wide kernel's residency (rows that break the promise then report
+    // TMS_ROW_UNSUPPORTED: no whole-row pass follows a top-k call): the
+    // general kernel.
     const dim3 grid((unsigned)(a->batch * k.S)), block(tms::kBlock);
 #define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F>), grid, block, 0, stream, k)
     switch (a->dtype) {
@@ -1592,7 +1575,7 @@ constexpr size_t align32(size_t words) { return (words + 31) / 32 * 32; }   // u
 constexpr size_t kNaCounters = 0;
 constexpr size_t kNaLists = kNaCounters + align32((size_t)kNoAllocRows * tms::kCounterStride / 2);
 constexpr size_t kNaTlists = kNaLists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kListStride);
-constexpr size_t kNaQueue = kNaTlists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kTopkListStride);
+constexpr size_t kNaQueue = kNaTlists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kWideListStride);
 constexpr size_t kNaHistN = kNaQueue + align32((tms::kDenseQueueHead + kNoAllocRows + 1) / 2);
 constexpr size_t kNaHistIds = kNaHistN + align32(kNoAllocRows / 2);
 constexpr size_t kNaHistVals = kNaHistIds + (size_t)kNoAllocRows * tms::kHistMax / 2;

@@ -43,12 +43,10 @@ constexpr int kListStride = kCand + 2;     // u64 per published list: header + e
 constexpr int kUni = 2048;                 // merge staging (u64)
 constexpr int kToppCap = 1024;             // candidates per top-p row
 constexpr int kMaxChunks = 64;             // chunks per row (vocab <= 1,048,576)
-constexpr int kLeanMaxChunksHost = 16;     // chunks per row of the top-k kernel (vocab <= 262,144)
 constexpr int kWideMaxChunksHost = 16;     // chunks per row of the wide top-k kernel
 constexpr int kWideChunkVecs = 4096;       // 16-byte vectors per chunk of the wide kernel
 constexpr int kWideMaxWindow = 1024;       // history positions the wide kernel holds (one per thread)
-constexpr int kTopkListStride = 1280;      // u64 per (row, chunk) list of the top-k kernel
-constexpr int kTopkMaxGrid = 1024;         // workgroups of a top-k launch (2 per CU resident)
+constexpr int kWideListStride = 136;       // u64 per (row, chunk) list of the wide kernel: header + 128 keys, padded
 constexpr int kRankLists = 16;             // most chunk lists the sampled merge reads in one round
 constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no effect
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
@@ -83,7 +81,7 @@ struct KArgs {
     // workspace
     uint32_t* counters;    // [B] arrival tickets, reset by the merger
     uint64_t* lists;       // [B][S][kListStride]: header, entries; headers reset by the merger
-    uint64_t* tlists;      // [B][S][kTopkListStride]: the top-k kernel's lists, zeroed by the merger
+    uint64_t* tlists;      // [B][S][kWideListStride]: the wide kernel's lists, zeroed by the merger
     uint64_t* dense;       // [B][2 * dense_stride]: the whole-row pass's keys and sums; null when
                            // the call runs no whole-row pass
     int64_t dense_stride;  // >= V
@@ -760,8 +758,6 @@ __device__ __forceinline__ int wave_min_nonneg(int v) {
 
 }  // namespace tms
 
-// Launches the top-k kernel (tms_topk.hip) over `batch` rows.
-int tms_launch_topk(const tms::KArgs& k, int dtype, bool fast, int batch, hipStream_t stream);
 // Launches the wide top-k kernel (tms_wide.hip) over `batch` rows.
 int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream);
 // Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.

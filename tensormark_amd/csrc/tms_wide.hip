@@ -43,7 +43,7 @@ constexpr int kWMax = kTMax / 64;   // waves per workgroup, at most
 constexpr int kWaveSlots = 128;     // waves x slots per thread, at most (32768 ids a chunk in fp32)
 constexpr int kMaxS = kWideMaxChunksHost;
 constexpr int kKMax = kTopkFast;    // largest K
-constexpr int kLStride = 136;       // u64 per (row, chunk) list: header + kKMax keys, padded
+constexpr int kLStride = kWideListStride;   // u64 per (row, chunk) list: header + kKMax keys, padded
 constexpr int kHash = 2048;         // window table slots (at most 1024 ids: half full)
 constexpr int kCntBits = 11;        // occurrence count bits of a table word (<= 1024)
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
@@ -105,20 +105,6 @@ struct Smem {
     int flags;
     int misc[4];
 };
-
-#ifdef TMS_WIDE_STOP
-// Timing builds: the kernel ends after phase n, storing a value that depends
-// on that phase's work so none of it is optimised away.
-#define WSTOP(n, val)                                                                   \
-    do {                                                                                \
-        if (TMS_WIDE_STOP == (n)) {                                                     \
-            if ((val) == 12345.678f) a.out_tokens[row] = 1;                             \
-            return;                                                                     \
-        }                                                                               \
-    } while (0)
-#else
-#define WSTOP(n, val) ((void)0)
-#endif
 
 #ifdef TMS_TRACE
 // Trace builds: lane 0 of every wave stamps the 100 MHz real-time counter at
@@ -534,7 +520,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         ticket = __hip_atomic_fetch_add(&a.counters[row * kCounterStride], 1u, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
     WTR(2);
-    WSTOP(1, m);
     // The widened values are formed again from the raw words where they are
     // used next: holding 32 widened 16-bit values across the bound would
     // take twice the registers of the words.
@@ -559,7 +544,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     }
     const uint64_t nfw = __ballot(nf);
     if (lane == 0) sm.wnf[wv] = nfw ? 1 : 0;
-    WSTOP(11, m);
     lds_sync();
     int flags = 0;
     {
@@ -606,7 +590,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         if (!(own_v < __builtin_huge_valf()) && own_v != NEG_INF) atomicOr(&sm.onf, 1);
     }
     WTR(3);
-    WSTOP(2, okey_inv(tkey));
 
     // ---- select: candidates are the entries at or above vlo, whose
     //      quotient can reach the bound's.
@@ -699,7 +682,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     int ncand = select ? sm.ncand : 0;
     const bool merger = S == 1 || (int)sm.ticket == S - 1;   // the last chunk of the row to arrive
     WTR(4);
-    WSTOP(22, (float)ncand);
     const bool radixed = ncand > kCap;
     if (radixed) {
         // ---- exact radix select (every wave): the chunk's K keys
@@ -799,10 +781,8 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         }
     }
     WTR(5);
-    WSTOP(3, (float)(key0 + key1));
 
     // ================= merge (the last chunk of the row)
-    WSTOP(4, (float)nlist);
     if (t == 0 && S > 1) st_agent(&a.counters[row * kCounterStride], 0u);
     if (wv < S && lane == 0) sm.mn[wv] = ncc;
     lds_sync();
@@ -813,7 +793,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     if (wv >= (S > kMW ? S : kMW)) return;
 
     WTR(7);
-    WSTOP(5, (float)(key0 + key1));
     // the lists' flags, lengths and bounds: lane l reads list l, and wave
     // reductions give each wave the totals and the largest bound
     int fo, ntot;
@@ -885,18 +864,15 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
             if (s0) sm.u.surv[off + r0] = key0;
             if (s1) sm.u.surv[off + __popcll(b0) + r1] = key1;
         }
-        WSTOP(51, (float)(b0 + b1));
         lds_sync();
         if (wv >= kMW) return;
         const int nsurv = sm.nsurv;
         WTR(13);
         WTV(14, nsurv);
-        WSTOP(52, (float)nsurv);
         rank_place<kMW * 64>(sm.u.surv, nsurv, K, sm.srt);
     }
     lds_sync();
     WTR(8);
-    WSTOP(6, (float)sm.srt[0]);
     const int N = min(ntot, K);
 
     if (greedy) {

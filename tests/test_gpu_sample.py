@@ -173,6 +173,32 @@ def test_cfg2_full_size_vs_oracle(sampler, orc, with_mask):
     check(g, want, 40)
 
 
+def test_benched_cfg2_path_vs_oracle(sampler, orc):
+    """The exact call bench.py times: config 2 with its mask, the TOPK row-kind
+    hint, no per-entry outputs (topk_cap 0: the tail decides the top-p cut and
+    the draw from tree sums within a margin), Philox draws from the row
+    parameters.  20 Philox offsets, so 1280 draws go through that tail at the
+    benchmark's shape; tokens, keep counts and status of every row."""
+    import torch
+
+    from tensormark_amd.sampler import ROWS_TOPK, row_kinds_of
+
+    w = workloads.cfg2(with_mask=True)
+    assert row_kinds_of(w["params"]) == ROWS_TOPK
+    x = _dev(w["logits"], torch)
+    rec = _dev(w["recent"].astype(np.int32), torch)
+    mask = _dev(w["mask"].view(np.int32), torch)
+    for off in range(20):
+        p = w["params"].copy()
+        p["offset"] = p["offset"] + off
+        want = orc.sample_batch(w["logits"], p, recent=w["recent"], mask=w["mask"])
+        out = sampler.sample(x, p, recent=rec, mask=mask, row_kinds=ROWS_TOPK)
+        torch.cuda.synchronize()
+        g = {k: v.cpu().numpy() for k, v in out.items()}
+        assert (want["status"] == 0).all()
+        check(g, want)
+
+
 @pytest.mark.parametrize("cap", [64, 0])
 def test_cfg3_full_size_fp16_vs_oracle(sampler, orc, cap):
     """cap 64 returns per-entry probabilities (the sequential top-p tail);
@@ -285,6 +311,15 @@ def test_cfg5_full_workload_vs_oracle(sampler, cfg5_full):
     g = run_gpu(sampler, bits, w["params"], recent=w["recent"], topk_cap=100, dtype="bf16")
     assert (want["status"] == 0).all()
     check(g, want, 100)
+
+
+def test_cfg5_full_workload_benched_path(sampler, cfg5_full):
+    """Config 5 as bench.py runs it: no per-entry outputs (topk_cap 0, the
+    tree-sum tail) and the row-kind hint from the parameters; tokens, keep
+    counts and status of all 1024 rows against the oracle."""
+    bits, w, want = cfg5_full
+    g = run_gpu(sampler, bits, w["params"], recent=w["recent"], topk_cap=0, dtype="bf16")
+    check(g, want)
 
 
 def test_many_draws_same_row(sampler, orc):
@@ -543,11 +578,12 @@ def test_dense_rows_whole_row_pass(sampler, orc, cap):
     check(g, want, cap)
 
 
-def test_topk_kernel_error_rows(sampler, orc):
-    """Rows the top-k kernel must reject like the general kernel: temperature
-    0 (BAD_PARAMS, on a row of ties), an all-masked row (ALL_MASKED), NaN and
-    +inf (NONFINITE); and a top-p row under the ROWS_TOPK promise, which the
-    top-k kernel reports as UNSUPPORTED instead of sampling it."""
+def test_wide_kernel_error_rows(sampler, orc):
+    """Rows the wide top-k kernel must reject like the general kernel:
+    temperature 0 (BAD_PARAMS, on a row of ties), an all-masked row
+    (ALL_MASKED), NaN and +inf (NONFINITE); and a top-p row under the
+    ROWS_TOPK promise, which the wide kernel reports as UNSUPPORTED instead
+    of sampling it."""
     import torch
 
     from tensormark_amd.sampler import ROWS_ANY, ROWS_TOPK
