@@ -107,6 +107,7 @@ public:
         hip(hipMalloc(&d_mask_, sizeof(uint32_t) * words), "hipMalloc");
         hip(hipMalloc(&d_small_, 256), "hipMalloc");
         hip(hipMalloc(&d_breaker_, static_cast<size_t>(max_vocab)), "hipMalloc");
+        hip(hipMalloc(&d_scale_, sizeof(float) * TMS_DRY_MAX_WINDOW), "hipMalloc");
         hip(hipStreamCreate(&stream_), "hipStreamCreate");
         (void)hipSetDevice(prev);
         max_vocab_ = max_vocab;
@@ -116,7 +117,7 @@ public:
         (void)hipGetDevice(&prev);
         (void)hipSetDevice(device_);
         if (stream_) (void)hipStreamDestroy(stream_);
-        for (void* p : {d_logits_, d_recent_, d_mask_, d_small_, d_breaker_})
+        for (void* p : {d_logits_, d_recent_, d_mask_, d_small_, d_breaker_, d_scale_})
             if (p) (void)hipFree(p);
         (void)hipSetDevice(prev);
         if (ctx_) (void)tms_destroy(ctx_);
@@ -142,15 +143,28 @@ public:
     // ceil(V / 32) words, bit id & 31 of word id >> 5) restricts the row
     // first, as GrammarFilter::restrict does (llama_chat.cpp:184-209).  With
     // the ban and DRY off only the repetition window is uploaded; otherwise
-    // the whole history (its last 65535 ids) and the breaker table go up and
-    // the library's history pre-pass runs.  Unlike the reference, `logits`
-    // is left as it was.
+    // the whole history (its last 65535 ids), the breaker table and the DRY
+    // scales (std::pow(base, (float)k), as tmsample.h:168 computes them) go
+    // up and the library's history pre-pass runs; a DRY window longer than
+    // the pre-pass holds (TMS_DRY_MAX_WINDOW) runs the three transforms on
+    // the host instead.  Unlike the reference, `logits` is left as it was.
     [[nodiscard]] int sample_token(std::vector<float>& logits, int V, const ChatOpts& o,
                                    bool greedy, std::mt19937& rng, const int* recent,
                                    int n_recent, const uint32_t* mask = nullptr) {
         tms_row_params p = row_params(o.temperature, o.top_k, o.top_p, greedy);
         p.repeat_penalty = o.repeat_penalty;
         p.repeat_last_n = o.repeat_last_n;
+        const int dry_window = std::min(n_recent, o.dry.penalty_last_n);
+        if (o.dry.multiplier > 0.0f && dry_window > TMS_DRY_MAX_WINDOW) {
+            std::vector<float> row(logits.begin(), logits.begin() + V);
+            if (mask) apply_mask(row, mask);
+            tms_host_repeat_penalty(row.data(), V, recent, n_recent, o.repeat_last_n, o.repeat_penalty);
+            tms_host_no_repeat_ngram(row.data(), V, recent, n_recent, o.no_repeat_ngram);
+            tms_host_dry(row.data(), V, recent, n_recent, o.dry.multiplier, o.dry.base,
+                         o.dry.allowed_length, o.dry.penalty_last_n, o.dry_breaker);
+            p.repeat_penalty = 1.0f;
+            return run_row(row.data(), V, p, nullptr, 0, nullptr, greedy, rng);
+        }
         if (o.no_repeat_ngram >= 2 || o.dry.multiplier > 0.0f) {
             tms_history_params h{};
             h.no_repeat_ngram = o.no_repeat_ngram;
@@ -241,6 +255,16 @@ private:
         if (hist && breaker)
             hip(hipMemcpyAsync(d_breaker_, breaker, static_cast<size_t>(V), hipMemcpyHostToDevice, stream_),
                 "hipMemcpyAsync");
+        // the DRY scales of the reference's arithmetic, one per exponent the
+        // row's window can need
+        int scale_n = 0;
+        if (hist && hist->dry_multiplier > 0.0f) {
+            scale_n = std::max(1, std::min(hist->dry_penalty_last_n, static_cast<int>(TMS_DRY_MAX_WINDOW)));
+            scale_.resize(static_cast<size_t>(scale_n));
+            check(tms_dry_scale_table(hist->dry_base, scale_n, scale_.data()), "tms_dry_scale_table");
+            hip(hipMemcpyAsync(d_scale_, scale_.data(), sizeof(float) * static_cast<size_t>(scale_n),
+                               hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+        }
         hip(hipMemcpyAsync(d, &h, sizeof(h), hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
         tms_sample_args a{};
         a.logits = d_logits_;
@@ -260,6 +284,8 @@ private:
         a.out_keep = &d->keep;
         a.history = hist ? &d->hist : nullptr;
         a.dry_breaker = (hist && breaker) ? static_cast<const uint8_t*>(d_breaker_) : nullptr;
+        a.dry_scale = scale_n ? static_cast<const float*>(d_scale_) : nullptr;
+        a.dry_scale_stride = scale_n;
         // The row is known here: a greedy or top-k <= 128 row may take the
         // library's top-k kernel.
         a.row_kinds = (h.params.greedy != 0 || (h.params.top_k >= 1 && h.params.top_k <= 128))
@@ -291,6 +317,8 @@ private:
     void* d_mask_ = nullptr;
     void* d_small_ = nullptr;
     void* d_breaker_ = nullptr;
+    void* d_scale_ = nullptr;
+    std::vector<float> scale_;
     hipStream_t stream_ = nullptr;
 };
 

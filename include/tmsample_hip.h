@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define TMS_ABI_VERSION 3
+#define TMS_ABI_VERSION 4
 
 /* Return codes of the entry points. */
 enum {
@@ -118,6 +118,9 @@ typedef struct tms_row_params {
 
 /* Most distinct ids the history steps (2, 3, 3a, 3b) of one row may touch. */
 #define TMS_HISTORY_MAX_IDS 4096
+/* Most window positions DRY (step 3b) reads on the device:
+ * min(n_recent, dry_penalty_last_n) above this reports TMS_ROW_UNSUPPORTED. */
+#define TMS_DRY_MAX_WINDOW 8192
 
 /*
  * Per-row n-gram ban and DRY settings (tms_sample_args.history).
@@ -183,6 +186,18 @@ typedef struct tms_sample_args {
     const uint8_t* dry_breaker;          /* device, [vocab], nullable: non-zero marks a
                                             DRY sequence breaker; ids outside
                                             [0, vocab) are not breakers */
+    const float* dry_scale;              /* device, [batch][dry_scale_stride], nullable:
+                                            entry k of row b is the DRY scale base^k as
+                                            the reference's std::pow(base, (float)k)
+                                            gives it (tmsample.h:168), for the row's
+                                            dry_base (tms_dry_scale_table fills one);
+                                            a row whose DRY window needs k >=
+                                            dry_scale_stride reports
+                                            TMS_ROW_UNSUPPORTED.  Null: the library's
+                                            own correctly rounded base^k, which differs
+                                            from glibc's powf by one ulp for about 0.1%
+                                            of (base, k) */
+    int64_t dry_scale_stride;            /* floats per row of dry_scale */
 } tms_sample_args;
 
 typedef struct tms_spec_args {
@@ -279,8 +294,8 @@ int tms_spec_verify(tms_context* ctx, const tms_spec_args* args, hipStream_t str
 /*
  * The history transforms on a host row of V fp32 logits, in place, for
  * host-side callers (the device runs them itself with
- * tms_sample_args.history).  tms_host_dry computes base^k as the device
- * does.
+ * tms_sample_args.history).  tms_host_dry computes base^k as the reference
+ * does, std::pow(base, (float)k) of the host's C library.
  *   tms_host_repeat_penalty   tmsample::apply_repeat_penalty  (tensormark/tmsample.h:52-63)
  *   tms_host_no_repeat_ngram  tmsample::apply_no_repeat_ngram (tensormark/tmsample.h:81-114)
  *   tms_host_dry              tmsample::apply_dry             (tensormark/tmsample.h:148-170),
@@ -294,6 +309,14 @@ void tms_host_no_repeat_ngram(float* logits, int V, const int32_t* recent, int n
 void tms_host_dry(float* logits, int V, const int32_t* recent, int n_recent, float multiplier,
                   float base, int allowed_length, int penalty_last_n,
                   const unsigned char* is_breaker);
+/*
+ * out[k] = std::pow(base, (float)k) for k in [0, n): one row of
+ * tms_sample_args.dry_scale, the scale apply_dry multiplies by
+ * (tensormark/tmsample.h:168), from this host's C library as the
+ * reference's own build computes it.  Returns TMS_ERR_INVALID_ARG for a
+ * null out or n < 0.
+ */
+int tms_dry_scale_table(float base, int n, float* out);
 
 /*
  * Host GBNF engine: the producer of the grammar bitmask.  Replaces

@@ -8,7 +8,8 @@
 //   the repetition penalty              (tmsample.h:52-63),
 //   the frequency/presence penalty,
 //   the no-repeat n-gram ban            (tmsample.h:81-114),
-//   DRY                                 (tmsample.h:148-170),
+//   DRY                                 (tmsample.h:148-170, with the caller's
+//                                        table of the reference's powf values),
 // and the general sampling kernel and the whole-row pass then take those
 // values in place of the logits of those ids (the window machinery they use
 // for the repetition penalty, fed with the list instead of the history).
@@ -22,6 +23,14 @@
 // applied in the reference's position order.  The list goes to the
 // workspace: ov_n[row] (-1 when the row touches more than kHistMax ids),
 // ov_ids[row][e], ov_vals[row][e].
+//
+// DRY's match lengths come from the window staged in LDS (reversed, so the
+// run ending at position i against the tail is the common prefix of r and
+// r[last - i ..]): every position compares up to kDryDirect ids directly,
+// in parallel; when some position reaches that many, one wave computes
+// every length again with the Z-function (linear in the window: each
+// extension step compares 64 ids by ballot), so a repetitive window costs
+// O(n) and not O(n^2).
 //
 // The n-gram ban's restore rule (the banned ids get their values back when
 // nothing above -inf is left) needs the row's maximum outside the list:
@@ -39,6 +48,9 @@ constexpr int kHSlots = 2 * kHistMax;
 constexpr uint32_t kHCount = 0xFFFFu;     // window count
 constexpr uint32_t kHDry = 1u << 30;      // a DRY target
 constexpr uint32_t kHBan = 1u << 31;      // banned by the n-gram rule
+constexpr int kDryMax = TMS_DRY_MAX_WINDOW;   // DRY window positions held in LDS
+constexpr int kDryDirect = 64;            // ids a position compares before the Z-function pass
+static_assert(kDryMax <= 2 * kHistMax, "the staged window lies over the table's keys");
 
 struct HistArgs {
     const void* logits;
@@ -52,19 +64,23 @@ struct HistArgs {
     int64_t recent_stride;
     const uint32_t* mask;      // never null (the all-ones row)
     int64_t mask_stride;
+    const float* dry_scale;    // [B][dry_scale_stride] or null
+    int64_t dry_scale_stride;
     int32_t* ov_n;             // [B]
     int32_t* ov_ids;           // [B][kHistMax]
     float* ov_vals;            // [B][kHistMax]
 };
 
 struct HistLds {
-    uint32_t key[kHSlots];     // id + 1; 0 = empty
+    uint32_t key[kHSlots];     // id + 1; 0 = empty (before the table: DRY's staged window)
     uint32_t info[kHSlots];    // kHCount | kHDry | kHBan
     uint16_t ent[kHSlots];     // the slot's entry
     uint16_t eslot[kHistMax];  // the entry's slot
     float val[kHistMax];
     int32_t tslot[kHBlock];    // DRY: one tile of target slots, in position order
     int32_t tk[kHBlock];       //      and their exponents L - allowed_length
+    uint16_t dlen[kDryMax];    // DRY: the match length at each window position
+    uint32_t dbrk[kDryMax / 32];   // DRY: staged window positions holding a breaker
     int wave_i[kHBlock / 64];
     int flag;                  // overflow
     int found;
@@ -131,16 +147,62 @@ __device__ __forceinline__ bool is_breaker(const uint8_t* brk, int V, int id) {
     return brk && id >= 0 && id < V && brk[id] != 0;
 }
 
-// DRY match length at window position i (tmsample.h:159-163): how far the
-// runs ending at i and at `last` agree, never across a breaker.
-__device__ __forceinline__ int dry_run(const int32_t* w, int i, int last, const uint8_t* brk, int V) {
-    int L = 0;
-    while (L <= i) {
-        const int a = w[i - L], b = w[last - L];
-        if (a != b || is_breaker(brk, V, a) || is_breaker(brk, V, b)) break;
-        ++L;
+// DRY match lengths (tmsample.h:159-163) of every window position i <
+// last = dn - 1: how far the runs ending at i and at last agree, never
+// across a breaker.  r[j] is the window's id at last - j (staged in the
+// table's key array), bit j of dbrk marks a breaker there; the length at i
+// is the common prefix of r and r[last - i ..], which stops at the window's
+// start (position d + k <= last).  Lengths go to L.dlen[i].
+__device__ __forceinline__ bool dry_eq(const int32_t* r, const uint32_t* brk, int a, int b) {
+    return r[a] == r[b] && !((brk[a >> 5] >> (a & 31)) & 1u) && !((brk[b >> 5] >> (b & 31)) & 1u);
+}
+
+__device__ void dry_lengths(const int32_t* dw, int dn, const uint8_t* breaker, int V, HistLds& L) {
+    const int t = threadIdx.x, lane = t & 63;
+    const int last = dn - 1;
+    int32_t* r = (int32_t*)L.key;
+    for (int i = t; i < kDryMax / 32; i += kHBlock) L.dbrk[i] = 0u;
+    __syncthreads();
+    for (int j = t; j < dn; j += kHBlock) {
+        const int id = dw[last - j];
+        r[j] = id;
+        if (is_breaker(breaker, V, id)) atomicOr(&L.dbrk[j >> 5], 1u << (j & 31));
     }
-    return L;
+    __syncthreads();
+    int over = 0;
+    for (int i = t; i < last; i += kHBlock) {
+        const int d = last - i;
+        int k = 0;
+        while (k < kDryDirect && d + k < dn && dry_eq(r, L.dbrk, k, d + k)) ++k;
+        over |= k == kDryDirect ? 1 : 0;
+        L.dlen[i] = (uint16_t)k;
+    }
+    if (!block_or(over, L)) return;
+    // Z-function over r, one wave: z(d) = common prefix of r and r[d ..],
+    // kept at dlen[last - d]; [lo, hi) is the rightmost match found so far.
+    if (t < 64) {
+        int lo = 0, hi = 0;
+        for (int d = 1; d < dn; ++d) {
+            int k = d < hi ? min(hi - d, (int)L.dlen[last - (d - lo)]) : 0;
+            if (d + k >= hi) {
+                for (;;) {
+                    const int b = d + k + lane;
+                    const bool eq = b < dn && dry_eq(r, L.dbrk, k + lane, b);
+                    const uint64_t ne = __ballot(!eq);
+                    if (ne) {
+                        k += __ffsll((unsigned long long)ne) - 1;
+                        break;
+                    }
+                    k += 64;
+                }
+                lo = d;
+                hi = d + k;
+            }
+            if (lane == 0) L.dlen[last - d] = (uint16_t)k;
+            wave_lds_sync();
+        }
+    }
+    __syncthreads();
 }
 
 template <typename T>
@@ -155,6 +217,21 @@ __global__ __launch_bounds__(kHBlock) void history_kernel(HistArgs a) {
     const int32_t* rec = a.recent + (int64_t)row * a.recent_stride;
     const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
     const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
+
+    // ---- DRY's window and every position's match length, first: the
+    //      window is staged over the table's keys, which are cleared after
+    const bool dry_on = H.dry_multiplier > 0.0f && H.dry_allowed_length >= 1 &&
+                        nrec >= H.dry_allowed_length + 1 &&
+                        min(nrec, H.dry_penalty_last_n) >= H.dry_allowed_length + 1;
+    const int dn = dry_on ? min(nrec, H.dry_penalty_last_n) : 0;
+    const int32_t* dw = rec + (nrec - dn);
+    const int dlast = dn - 1;
+    // every exponent L - allowed_length is below dn - allowed_length
+    if (dry_on && (dn > kDryMax || (a.dry_scale && a.dry_scale_stride < dn - H.dry_allowed_length))) {
+        if (t == 0) a.ov_n[row] = -1;   // the row reports TMS_ROW_UNSUPPORTED
+        return;
+    }
+    if (dry_on) dry_lengths(dw, dn, a.breaker, V, L);
 
     {
         uint4* k4 = (uint4*)L.key;
@@ -208,15 +285,9 @@ __global__ __launch_bounds__(kHBlock) void history_kernel(HistArgs a) {
     }
 
     // ---- DRY targets (tmsample.h:150-169)
-    const bool dry_on = H.dry_multiplier > 0.0f && H.dry_allowed_length >= 1 &&
-                        nrec >= H.dry_allowed_length + 1 &&
-                        min(nrec, H.dry_penalty_last_n) >= H.dry_allowed_length + 1;
-    const int dn = dry_on ? min(nrec, H.dry_penalty_last_n) : 0;
-    const int32_t* dw = rec + (nrec - dn);
-    const int dlast = dn - 1;
     if (dry_on) {
         for (int i = t; i < dlast; i += kHBlock) {
-            if (dry_run(dw, i, dlast, a.breaker, V) < H.dry_allowed_length) continue;
+            if (L.dlen[i] < H.dry_allowed_length) continue;
             const int id = dw[i + 1];
             if (id < 0 || id >= V || is_breaker(a.breaker, V, id)) continue;
             const int s = hinsert(L, id);
@@ -301,11 +372,12 @@ __global__ __launch_bounds__(kHBlock) void history_kernel(HistArgs a) {
     //      target entry subtracts its hits in that order.
     if (dry_on) {
         const float mult = H.dry_multiplier, dbase = H.dry_base;
+        const float* scale = a.dry_scale ? a.dry_scale + (int64_t)row * a.dry_scale_stride : nullptr;
         for (int i0 = 0; i0 < dlast; i0 += kHBlock) {
             const int i = i0 + t;
             int slot = -1, k = 0;
             if (i < dlast) {
-                const int Lr = dry_run(dw, i, dlast, a.breaker, V);
+                const int Lr = L.dlen[i];
                 if (Lr >= H.dry_allowed_length) {
                     const int id = dw[i + 1];
                     if (id >= 0 && id < V && !is_breaker(a.breaker, V, id)) {
@@ -327,7 +399,8 @@ __global__ __launch_bounds__(kHBlock) void history_kernel(HistArgs a) {
                     if (!(L.info[s] & kHDry)) continue;
                     float v = L.val[q];
                     for (int j = 0; j < nh; ++j)
-                        if (L.tslot[j] == s) v -= mult * tms_dry_scale(dbase, L.tk[j]);
+                        if (L.tslot[j] == s)
+                            v -= mult * (scale ? scale[L.tk[j]] : tms_dry_scale(dbase, L.tk[j]));
                     L.val[q] = v;
                 }
             }
@@ -348,8 +421,8 @@ __global__ __launch_bounds__(kHBlock) void history_kernel(HistArgs a) {
 }  // namespace tms
 
 int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,
-                       int dtype, int batch, int32_t* ov_n, int32_t* ov_ids, float* ov_vals,
-                       hipStream_t stream) {
+                       const float* dry_scale, int64_t dry_scale_stride, int dtype, int batch,
+                       int32_t* ov_n, int32_t* ov_ids, float* ov_vals, hipStream_t stream) {
     tms::HistArgs h;
     h.logits = k.logits;
     h.row_stride = k.row_stride;
@@ -362,6 +435,8 @@ int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const 
     h.recent_stride = k.recent_stride;
     h.mask = k.mask;
     h.mask_stride = k.mask_stride;
+    h.dry_scale = dry_scale;
+    h.dry_scale_stride = dry_scale_stride;
     h.ov_n = ov_n;
     h.ov_ids = ov_ids;
     h.ov_vals = ov_vals;

@@ -11,11 +11,11 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <utility>
 #include <vector>
 
 #include "../../include/tmsample_hip.h"
-#include "tms_history.h"
 
 // tensormark/tmsample.h:52-63: v > 0 ? v / p : v * p, once per occurrence.
 extern "C" void tms_host_repeat_penalty(float* logits, int V, const int32_t* recent, int n_recent,
@@ -95,6 +95,12 @@ extern "C" void tms_host_dry(float* logits, int V, const int32_t* recent, int n_
         if (L < allowed_length) continue;
         const int32_t next = w[i + 1];
         if (next < 0 || next >= V || breaker(next)) continue;
-        logits[next] -= multiplier * tms_dry_scale(base, L - allowed_length);
+        logits[next] -= multiplier * std::pow(base, (float)(L - allowed_length));
     }
+}
+
+extern "C" int tms_dry_scale_table(float base, int n, float* out) {
+    if (!out || n < 0) return TMS_ERR_INVALID_ARG;
+    for (int k = 0; k < n; ++k) out[k] = std::pow(base, (float)k);
+    return TMS_OK;
 }

@@ -1450,8 +1450,9 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
         // The history pre-pass lists every row's touched ids with their
         // final values; the general kernel and the whole-row pass take the
         // list as the window (tms_hist.hip).
-        const int rc = tms_launch_history(k, a->history, a->dry_breaker, a->dtype, a->batch, w.ov_n,
-                                          w.ov_ids, w.ov_vals, stream);
+        if (a->dry_scale && a->dry_scale_stride <= 0) return TMS_ERR_INVALID_ARG;
+        const int rc = tms_launch_history(k, a->history, a->dry_breaker, a->dry_scale, a->dry_scale_stride,
+                                          a->dtype, a->batch, w.ov_n, w.ov_ids, w.ov_vals, stream);
         if (rc != TMS_OK) return rc;
         k.recent = w.ov_ids;
         k.n_recent = w.ov_n;

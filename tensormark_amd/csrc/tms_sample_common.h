@@ -763,5 +763,5 @@ int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int sl
 // Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.
 int tms_launch_dense(const tms::KArgs& k, int dtype, int workgroups, hipStream_t stream);
 int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,
-                       int dtype, int batch, int32_t* ov_n, int32_t* ov_ids, float* ov_vals,
-                       hipStream_t stream);
+                       const float* dry_scale, int64_t dry_scale_stride, int dtype, int batch,
+                       int32_t* ov_n, int32_t* ov_ids, float* ov_vals, hipStream_t stream);

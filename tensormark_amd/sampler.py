@@ -44,6 +44,7 @@ EXPORTS = (
     "tms_host_repeat_penalty",
     "tms_host_no_repeat_ngram",
     "tms_host_dry",
+    "tms_dry_scale_table",
     "tms_grammar_parse",
     "tms_grammar_free",
     "tms_grammar_rule_count",
@@ -129,6 +130,7 @@ HISTORY_DTYPE = np.dtype(
     ]
 )
 HISTORY_MAX_IDS = 4096   # TMS_HISTORY_MAX_IDS
+DRY_MAX_WINDOW = 8192    # TMS_DRY_MAX_WINDOW
 
 
 def make_history(B: int, *, no_repeat_ngram=0, dry_multiplier=0.0, dry_base=1.75,
@@ -143,6 +145,23 @@ def make_history(B: int, *, no_repeat_ngram=0, dry_multiplier=0.0, dry_base=1.75
     h["dry_allowed_length"] = dry_allowed_length
     h["dry_penalty_last_n"] = dry_penalty_last_n
     return h
+
+
+def dry_scale_table(history: np.ndarray) -> np.ndarray:
+    """[B, n] float32 of tms_sample_args.dry_scale for a HISTORY_DTYPE array:
+    row b holds std::pow(dry_base_b, (float)k) for k < n, from this host's C
+    library through tms_dry_scale_table (the reference's own arithmetic,
+    tensormark/tmsample.h:168); n covers every row's DRY window."""
+    lib = load_library()
+    h = np.asarray(history, HISTORY_DTYPE)
+    n = int(min(max(1, int(np.max(h["dry_penalty_last_n"], initial=1))), DRY_MAX_WINDOW))
+    out = np.zeros((len(h), n), np.float32)
+    for b in range(len(h)):
+        if h["dry_multiplier"][b] > 0.0:
+            _check(lib.tms_dry_scale_table(C.c_float(float(h["dry_base"][b])), n,
+                                           out[b].ctypes.data_as(C.POINTER(C.c_float))),
+                   "tms_dry_scale_table")
+    return out
 
 
 @dataclasses.dataclass
@@ -184,6 +203,7 @@ class SampleArgs(C.Structure):
         ("out_keep", C.c_void_p), ("out_topk_ids", C.c_void_p), ("out_topk_probs", C.c_void_p),
         ("row_kinds", C.c_uint32), ("reserved", C.c_uint32),
         ("history", C.c_void_p), ("dry_breaker", C.c_void_p),
+        ("dry_scale", C.c_void_p), ("dry_scale_stride", C.c_int64),
     ]
 
 
@@ -229,6 +249,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         fp, ip = C.POINTER(C.c_float), C.POINTER(C.c_int32)
         lib.tms_host_repeat_penalty.argtypes = [fp, C.c_int, ip, C.c_int, C.c_int, C.c_float]
         lib.tms_host_no_repeat_ngram.argtypes = [fp, C.c_int, ip, C.c_int, C.c_int]
+        lib.tms_dry_scale_table.argtypes = [C.c_float, C.c_int, fp]
         lib.tms_host_dry.argtypes = [fp, C.c_int, ip, C.c_int, C.c_float, C.c_float, C.c_int,
                                      C.c_int, C.c_void_p]
         for f in (lib.tms_host_repeat_penalty, lib.tms_host_no_repeat_ngram, lib.tms_host_dry):
@@ -373,7 +394,7 @@ class Sampler:
 
     def sample(self, logits, params, *, recent=None, n_recent=None, mask=None, draws=None,
                topk_cap: int = 0, out=None, stream=None, row_kinds=None, noalloc=False,
-               history=None, dry_breaker=None):
+               history=None, dry_breaker=None, dry_scale=None):
         """Sample one token per row of ``logits`` ([B, V] fp32/fp16/bf16, cuda).
 
         ``params`` is a device uint8 tensor from params_tensor() (or a numpy
@@ -385,7 +406,10 @@ class Sampler:
         workspace) instead of this context's.  ``history`` (a
         HISTORY_DTYPE array from make_history, or a device uint8 tensor of
         one) turns on the n-gram ban and DRY, with ``dry_breaker`` an
-        optional device uint8 [V] breaker table.  Returns a dict of device
+        optional device uint8 [V] breaker table and ``dry_scale`` the
+        [B, n] table of DRY scales (dry_scale_table(); built here from a
+        numpy ``history`` when not given; pass False for the library's own
+        correctly rounded powers).  Returns a dict of device
         tensors: tokens, status, keep, and topk_ids/topk_probs when
         topk_cap > 0.
         """
@@ -396,6 +420,13 @@ class Sampler:
                 row_kinds = row_kinds_of(params)
         if isinstance(params, np.ndarray):
             params = self.params_tensor(params)
+        if isinstance(history, np.ndarray) and dry_scale is None:
+            dry_scale = dry_scale_table(history)
+        if dry_scale is False:
+            dry_scale = None
+        if isinstance(dry_scale, np.ndarray):
+            dry_scale = torch.from_numpy(np.ascontiguousarray(dry_scale, np.float32)).to(
+                f"cuda:{self.device}")
         if isinstance(history, np.ndarray):
             raw = np.ascontiguousarray(history, HISTORY_DTYPE).view(np.uint8)
             history = torch.from_numpy(raw.copy()).to(f"cuda:{self.device}")
@@ -414,6 +445,8 @@ class Sampler:
                            draws=draws, topk_cap=topk_cap, out=out, row_kinds=row_kinds)
         a.history = _ptr(history)
         a.dry_breaker = _ptr(dry_breaker)
+        a.dry_scale = _ptr(dry_scale)
+        a.dry_scale_stride = dry_scale.shape[1] if dry_scale is not None else 0
         s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
         if noalloc:
             _check(self.lib.tms_sample_batch_noalloc(C.byref(a), C.c_void_p(s)),

@@ -34,8 +34,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_sizes():
     lib = sampler.load_library()
-    assert lib.tms_abi_version() == 3
-    assert ctypes.sizeof(sampler.SampleArgs) == 152
+    assert lib.tms_abi_version() == 4
+    assert ctypes.sizeof(sampler.SampleArgs) == 168
     assert ctypes.sizeof(sampler.RowParams) == 56
     assert sampler.HISTORY_DTYPE.itemsize == 24
     assert lib.tms_status_string(-2).decode().startswith("batch")

@@ -5,11 +5,12 @@ penalty, frequency/presence, apply_no_repeat_ngram, apply_dry, sample).
 Tokens, keep counts and top-k ids bit-exact; top-k probabilities within
 1e-6 relative.
 
-DRY's base^k is correctly rounded on the device and glibc's powf in the
-oracle; they differ by 1 ulp for about 0.1% of (base, k).  The cases here use
-bases and run lengths where the two agree (base 2.0 is exact, 1.5 agrees for
-every k <= 1000, 1.75 below k = 83); the CPU test
-test_history.py::test_dry_scale_against_glibc_powf states the bound."""
+DRY's scale base^k comes from the caller's table of the reference's powf
+values (Sampler.sample builds it with tms_dry_scale_table); without a table
+the device uses its own correctly rounded power, which is one ulp off glibc's
+powf at (1.75, 83), (1.1, 56) and (1.1, 294) among the pairs sampled
+(test_history.py).  test_dry_scale_table_decides_ties pins both forms at
+exactly those pairs."""
 from __future__ import annotations
 
 import numpy as np
@@ -23,7 +24,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(sampler, x, p, *, recent, n_recent=None, mask=None, history=None, breaker=None,
-         topk_cap=0, dtype="f32", noalloc=False):
+         topk_cap=0, dtype="f32", noalloc=False, dry_scale=None):
     import torch
 
     if dtype == "f32":
@@ -36,7 +37,7 @@ def _run(sampler, x, p, *, recent, n_recent=None, mask=None, history=None, break
     out = sampler.sample(t, p, recent=dev(recent, np.int32), n_recent=dev(n_recent, np.int32),
                          mask=None if mask is None else dev(mask.astype(np.uint32).view(np.int32), np.int32),
                          topk_cap=topk_cap, history=history, dry_breaker=dev(breaker, np.uint8),
-                         noalloc=noalloc)
+                         noalloc=noalloc, dry_scale=dry_scale)
     torch.cuda.synchronize()
     return {k: v.cpu().numpy() for k, v in out.items()}
 
@@ -225,3 +226,114 @@ def test_history_without_ngram_or_dry_equals_plain(sampler, orc):
     a = _run(sampler, w["logits"], w["params"], recent=w["recent"], history=h, topk_cap=40)
     want = orc.sample_batch(w["logits"], w["params"], recent=w["recent"], topk_cap=40)
     check(a, want, 40)
+
+
+def _ties_at(pairs, allowed=2):
+    """Two greedy rows per (base, k): the history `1 t 2 t` (t = k + allowed
+    distinct ids) gives id 2 exactly one DRY hit of length k + allowed, so
+    its logit 0 becomes -(2^-60 * s), s = powf(base, k) as the reference
+    computes it; a twin id holds exactly that value, below id 2 (id 0) in
+    one row and above it (id 400) in the other.  Equal values go to the
+    lower id, so the reference answers 0 and then 2, and a scale one ulp
+    off either way changes one of the two answers."""
+    from tensormark_amd.sampler import dry_scale_table
+
+    V = 512
+    B = 2 * len(pairs)
+    n = max(2 * (k + allowed) + 2 for _, k in pairs)
+    x = np.full((B, V), -1e30, np.float32)
+    recent = np.zeros((B, n), np.int32)
+    n_recent = np.zeros(B, np.int32)
+    h = make_history(B, dry_multiplier=2.0 ** -60, dry_allowed_length=allowed, dry_penalty_last_n=n)
+    for i, (base, k) in enumerate(pairs):
+        L = k + allowed
+        t = np.arange(10, 10 + L, dtype=np.int32)
+        hist = np.concatenate([[1], t, [2], t]).astype(np.int32)
+        s = dry_scale_table(make_history(1, dry_multiplier=1.0, dry_base=base, dry_penalty_last_n=k + 1))[0][k]
+        v = np.float32(0.0) - np.float32(2.0 ** -60) * s
+        for j, twin in ((2 * i, 0), (2 * i + 1, 400)):
+            recent[j, : hist.size] = hist
+            n_recent[j] = hist.size
+            h["dry_base"][j] = base
+            x[j, 2] = 0.0
+            x[j, twin] = v
+    p = params_array(B, temperature=1.0, top_k=40, top_p=1.0, seed=np.arange(B))
+    p["greedy"] = 1
+    return x, p, recent, n_recent, h
+
+
+# where glibc's powf and the correctly rounded power differ, and pairs where they agree
+POWF_DIFFER = [(1.75, 83), (1.1, 56), (1.1, 294)]
+POWF_AGREE = [(1.75, 82), (1.5, 40), (2.0, 100)]
+
+
+def test_dry_scale_table_decides_ties(sampler, orc):
+    """With the table the device reproduces the reference's scale bit for
+    bit (the oracle applies the reference's powf): every twin row answers as
+    the oracle does, 0 then 2."""
+    x, p, recent, n_recent, h = _ties_at(POWF_DIFFER + POWF_AGREE)
+    want = orc.sample_batch(x, p, recent=recent, n_recent=n_recent, history=h)
+    assert list(want["tokens"]) == [0, 2] * (len(want["tokens"]) // 2)
+    g = _run(sampler, x, p, recent=recent, n_recent=n_recent, history=h)
+    check(g, want)
+
+
+def test_dry_without_table_is_the_correctly_rounded_power(sampler):
+    """Without a table the device's own power is the correctly rounded one:
+    at the pairs where glibc's powf is one ulp off, one twin row of each pair
+    changes its answer in the direction the exact power gives; where they
+    agree both rows keep the reference's answers."""
+    from fractions import Fraction
+
+    from tests.test_history import _round_f32
+
+    pairs = POWF_DIFFER + POWF_AGREE
+    x, p, recent, n_recent, h = _ties_at(pairs)
+    g = _run(sampler, x, p, recent=recent, n_recent=n_recent, history=h, dry_scale=False)
+    assert (g["status"] == 0).all()
+    for i, (base, k) in enumerate(pairs):
+        cr = _round_f32(Fraction(float(np.float32(base))) ** k)
+        ref = x[2 * i, 0] / np.float32(-(2.0 ** -60))   # the table's value
+        if cr > ref:     # a larger penalty: id 2 falls below its twins
+            want = [0, 400]
+        elif cr < ref:   # smaller: id 2 rises above them
+            want = [2, 2]
+        else:
+            want = [0, 2]
+        assert list(g["tokens"][2 * i: 2 * i + 2]) == want, (base, k, cr, ref)
+
+
+def test_dry_long_repetitive_windows(sampler, orc):
+    """Windows of TMS_DRY_MAX_WINDOW ids that repeat one id, or a period of 2
+    or 5: every position matches far back, so the pre-pass takes its linear
+    Z-function pass; the rows match the oracle, and one call stays well
+    under a second.  A DRY window longer than the bound reports
+    TMS_ROW_UNSUPPORTED."""
+    import time
+
+    import torch
+
+    from tensormark_amd.sampler import DRY_MAX_WINDOW
+
+    rng = np.random.default_rng(41)
+    B, V, n = 4, 30000, DRY_MAX_WINDOW
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = np.zeros((B, n + 10), np.int32)
+    recent[0, :n] = 7
+    recent[1, :n] = np.resize([11, 12], n)
+    recent[2, :n] = np.resize([20, 21, 22, 23, 24], n)
+    recent[3] = 5
+    n_recent = np.array([n, n, n, n + 10], np.int32)
+    x[:, :30] += 9.0
+    p = params_array(B, temperature=0.9, top_k=40, top_p=0.95, seed=np.arange(B) + 3)
+    h = make_history(B, dry_multiplier=0.01, dry_base=1.001, dry_allowed_length=2,
+                     dry_penalty_last_n=n + 10)
+    want = orc.sample_batch(x, p, recent=recent, n_recent=n_recent, history=h, topk_cap=8)
+    _run(sampler, x, p, recent=recent, n_recent=n_recent, history=h, topk_cap=8)   # warm
+    t0 = time.perf_counter()
+    g = _run(sampler, x, p, recent=recent, n_recent=n_recent, history=h, topk_cap=8)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    assert dt < 1.0, dt
+    assert g["status"][3] == 4 and g["tokens"][3] == -1
+    check(g, want, 8, rows=[0, 1, 2])
