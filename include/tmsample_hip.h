@@ -441,9 +441,13 @@ int tms_filter_stall(const tms_filter* f);
  *   tms_mask_pipe_acquire  waits for the workers; makes `stream` wait for the
  *                          upload; *words = device [batch][n_words]; allowed
  *                          (nullable) = ids per row (0: failed open, -1: no
- *                          filter)
- *   tms_mask_pipe_release  after enqueueing the launches that read the words
- *                          on `stream`
+ *                          filter).  TMS_ERR_INVALID_ARG while an earlier
+ *                          step's words are still acquired and not released
+ *   tms_mask_pipe_release  after enqueueing the launches that read the acquired
+ *                          words on `stream` (the next step may be submitted
+ *                          already); TMS_ERR_INVALID_ARG with nothing acquired.
+ *                          A submit whose slot still holds acquired, unreleased
+ *                          words returns TMS_ERR_INVALID_ARG
  */
 typedef struct tms_mask_pipe tms_mask_pipe;
 tms_mask_pipe* tms_mask_pipe_create(int device, int batch, int n_words, int threads);

@@ -94,7 +94,11 @@ __global__ void xcc_of(int* ids) {
 //            had finished;
 // counts[3]: workgroups w of a 64-workgroup grid not on XCD w mod (XCD
 //            count), the placement the sampler's row mapping assumes;
-// counts[4]: the XCD count seen.  Synchronous; `trials` of each.
+// counts[4]: the XCD count seen;
+// counts[5]: trials of (a) and (b) not run because no workgroup of a grid
+//            landed on an XCD a role needs (the reader's result keeps its
+//            sentinel); they count as neither stale nor lost.
+// Synchronous; `trials` of each.
 extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
     if (!counts || trials <= 0) return TMS_ERR_INVALID_ARG;
     constexpr int kGrid = 64;
@@ -120,7 +124,8 @@ extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
             rc = TMS_ERR_HIP;
         for (int i = 0; i < kGrid; ++i) nx = std::max(nx, hid[i] + 1);
     }
-    int stale = 0, lost = 0, overlap = 0, placed = 0;
+    int stale = 0, lost = 0, overlap = 0, placed = 0, not_run = 0;
+    constexpr uint64_t kSentinel = ~0ull;   // `out` before a read: no reader ran
     if (rc == TMS_OK) {
         for (int i = 0; i < kGrid; ++i) placed += hid[i] != i % nx;
         const int b = nx > 1 ? 1 : 0, c2 = nx > 2 ? 2 : 0;
@@ -132,18 +137,22 @@ extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
             (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
             hipLaunchKernelGGL(tms::line_write, dim3(kGrid), dim3(64), 0, s, line, (uint64_t)it, 0, 0, claim);
             (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            (void)hipMemsetAsync(out, 0xFF, 8, s);
             hipLaunchKernelGGL(tms::line_read, dim3(kGrid), dim3(64), 0, s, line, b, claim, out);
             if (hipMemcpyAsync(&sum, out, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
                 hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
-            stale += sum != 16ull * (uint64_t)it;
+            if (sum == kSentinel) ++not_run;
+            else stale += sum != 16ull * (uint64_t)it;
             // (b) XCDs 0 and b write alternate words in one kernel; XCD c2 reads
             (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
             hipLaunchKernelGGL(tms::line_write, dim3(kGrid), dim3(64), 0, s, line, (uint64_t)it + 1000000, 0, b, claim);
             (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            (void)hipMemsetAsync(out, 0xFF, 8, s);
             hipLaunchKernelGGL(tms::line_read, dim3(kGrid), dim3(64), 0, s, line, c2, claim, out);
             if (hipMemcpyAsync(&sum, out, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
                 hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
-            lost += sum != 16ull * ((uint64_t)it + 1000000);
+            if (sum == kSentinel) ++not_run;
+            else lost += sum != 16ull * ((uint64_t)it + 1000000);
         }
         // (c) back-to-back kernels
         if (rc == TMS_OK) {
@@ -163,6 +172,7 @@ extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
     counts[2] = overlap;
     counts[3] = placed;
     counts[4] = nx;
+    counts[5] = not_run;
     if (s) (void)hipStreamDestroy(s);
     for (void* q : {(void*)line, (void*)out, (void*)claim, (void*)ids, (void*)bad, (void*)ctr})
         if (q) (void)hipFree(q);

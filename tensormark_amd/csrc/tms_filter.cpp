@@ -319,6 +319,7 @@ struct tms_mask_pipe {
     int pending = 0;
     bool stop = false;
     int slot = 0;          // slot being produced / last produced
+    int acquired = -1;     // slot handed out by acquire and not yet released
     bool in_flight = false;
     int rc = TMS_OK;
 
@@ -361,8 +362,13 @@ struct tms_mask_pipe {
     // slot two steps ago is done with it.
     void finish(int s) {
         int r = TMS_OK;
+        bool wait_consumed;
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            wait_consumed = consumed_valid[s];
+        }
         if (hipSetDevice(device) != hipSuccess) r = TMS_ERR_HIP;
-        if (r == TMS_OK && consumed_valid[s] && hipStreamWaitEvent(copy, consumed[s], 0) != hipSuccess)
+        if (r == TMS_OK && wait_consumed && hipStreamWaitEvent(copy, consumed[s], 0) != hipSuccess)
             r = TMS_ERR_HIP;
         if (r == TMS_OK && hipMemcpyAsync(dev[s], host[s], bytes, hipMemcpyHostToDevice, copy) != hipSuccess)
             r = TMS_ERR_HIP;
@@ -445,6 +451,7 @@ extern "C" int tms_mask_pipe_submit(tms_mask_pipe* p, const int32_t* tokens) {
     std::unique_lock<std::mutex> lk(p->mu);
     if (p->in_flight) return TMS_ERR_INVALID_ARG;   // acquire the previous step first
     const int s = p->slot ^ 1;
+    if (p->acquired == s) return TMS_ERR_INVALID_ARG;   // release the step that slot holds first
     lk.unlock();
     // the staging slot is free once its previous upload has finished
     if (p->copied_valid[s] && hipEventSynchronize(p->copied[s]) != hipSuccess) return TMS_ERR_HIP;
@@ -483,19 +490,25 @@ extern "C" int tms_mask_pipe_acquire(tms_mask_pipe* p, hipStream_t stream, const
     p->cv_done.wait(lk, [&] { return !p->in_flight; });
     if (p->rc != TMS_OK || !p->copied_valid[p->slot]) return p->rc != TMS_OK ? p->rc : TMS_ERR_INVALID_ARG;
     const int s = p->slot;
+    if (p->acquired >= 0 && p->acquired != s) return TMS_ERR_INVALID_ARG;   // the other slot is still held
     if (hipStreamWaitEvent(stream, p->copied[s], 0) != hipSuccess) return TMS_ERR_HIP;
+    p->acquired = s;
     *words = p->dev[s];
     if (allowed) memcpy(allowed, p->counts.data(), sizeof(int32_t) * (size_t)p->batch);
     return TMS_OK;
 }
 
 // After enqueueing the launches that read the acquired words on `stream`:
-// the slot is refilled only after `stream` has passed this point.
+// the slot acquire handed out is refilled only after `stream` has passed
+// this point.  The next step may already be submitted (it fills the other
+// slot); a release with no acquire outstanding is an error.
 extern "C" int tms_mask_pipe_release(tms_mask_pipe* p, hipStream_t stream) {
     if (!p) return TMS_ERR_INVALID_ARG;
     std::lock_guard<std::mutex> lk(p->mu);
-    const int s = p->slot;
+    const int s = p->acquired;
+    if (s < 0) return TMS_ERR_INVALID_ARG;
     if (hipEventRecord(p->consumed[s], stream) != hipSuccess) return TMS_ERR_HIP;
     p->consumed_valid[s] = true;
+    p->acquired = -1;
     return TMS_OK;
 }

@@ -110,6 +110,36 @@ def _decode(sampler, mode, steps=48, B=8, seed=3):
     return np.array(out_tokens), t, done, narrowed
 
 
+def test_mask_pipe_acquire_release_order(dev_sampler):
+    """release needs an acquire; words stay held until released, so acquiring
+    the next step, or submitting the one after it into the held slot, is
+    refused; the next step may be submitted while the current one is held."""
+    import torch
+
+    from tensormark_amd.grammar import MaskPipe
+
+    stream = torch.cuda.current_stream().cuda_stream
+    pipe = MaskPipe(4, 1000, threads=1)
+    with pytest.raises(RuntimeError):
+        pipe.release(stream)             # nothing acquired
+    pipe.submit(None)
+    pipe.acquire(stream)                 # step 0 held (slot A)
+    pipe.submit(None)                    # step 1 fills slot B: allowed
+    with pytest.raises(RuntimeError):
+        pipe.acquire(stream)             # step 1 while step 0 is held
+    with pytest.raises(RuntimeError):
+        pipe.submit(None)                # step 2 would refill slot A, still held
+    pipe.release(stream)                 # step 0 done
+    pipe.acquire(stream)                 # step 1 (slot B)
+    pipe.release(stream)
+    with pytest.raises(RuntimeError):
+        pipe.release(stream)             # released twice
+    pipe.submit(None)                    # step 2 (slot A): allowed now
+    pipe.acquire(stream)
+    pipe.release(stream)
+    pipe.close()
+
+
 def test_mask_pipe_matches_synchronous_masks(dev_sampler):
     sync, t, done_s, narrowed = _decode(dev_sampler, "sync")
     piped, _, done_p, _ = _decode(dev_sampler, "pipe")

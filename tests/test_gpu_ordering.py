@@ -5,9 +5,10 @@ tms_debug_ordering runs writer/reader kernel pairs with the writer and reader
 workgroups on different XCDs (each XCD has its own L2) and counts violations:
 a reader kernel that sees a value older than the previous kernel's store, a
 store to one word of a 128-byte line that loses another workgroup's store to a
-neighbouring word, two kernels on one stream whose executions overlap, and
-workgroups not placed round-robin over the XCDs (the blockIdx -> XCD mapping
-the launches are shaped for)."""
+neighbouring word, and two kernels on one stream whose executions overlap.
+It also reports the XCD count and whether workgroups land round-robin over
+the XCDs: the launches are shaped for that placement, but it only decides
+their speed, so it is reported, not asserted."""
 from __future__ import annotations
 
 import ctypes as C
@@ -29,13 +30,15 @@ def test_device_ordering_facts():
     counts = (C.c_int32 * 8)()
     rc = lib.tms_debug_ordering(64, counts)
     assert rc == 0, lib.tms_status_string(rc)
-    stale, lost, overlap, misplaced, xcds = list(counts)[:5]
-    print(f"ordering: stale={stale} lost={lost} overlap={overlap} misplaced={misplaced} xcds={xcds}")
-    assert xcds == 8
+    stale, lost, overlap, misplaced, xcds, not_run = list(counts)[:6]
+    print(f"ordering: stale={stale} lost={lost} overlap={overlap} misplaced={misplaced} xcds={xcds} "
+          f"not_run={not_run}")
+    if xcds < 3:
+        pytest.skip(f"{xcds} XCD(s): the cross-XCD cases need three")
+    assert not_run < 2 * 64, "no trial found its XCD roles"
     assert stale == 0
     assert lost == 0
     assert overlap == 0
-    assert misplaced == 0
 
 
 def test_workspace_reset_then_sample(sampler, orc):
