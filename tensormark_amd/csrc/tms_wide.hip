@@ -10,9 +10,10 @@
 //
 //   window    while the stream is in flight: the row's history ids that fall
 //             in the chunk go into an LDS bitmap and a hash table; the first
-//             position holding an id owns it and counts its occurrences.  The
-//             stream leaves those ids out; after the bound the owners bring
-//             them back penalised (tmsample.h:52-63 compounding, then
+//             position holding an id owns it, counts its occurrences and
+//             loads the id's logit and mask word itself.  The stream leaves
+//             those ids out; after the bound the owners bring them back
+//             penalised (tmsample.h:52-63 compounding, then
 //             frequency/presence).
 //   pass 1    per 16-byte slot: mask bit (and not a window id) -> value,
 //             else -inf; the thread's maximum; NaN / +inf flagged.
@@ -75,7 +76,6 @@ __device__ int32_t kNoHistory[1] = {-1};
 struct Smem {
     uint32_t wbits[1024];           // window ids of the chunk, one bit per id (<= 32768 ids)
     uint32_t wtab[kHash];           // window ids: chunk offset << kCntBits | occurrences, or kEmpty
-    float wval[kHash];              // each window id's masked value
     alignas(16) union {
         struct {
             uint64_t cand[kCap + kPad];     // the chunk's candidates: value bits << 32 | id, then keys
@@ -108,17 +108,17 @@ struct Smem {
 
 #ifdef TMS_TRACE
 // Trace builds: lane 0 of every wave stamps the 100 MHz real-time counter at
-// phase boundaries, 16 slots per wave.
+// phase boundaries, 32 slots per wave.
 #define WTR(i)                                                                          \
     do {                                                                                \
         if ((threadIdx.x & 63) == 0 && a.trace)                                         \
-            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 16 + (i)] =                \
+            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 32 + (i)] =                \
                 __builtin_amdgcn_s_memrealtime();                                       \
     } while (0)
 #define WTV(i, val)                                                                     \
     do {                                                                                \
         if ((threadIdx.x & 63) == 0 && a.trace)                                         \
-            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 16 + (i)] = (uint64_t)(val); \
+            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 32 + (i)] = (uint64_t)(val); \
     } while (0)
 #else
 #define WTR(i) ((void)0)
@@ -325,22 +325,6 @@ __device__ __forceinline__ uint4 fold_bits(const uint4& q, uint32_t bits) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// The window ids of a slot (bits wb, chunk offsets off + e): each value, as
-// folded by the mask, goes to its table entry, and the entry becomes -inf in
-// the slot.
-template <typename T>
-__device__ void window_out(uint4& q, uint32_t wb, int off, Smem& sm) {
-    constexpr int VEC = Elt<T>::kVec;
-    for (uint32_t b = wb; b; b &= b - 1u) {
-        const int e = __builtin_ctz(b);
-        const uint32_t oe = (uint32_t)(off + e);
-        int sl = hash_slot(oe);
-        for (int probe = 0; probe < kHash && (sm.wtab[sl] >> kCntBits) != oe; ++probe)
-            sl = (sl + 1) & (kHash - 1);
-        sm.wval[sl] = elt<T>(q, e);
-    }
-    q = fold_bits<T>(q, ~wb & ((1u << VEC) - 1u));
-}
 
 // NT threads of kSlots 16-byte slots each: (1024, 4) two workgroups per
 // CU; (1024, 8), fp32, one workgroup per CU.
@@ -465,6 +449,11 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         atomicAdd(&sm.wtab[sl], 1u);
         wslot = sl;
     }
+    // The owner's own copy of its id's masked logit, loaded now and used
+    // after the bound: the streaming thread only takes the id out of the
+    // stream, with no table lookup on its path.
+    float own_x = NEG_INF;
+    if (owner && ((mrow[wid_raw >> 5] >> (wid_raw & 31)) & 1u)) own_x = Elt<T>::scalar(base + wid_raw);
     WTR(1);
 
     // ---- pass 1, per slot as it lands: the mask folded into the words (an
@@ -486,8 +475,8 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
             m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(elt<T>(raw[j], e), elt<T>(raw[j], e + 1)));
     }
     lds_sync();   // the window table is complete
-    // ---- window ids out of the stream: the (masked) value of each goes to
-    //      its table entry and the entry becomes -inf in place; the few
+    // ---- window ids out of the stream: each becomes -inf in place (its
+    //      owner forms the penalised value from its own load); the few
     //      threads holding one form their maximum again.
     if (pn.on) {
         bool again = false;
@@ -499,7 +488,7 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
             const uint32_t wb = (sm.wbits[off >> 5] >> (off & 31)) & vmask;
             if (wb) {   // rare
                 again = true;
-                window_out<T>(raw[j], wb, off, sm);
+                raw[j] = fold_bits<T>(raw[j], ~wb & ((1u << VEC) - 1u));
             }
         }
         if (again) {
@@ -586,7 +575,7 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     // entries already meet
     float own_v = NEG_INF;
     if (owner) {
-        own_v = apply_pen(sm.wval[wslot], sm.wtab[wslot] & ((1u << kCntBits) - 1u), pn);
+        own_v = apply_pen(own_x, sm.wtab[wslot] & ((1u << kCntBits) - 1u), pn);
         if (!(own_v < __builtin_huge_valf()) && own_v != NEG_INF) atomicOr(&sm.onf, 1);
     }
     WTR(3);
