@@ -115,6 +115,14 @@ struct Smem {
             a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 32 + (i)] =                \
                 __builtin_amdgcn_s_memrealtime();                                       \
     } while (0)
+// A stamp that waits for `dep` (a value computed from the stream), so the
+// compiler cannot move it ahead of the data it follows.
+#define WTRD(i, dep)                                                                    \
+    do {                                                                                \
+        if ((threadIdx.x & 63) == 0 && a.trace && __float_as_uint(dep) != 0x7FC0ABCDu)     \
+            a.trace[(blockIdx.x * kWMax + (threadIdx.x >> 6)) * 32 + (i)] =                \
+                __builtin_amdgcn_s_memrealtime();                                       \
+    } while (0)
 #define WTV(i, val)                                                                     \
     do {                                                                                \
         if ((threadIdx.x & 63) == 0 && a.trace)                                         \
@@ -122,6 +130,7 @@ struct Smem {
     } while (0)
 #else
 #define WTR(i) ((void)0)
+#define WTRD(i, dep) ((void)0)
 #define WTV(i, val) ((void)0)
 #endif
 
@@ -241,6 +250,38 @@ __device__ __forceinline__ void rank_place(const uint64_t* keys, int n, int K, u
             out[cnt] = k;
             if (gout) st_agent(&gout[cnt], k);
         }
+    }
+}
+
+// Every thread of the first ceil(n / 64) waves of NT: key t of keys[0..n)
+// (distinct, 16-byte aligned) lands at out[rank] when its rank (the number
+// of larger keys) is below K.  Each lane scans the whole list at addresses
+// common to the wave (broadcast reads), eight keys a step into eight
+// independent counts, so the compares do not wait on one another.
+template <int NT>
+__device__ __forceinline__ void rank_scan(const uint64_t* keys, int n, int K, uint64_t* out) {
+    const int t = threadIdx.x;
+    const ulonglong2* k2 = (const ulonglong2*)keys;
+    for (int base = 0; base < n; base += NT) {
+        const int i = base + t;
+        if (base + (t & ~63) >= n) break;   // whole waves past the list
+        const uint64_t x = i < n ? keys[i] : ~0ull;
+        int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        const int n8 = n >> 3;
+#pragma unroll 1
+        for (int q = 0; q < n8; ++q) {
+            ulonglong2 y[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) y[u] = k2[4 * q + u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                c[2 * u] += y[u].x > x ? 1 : 0;
+                c[2 * u + 1] += y[u].y > x ? 1 : 0;
+            }
+        }
+        for (int j = n8 * 8; j < n; ++j) c[j & 7] += keys[j] > x ? 1 : 0;
+        const int r = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[4] + c[5]) + (c[6] + c[7]));
+        if (i < n && r < K) out[r] = x;
     }
 }
 
@@ -474,6 +515,7 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         for (int e = 0; e < VEC; e += 2)
             m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(elt<T>(raw[j], e), elt<T>(raw[j], e + 1)));
     }
+    WTRD(16, m);
     lds_sync();   // the window table is complete
     // ---- window ids out of the stream: each becomes -inf in place (its
     //      owner forms the penalised value from its own load); the few
@@ -499,6 +541,7 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
                 for (int e = 0; e < VEC; ++e) m = __builtin_elementwise_maximum(m, elt<T>(raw[j], e));
         }
     }
+    WTRD(17, m);
     const bool nf = !(m < __builtin_huge_valf()) && m != NEG_INF;   // NaN or +inf
     // The row's ticket, now that the chunk's data is in: its round trip
     // overlaps the selection.  The last chunk of the row to get here merges;
@@ -590,10 +633,16 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     const float tau = okey_inv(tkey);
     float vlo = tau;
     if (divide && tau != NEG_INF) {
-        const double lo = (double)tau - (fabs((double)tau) * 0x1p-19 + (double)temp * 0x1p-140);
-        float f = (float)lo;
-        if ((double)f > lo) f = float_below(f);
-        vlo = f;
+        if (fabsf(tau) >= temp * 0x1p-100f) {
+            // normal quotients: tau - |tau| 2^-18 rounds to at most
+            // tau (1 - 2^-19)
+            vlo = tau - fabsf(tau) * 0x1p-18f;
+        } else {
+            const double lo = (double)tau - (fabs((double)tau) * 0x1p-19 + (double)temp * 0x1p-140);
+            float f = (float)lo;
+            if ((double)f > lo) f = float_below(f);
+            vlo = f;
+        }
     }
     vlo = fmaxf(vlo, -FLT_MAX);
     auto key_of = [&](float v, uint32_t id) { return ckey(divide ? v / temp : v, id); };
