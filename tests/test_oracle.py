@@ -360,3 +360,58 @@ def test_tie_order_brute_force_tiny(orc):
                 w0, w1 = words_for((lo + cp[j]) / 2.0)
                 t = orc.sample_batch(x[None], p, draws=np.array([[w0, w1]], np.uint32))["tokens"][0]
                 assert t == want[j], (row, k, j)
+
+
+@pytest.mark.parametrize("V,k,seed", [(2, 1, 21), (3, 2, 22), (4, 3, 23), (5, 3, 24), (5, 2, 25)])
+def test_spec_every_position_follows_the_target(orc, V, k, seed):
+    """Speculative sampling's defining property at every position, including
+    the bonus: with each draft token drawn from the draft distribution, the
+    token emitted at position i (the accepted draft, or the residual draw at
+    the first rejection, or the bonus draw after k acceptances) is
+    distributed as the target row i, given that position i is reached; and
+    position i + 1 is reached with probability sum_x min(p_t(x), p_d(x)).
+    The probabilities are the oracle's own weights (its q44 grid, so the
+    checks are exact in expectation); Monte Carlo over 40,000 sequences,
+    V <= 5, k <= 3, some target and draft entries -inf."""
+    rng = np.random.default_rng(seed)
+    t = rng.normal(0, 1.5, (k + 1, V)).astype(np.float32)
+    d = (t[:k] + rng.normal(0, 1.0, (k, V))).astype(np.float32)
+    t[0, V - 1] = -np.inf            # a token the target never emits at position 0
+    d[k - 1, 0] = -np.inf            # one the draft never proposes at position k - 1
+    T = float(rng.choice([0.7, 1.0, 1.3]))
+    pt, pd = [], []
+    for i in range(k + 1):
+        st, e, Z, _ = orc.spec_weights(t[i], T)
+        assert st == 0
+        pt.append(e / Z)
+    for i in range(k):
+        st, e, Z, _ = orc.spec_weights(d[i], T)
+        assert st == 0
+        pd.append(e / Z)
+    n = 40000
+    emitted = np.zeros((k + 1, V))   # token counts at each position reached
+    reached = np.zeros(k + 2)
+    cpd = [np.cumsum(p) for p in pd]
+    for _ in range(n):
+        xs = np.array([min(int(np.searchsorted(c, rng.random(), side="right")), V - 1) for c in cpd], np.int32)
+        words = rng.integers(0, 2**32, (k + 1) * 2).astype(np.uint32)
+        st, acc, tok = orc.spec_verify_seq(t, d, xs, T, words)
+        assert st == 0 and 0 <= acc <= k
+        for i in range(acc):
+            reached[i] += 1
+            emitted[i, xs[i]] += 1
+        reached[acc] += 1
+        emitted[acc, tok] += 1
+    for i in range(k + 1):
+        if reached[i] < 2000:
+            continue
+        f = emitted[i] / reached[i]
+        tol = 4.5 * np.sqrt(pt[i] * (1 - pt[i]) / reached[i]) + 2e-3
+        assert np.all(np.abs(f - pt[i]) <= tol), (i, f, pt[i])
+        assert emitted[i][pt[i] == 0].sum() == 0, i   # never emits a token of target weight 0
+    # the chance of moving past each drafted position
+    p_reach = 1.0
+    for i in range(k):
+        p_reach *= float(np.minimum(pt[i], pd[i]).sum())
+        want = n * p_reach
+        assert abs(reached[i + 1] - want) <= 4.5 * np.sqrt(want) + 20, (i, reached[i + 1], want)
