@@ -74,8 +74,8 @@ enum {
     TMS_ROW_ALL_MASKED = 2,   /* every id is -inf after mask and penalties */
     TMS_ROW_NONFINITE = 3,    /* NaN or +inf after masking, or lg overflowed */
     TMS_ROW_UNSUPPORTED = 4,  /* a row that breaks the TMS_ROWS_TOPK promise (top_k = 0
-                                 or > 128, not greedy) in a call that runs no whole-row
-                                 pass; or, with `history`, a row whose history touches
+                                 or > 128, not greedy) in a call the top-k kernel
+                                 takes; or, with `history`, a row whose history touches
                                  more than TMS_HISTORY_MAX_IDS distinct ids */
     TMS_ROW_INTERNAL = 5      /* a chunk list never arrived (bounded wait expired) */
 };
@@ -169,13 +169,13 @@ typedef struct tms_sample_args {
     uint32_t row_kinds;       /* TMS_ROWS_ANY, or TMS_ROWS_TOPK: the caller promises
                                  every row is greedy or has 1 <= top_k <= 128, and
                                  the library may take its top-k kernel (it does when
-                                 batch x chunks <= 1024 workgroups).  TMS_ROWS_ANY
-                                 calls (and TMS_ROWS_TOPK calls with recent_stride >
-                                 512) are followed by a second launch, the whole-row
-                                 pass, that samples every row the chunked kernel
-                                 could not finish (top-p rows with more than 1024
-                                 entries within 40 of the maximum, draws past those
-                                 entries); without that pass a row that breaks the
+                                 batch x chunks <= 1024 workgroups).  Every other
+                                 call takes the general kernel, whose row mergers
+                                 sample whole any row the candidate lists cannot
+                                 finish (top-p rows with more than 1024 entries
+                                 within 40 of the maximum, draws past those
+                                 entries, rows that break the promise) in the same
+                                 launch.  In the top-k kernel a row that breaks the
                                  promise gets TMS_ROW_UNSUPPORTED, never a wrong
                                  sample */
     uint32_t reserved;        /* must be 0 */
@@ -242,7 +242,7 @@ size_t tms_workspace_bytes(const tms_context* ctx);
 /*
  * Zero the words of the workspace that the calls' cross-workgroup protocols
  * expect at zero between calls (arrival counters and tickets, list and part
- * words, the whole-row queue), stream-ordered.  The calls leave them at zero
+ * words, the whole-row region locks), stream-ordered.  The calls leave them at zero
  * themselves; a row that reports TMS_ROW_INTERNAL (a bounded wait ran out)
  * may leave late words behind, so a caller that sees that status calls this
  * before the next call on the context.  ctx == NULL resets the current

@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtmsample_hip.so")
-SOURCES = ["tms_sample.hip", "tms_wide.hip", "tms_dense.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
+SOURCES = ["tms_sample.hip", "tms_wide.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
 
 # -ffp-contract=off keeps every a*b+c as two rounded operations, so the
 # device arithmetic matches the host checker bit for bit.  Packed-FP32 ops
@@ -76,6 +76,21 @@ def _check_no_scratch(src: str, remarks: str) -> None:
         raise RuntimeError(f"{src}: a kernel uses scratch memory ({sizes}); it must fit its register limit")
 
 
+# Largest LDS a kernel of the file may take.  Four general-kernel
+# workgroups share a CU's 160 KiB of LDS; a few hundred bytes more (a
+# runtime helper's LDS word, say) would leave three and add a round of
+# residency to a 1,280-workgroup grid.
+LDS_MAX = {"tms_sample.hip": 40960}
+
+
+def _check_lds(src: str, remarks: str) -> None:
+    sizes = [int(x) for x in re.findall(r"LDS Size \[bytes/block\]: (\d+)", remarks)]
+    if not sizes:
+        raise RuntimeError(f"{src}: no kernel resource report from hipcc")
+    if max(sizes) > LDS_MAX[src]:
+        raise RuntimeError(f"{src}: a kernel takes {max(sizes)} bytes of LDS, above {LDS_MAX[src]}")
+
+
 def build(verbose: bool = False) -> str:
     """Compiles every source to an object (in parallel), then links the library."""
     os.makedirs(BUILD_DIR, exist_ok=True)
@@ -92,6 +107,8 @@ def build(verbose: bool = False) -> str:
     for (src, _, _), rem in zip(jobs, remarks):
         if src in NO_SCRATCH:
             _check_no_scratch(src, rem)
+        if src in LDS_MAX:
+            _check_lds(src, rem)
     _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", LIB + ".tmp", *[j[1] for j in jobs]], verbose)
     os.replace(LIB + ".tmp", LIB)
     return LIB

@@ -43,12 +43,12 @@ struct tms_context {
     uint32_t* spec_tickets;    // [max_batch][kCounterStride] verify arrival counters (word 0)
     uint64_t* spec_parts;      // [max_batch][kSpecParts][kPartWords] published partial sums
     tms_spec_stat* spec_stats; // [max_batch][2 * kSpecMaxK + 1]
-    uint32_t* dqueue;          // whole-row pass queue: 3 counters, then [max_batch] rows
+    uint32_t* dlocks;          // [dense_slots] whole-row region locks
     int32_t* ov_n;             // [max_batch] history pre-pass: list lengths (-1: overflow)
     int32_t* ov_ids;           // [max_batch][TMS_HISTORY_MAX_IDS] listed ids
     float* ov_vals;            // [max_batch][TMS_HISTORY_MAX_IDS] their final values
-    uint64_t* dense;           // [dense_slots][2 * max_vocab] the whole-row pass (separate allocation)
-    int dense_slots;           // min(max_batch, kDenseGridMax): one region per pass workgroup
+    uint64_t* dense;           // [dense_slots][2 * max_vocab] the whole-row path (separate allocation)
+    int dense_slots;           // min(max_batch, kDenseSlotsMax) regions, each taken by a lock
     size_t dense_bytes;
 };
 

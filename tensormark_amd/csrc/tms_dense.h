@@ -5,9 +5,10 @@
 // capacity, a draw that lands past the last significant entry, and rows that
 // break the top-k kernel's row-kind hint.
 //
-// The row's merger queues the row; a second launch (tms_dense.hip) then
-// samples every queued row with one workgroup of 256 threads, over that
-// workgroup's region of the context's workspace (2 x vocab 64-bit words):
+// The row's merger samples such a row itself, right where it finds it needs
+// the whole row (no second launch): 256 threads of its workgroup, over a
+// region of the context's workspace (2 x vocab 64-bit words) taken by a
+// lock (dense_inline):
 //
 //   1. window counts per id (global atomics into the second half);
 //   2. the row maximum of lg = penalised value / T;
@@ -40,6 +41,7 @@ struct DenseLds {
     double wave_d[kWaves];
     int wave_i[kWaves];
     float wave_f[kWaves];
+    int wave_any[kWaves];
     int misc[8];
 };
 
@@ -149,7 +151,12 @@ __device__ __forceinline__ uint64_t* dense_sort(uint64_t* src, uint64_t* dst, in
         int start = inc - tot;
 #pragma unroll
         for (int q = 0; q < kWaves; ++q) start += q < w ? L.wave_i[q] : 0;
-        const bool one_digit = __syncthreads_or(tot == n);
+        const bool any = __any(tot == n);
+        if (lane == 0) L.wave_any[w] = any;
+        dense_sync();
+        bool one_digit = false;
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) one_digit |= L.wave_any[q] != 0;
         if (one_digit) continue;   // every key has this digit: order unchanged
         uint32_t b = (uint32_t)start;
 #pragma unroll
@@ -460,6 +467,53 @@ __device__ __forceinline__ void dense_row(const KArgs& a, int row, tms_row_param
         }
         return;
     }
+}
+
+// A region of the workspace for the whole-row path: slot row mod n first,
+// then the next ones, each taken by an agent-scope compare-and-swap on its
+// lock word (0 free, 1 taken).  A slot is held only by a workgroup already
+// running the path, which frees it when done, so the wait ends; it is still
+// bounded (-1: none taken).
+__device__ __forceinline__ int take_dense_slot(uint32_t* locks, int n, int row) {
+    int s = row % n;
+    for (int spins = 0; spins < kPollCap; ++spins) {
+        uint32_t expect = 0u;
+        if (__hip_atomic_compare_exchange_strong(&locks[s], &expect, 1u, __ATOMIC_ACQUIRE, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+            return s;
+        s = s + 1 == n ? 0 : s + 1;
+        if (s == row % n) __builtin_amdgcn_s_sleep(8);   // a full round without a free slot
+    }
+    return -1;
+}
+
+// The whole-row path for row `row`, run by the first 256 threads of the
+// calling workgroup (every one of them calls it, and no other thread of the
+// workgroup is left waiting at a barrier), its LDS in L: a region of the
+// workspace is taken, the row sampled by dense_row, the region freed (a
+// release store, after every store of the path).  Without a region the row
+// reports TMS_ROW_UNSUPPORTED.
+template <typename T>
+__device__ void dense_inline(const KArgs& a, int row, DenseLds& L) {
+    if (!a.dense) {
+        write_row_error(a, row, TMS_ROW_UNSUPPORTED);
+        return;
+    }
+    if (threadIdx.x == 0) L.misc[7] = take_dense_slot(a.dlocks, a.dense_slots, row);
+    dense_sync();
+    const int slot = L.misc[7];
+    dense_sync();
+    if (slot < 0) {
+        write_row_error(a, row, TMS_ROW_INTERNAL);
+        return;
+    }
+    const tms_row_params P = a.params[row];
+    const int V = a.V;
+    const int K = (P.top_k <= 0 || P.top_k > V) ? V : P.top_k;
+    dense_row<T>(a, row, P, K, a.dense + (int64_t)slot * 2 * a.dense_stride, L);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    dense_sync();
+    if (threadIdx.x == 0) __hip_atomic_store(&a.dlocks[slot], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace tms

@@ -10,7 +10,7 @@
 //   the no-repeat n-gram ban            (tmsample.h:81-114),
 //   DRY                                 (tmsample.h:148-170, with the caller's
 //                                        table of the reference's powf values),
-// and the general sampling kernel and the whole-row pass then take those
+// and the general sampling kernel and its whole-row path then take those
 // values in place of the logits of those ids (the window machinery they use
 // for the repetition penalty, fed with the list instead of the history).
 // Every other id keeps its masked logit, which is what the reference's

@@ -20,7 +20,7 @@
 //   top-p   K > kTopkFast (top_k = 0 or large): every chunk entry whose
 //           probability can change the fp64 sums, i.e. v / T within 40 of
 //           the chunk maximum (exp(-40) < 2^-57); rows past the capacity
-//           go to the whole-row pass (tms_dense.hip).
+//           are sampled whole by their merger (tms_dense.h).
 //
 // Timeline of a workgroup: the stream's loads are the kernel's first
 // instructions and are issued unconditionally (clamped addresses, an all-ones
@@ -85,7 +85,8 @@ __device__ __forceinline__ void rank_all(const uint64_t* keys, int n, uint64_t* 
 // only.  A few barriers and a handful of reads a key, where binary searches
 // over sorted lists cost dependent reads at conflicting addresses.  keys is
 // reordered; cnt holds kBuckets ints of scratch.  Correct for any keys;
-// massive ties (one bucket holding most keys) only cost time.
+// massive ties (one bucket holding most keys) only cost time.  Keys equal
+// to 0 (never a real key) are absent: unranked and not counted.
 constexpr int kBuckets = 2 * kBlock;
 template <int kPer, typename SM>   // keys per thread: n <= kPer * kBlock
 __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int* cnt, SM& sm) {
@@ -98,7 +99,7 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
     for (int u = 0; u < kPer; ++u) {
         const int i = t + u * kBlock;
         k[u] = i < n ? keys[i] : 0ull;
-        if (i < n) {
+        if (k[u] != 0ull) {
             const float q = ckey_val(k[u]);
             qhi = fmaxf(qhi, q);
             qlo_neg = fmaxf(qlo_neg, -q);
@@ -127,7 +128,7 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
         const int i = t + u * kBlock;
         b[u] = 0;
         slot[u] = 0;
-        if (i < n) {
+        if (k[u] != 0ull) {
             const float f = (ckey_val(k[u]) - qmin) * scale;   // NaN (inf * 0) and below 0 -> bucket 0
             b[u] = f >= (float)(kBuckets - 1) ? kBuckets - 1 : (f >= 1.0f ? (int)f : 0);
             slot[u] = atomicAdd(&cnt[b[u]], 1);
@@ -135,6 +136,7 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
     }
     lds_sync();
     // descending exclusive scan: start[b] = keys in buckets above b
+    int tot;   // keys present
     {
         constexpr int kB = kBuckets / kBlock;   // buckets per thread
         int cb[kB], loc = 0;
@@ -143,7 +145,6 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
             cb[u] = cnt[kBuckets - 1 - (t * kB + u)];
             loc += cb[u];
         }
-        int tot;
         int st = block_excl_scan(loc, tot, sm);
 #pragma unroll
         for (int u = 0; u < kB; ++u) {
@@ -155,12 +156,12 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
     // every key was read into registers above: scatter in place
 #pragma unroll
     for (int u = 0; u < kPer; ++u)
-        if (t + u * kBlock < n) keys[cnt[b[u]] + slot[u]] = k[u];
+        if (k[u] != 0ull) keys[cnt[b[u]] + slot[u]] = k[u];
     lds_sync();
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-        if (t + u * kBlock < n) {
-            const int lo = cnt[b[u]], hi = b[u] > 0 ? cnt[b[u] - 1] : n;
+        if (k[u] != 0ull) {
+            const int lo = cnt[b[u]], hi = b[u] > 0 ? cnt[b[u] - 1] : tot;
             int r = lo;
             for (int j = lo; j < hi; ++j) r += keys[j] > k[u] ? 1 : 0;
             if (r < nkeep) out[r] = k[u];
@@ -320,11 +321,27 @@ __device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tm
     return 0;
 }
 
-template <typename T, bool FAST>
+// log2 of the words per list (header + entries) a whole-list merger reads
+// with the headers: the largest power of two that kUni holds for S lists,
+// at most 128.
+__device__ __forceinline__ int stage_log2(int S) {
+    int l = 7;
+    while (l > 0 && (S << l) > kUni) --l;
+    return l;
+}
+
+// NV logits a thread: kEpt, or kEptPacked for calls without a history
+// window on 16-byte-aligned 2-byte rows, whose stream stays in registers as
+// the masked raw vectors (half the registers of widened values), so a
+// chunk holds 20480 ids and fewer workgroups cover a row.
+template <typename T, bool FAST, int NV>
 __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     constexpr int VEC = Elt<T>::kVec;
-    constexpr int NVT = kEpt / VEC;
+    constexpr int NVT = NV / VEC;
+    constexpr bool kPacked = NV != kEpt;
+    static_assert(!kPacked || (FAST && VEC == 8), "the packed stream: 2-byte, aligned rows");
     __shared__ Smem sm;
+    static_assert(sizeof(DenseLds) <= sizeof(sm.big), "the whole-row path's LDS over the merge staging");
     const float NEG_INF = -__builtin_huge_valf();
     const int t = threadIdx.x;
     const int lane = t & 63, wv = t >> 6;
@@ -366,7 +383,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
     uint4 raw[NVT];
     uint32_t mw[NVT];
-    float sx[FAST ? 1 : kEpt];
+    float sx[FAST ? 1 : NV];
 #pragma unroll
     for (int j = 0; j < NVT; ++j) {
         const int v = min(t + j * kBlock, nvec - 1);
@@ -391,7 +408,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     Pen pn;
     pn.rep_on = !(P.repeat_penalty <= 1.0f);
     pn.fp_on = P.frequency_penalty != 0.0f || P.presence_penalty != 0.0f;
-    pn.on = nrec > 0 && (ovm || (P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on)));
+    pn.on = !kPacked && nrec > 0 && (ovm || (P.repeat_last_n > 0 && (pn.rep_on || pn.fp_on)));
     pn.rep = P.repeat_penalty;
     pn.freq = P.frequency_penalty;
     pn.pres = P.presence_penalty;
@@ -438,37 +455,65 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     }
 
     // ---- pass 1, as each slot lands: widen, mask, NaN/+inf check, slot max.
-    float x[kEpt];
+    //      The packed form keeps the masked raw vector (a masked entry holds
+    //      the type's -inf) and widens it again where it is read.
+    float x[kPacked ? 1 : NV];
+    uint4 xr[kPacked ? NVT : 1];
     float vmax[NVT];
     int nonfinite = 0;
 #pragma unroll
     for (int j = 0; j < NVT; ++j) {
         const int v = t + j * kBlock;
         const int eb = e0 + v * VEC;
-        float f[VEC];
-        if constexpr (FAST) {
-            Elt<T>::widen(raw[j], f);
-        } else {
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) f[e] = sx[j * VEC + e];
-        }
-        const uint32_t mb = (v < nvec) ? ((mw[j] >> (eb & 31)) & ~(uint32_t)(penbits >> (j * VEC))) : 0u;
+        uint32_t mb = (v < nvec) ? (mw[j] >> (eb & 31)) : 0u;
+        if constexpr (!kPacked) mb &= ~(uint32_t)(penbits >> (j * VEC));
         float vm = NEG_INF;
+        if constexpr (kPacked) {
+            uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            // bit e of mb, sign-extended, selects the value or -inf
-            const uint32_t sel = (uint32_t)((int)(mb << (31 - e)) >> 31);
-            uint32_t bits = (__float_as_uint(f[e]) & sel) | (0xFF800000u & ~sel);
-            if constexpr (!FAST) bits = (eb + e < e1) ? bits : 0xFF800000u;
-            const float g = __uint_as_float(bits);
-            // IEEE maximum (v_maximum3_f32) keeps a NaN, so one class test
-            // of the slot maximum finds any NaN or +inf of the slot.
-            vm = __builtin_elementwise_maximum(vm, g);
-            x[j * VEC + e] = g;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = (((mb >> (2 * i)) & 1u) ? 0x0000FFFFu : 0u) |
+                                   (((mb >> (2 * i + 1)) & 1u) ? 0xFFFF0000u : 0u);
+                wd[i] = (wd[i] & m) | (Elt<T>::kNegInfWord & ~m);
+            }
+            xr[j] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            float f[VEC];
+            Elt<T>::widen(xr[j], f);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) vm = __builtin_elementwise_maximum(vm, f[e]);
+        } else {
+            float f[VEC];
+            if constexpr (FAST) {
+                Elt<T>::widen(raw[j], f);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) f[e] = sx[j * VEC + e];
+            }
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                // bit e of mb, sign-extended, selects the value or -inf
+                const uint32_t sel = (uint32_t)((int)(mb << (31 - e)) >> 31);
+                uint32_t bits = (__float_as_uint(f[e]) & sel) | (0xFF800000u & ~sel);
+                if constexpr (!FAST) bits = (eb + e < e1) ? bits : 0xFF800000u;
+                const float g = __uint_as_float(bits);
+                // IEEE maximum (v_maximum3_f32) keeps a NaN, so one class test
+                // of the slot maximum finds any NaN or +inf of the slot.
+                vm = __builtin_elementwise_maximum(vm, g);
+                x[j * VEC + e] = g;
+            }
         }
         nonfinite |= __builtin_amdgcn_class(vm, 0x203);   // NaN or +inf
         vmax[j] = vm;
     }
+    // The stream values of slot j, widened (masked entries -inf).
+    auto slot_vals = [&](int j, float (&f)[VEC]) {
+        if constexpr (kPacked) {
+            Elt<T>::widen(xr[j], f);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) f[e] = x[j * VEC + e];
+        }
+    };
 
     __builtin_amdgcn_sched_barrier(0);
     TMS_TR(3);
@@ -508,7 +553,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     }
 
     // ---- pass 2 (long windows only): history penalties from the counts.
-    if (pn.on && !pen_own) {
+    if constexpr (!kPacked) if (pn.on && !pen_own) {
         // Positions [0, kWin * kBlock) came with the stream; later ones are
         // read now.
         for (int p0 = 0; p0 < nrec; p0 += kBlock * kWin) {
@@ -571,7 +616,12 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         for (int j = 1; j < NVT; ++j) smax = fmaxf(smax, vmax[j]);
         int q = 0;
 #pragma unroll
-        for (int i = kEpt - 1; i >= 0; --i) q = x[i] == smax ? i : q;
+        for (int j = NVT - 1; j >= 0; --j) {
+            float f[VEC];
+            slot_vals(j, f);
+#pragma unroll
+            for (int e = VEC - 1; e >= 0; --e) q = f[e] == smax ? j * VEC + e : q;
+        }
         uint64_t gb = smax != NEG_INF
                           ? ckey(smax, (uint32_t)(e0 + (t + (q / VEC) * kBlock) * VEC + q % VEC))
                           : 0ull;
@@ -680,10 +730,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                     const int pos = ns + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
                     if (sj && pos < kStage) {
+                        float f[VEC];
+                        slot_vals(j, f);
 #pragma unroll
                         for (int e = 0; e < VEC; e += 4)
-                            *(float4*)(stv + pos * VEC + e) =
-                                make_float4(x[j * VEC + e], x[j * VEC + e + 1], x[j * VEC + e + 2], x[j * VEC + e + 3]);
+                            *(float4*)(stv + pos * VEC + e) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
                         sts[pos] = t + j * kBlock;
                     }
                     ns += __popcll(m);
@@ -710,9 +761,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
 #pragma unroll
                 for (int j = 0; j < NVT; ++j) {
                     if (__any(vmax[j] >= thr)) {
+                        float fv[VEC];
+                        slot_vals(j, fv);
 #pragma unroll
                         for (int e = 0; e < VEC; ++e) {
-                            const float f = x[j * VEC + e];
+                            const float f = fv[e];
                             const bool p = f >= thr;
                             const uint64_t m = __ballot(p);
                             if (m) {
@@ -761,9 +814,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
 #pragma unroll
                 for (int j = 0; j < NVT; ++j) {
                     if (vmax[j] >= thr) {
+                        float fv[VEC];
+                        slot_vals(j, fv);
 #pragma unroll
                         for (int e = 0; e < VEC; ++e) {
-                            const float f = x[j * VEC + e];
+                            const float f = fv[e];
                             if (f >= thr) {
                                 const int pos = atomicAdd(&sm.ncand, 1);
                                 if (pos < kCand)
@@ -787,35 +842,76 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                 for (int w = 1; w < kWaves; ++w) cw[w] = 0;
             }
             TMS_TR(21);
-            if (n <= kCand) {
-                // Dense pass (the window counts are dead now): divide the
-                // candidates, form their keys contiguously in uni; top-p drops
-                // those below the exact span (key 0 sorts last).  Then rank
-                // them by counting into cand.
-                uint64_t* keys = sm.big.m.uni;
-                int nv = 0;
-                for (int i = t; i < n; i += kBlock) {
-                    int w = 0, base_i = 0;
+            // The raw candidate i, divided: its key (value, id) and whether
+            // a top-p row keeps it (within the exact span).
+            auto cand_key = [&](int i, bool& keepit) {
+                // the wave segment holding i (static indices into cw)
+                int w = 0, base_i = 0, acc = 0;
 #pragma unroll
-                    for (int u = 0; u < kWaves - 1; ++u)
-                        if (i >= base_i + cw[w]) { base_i += cw[w]; ++w; }
-                    const uint64_t rw = sm.cand[(over ? 0 : w * kSeg) + (i - base_i)];
-                    const float f = __uint_as_float((uint32_t)(rw >> 32));
-                    const uint32_t id = (uint32_t)rw;
-                    const float lg = divide ? f / temp : f;
-                    const bool keepit = mode == MODE_TOPK || (double)lg >= lthr;
-                    keys[i] = keepit ? ckey(lg, id) : 0ull;
-                    nv += keepit;
+                for (int u = 0; u < kWaves - 1; ++u) {
+                    acc += cw[u];
+                    if (i >= acc) {
+                        w = u + 1;
+                        base_i = acc;
+                    }
                 }
-                if (mode == MODE_TOPP) {
-                    nv = wave_sum_dpp(nv);
-                    if (lane == 0) sm.wave_i[wv] = nv;
+                const uint64_t rw = sm.cand[(over ? 0 : w * kSeg) + (i - base_i)];
+                const float f = __uint_as_float((uint32_t)(rw >> 32));
+                const uint32_t id = (uint32_t)rw;
+                const float lg = divide ? f / temp : f;
+                keepit = mode == MODE_TOPK || (double)lg >= lthr;
+                return ckey(lg, id);
+            };
+            if (n <= kCand && mode == MODE_TOPP) {
+                // Top-p lists are merged whole and ranked by the merger, so
+                // the chunk only compacts the kept keys into cand, in
+                // candidate order (two candidates a thread at most).
+                static_assert(kCand <= 2 * kBlock, "two candidates a thread");
+                bool kp0 = false, kp1 = false;
+                const uint64_t kk0 = t < n ? cand_key(t, kp0) : 0ull;
+                const uint64_t kk1 = t + kBlock < n ? cand_key(t + kBlock, kp1) : 0ull;
+                kp0 = kp0 && t < n;
+                kp1 = kp1 && t + kBlock < n;
+                const uint64_t bm0 = __ballot(kp0), bm1 = __ballot(kp1);
+                if (lane == 0) {
+                    sm.list_src[wv] = __popcll(bm0);
+                    sm.list_src[kWaves + wv] = __popcll(bm1);
+                }
+                lds_sync();   // every raw candidate read, every wave counted
+                TMS_TR(17);
+                TMS_TV(19, n + 1);
+                int off0 = 0, off1 = 0;
+                nout = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    const int c0 = sm.list_src[w], c1 = sm.list_src[kWaves + w];
+                    off0 += w < wv ? c0 : 0;
+                    off1 += w < wv ? c1 : 0;
+                    nout += c0;
+                }
+                off1 += nout;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) nout += sm.list_src[kWaves + w];
+                if (kp0)
+                    sm.cand[off0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(bm0 >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bm0, 0u))] = kk0;
+                if (kp1)
+                    sm.cand[off1 + __builtin_amdgcn_mbcnt_hi((uint32_t)(bm1 >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bm1, 0u))] = kk1;
+                lds_sync();
+                TMS_TR(18);
+            } else if (n <= kCand) {
+                // Top-k: the candidates' keys contiguously in uni (the window
+                // counts are dead now), then ranked by counting into cand.
+                uint64_t* keys = sm.big.m.uni;
+                for (int i = t; i < n; i += kBlock) {
+                    bool keepit;
+                    keys[i] = cand_key(i, keepit);
                 }
                 lds_sync();
                 TMS_TR(17);
                 TMS_TV(19, n + 1);
-                if (mode == MODE_TOPP) nout = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
-                else nout = n < K ? n : K;
+                nout = n < K ? n : K;
                 rank_all(keys, n, sm.cand);
                 lds_sync();
                 TMS_TR(18);
@@ -825,7 +921,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             if (mode == MODE_TOPK) {
                 nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn.on, pn.rep_on, pn.fp_on, pn.rep,
                                      pn.freq, pn.pres, pn.ov, sm);
-                sort_cand(nout, sm);
+                [[clang::always_inline]] sort_cand(nout, sm);
             } else {
                 flags |= FLAG_OVERFLOW;
                 nout = 0;
@@ -894,6 +990,9 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         sm.theta = 0;     // lists to read again (bit per list)
         sm.misc[3] = 0;   // a list never arrived
     }
+    uint64_t* srt = sm.big.m.surv;
+    const int RL = stage_log2(S), RT = 1 << RL;   // staged words per list (whole lists)
+    uint64_t hv[kUni / kBlock];
     if (spec) {
         // Every word read must be set: a ready header, non-zero entries (the
         // writer padded its r slots).  Each thread checks its own words.
@@ -952,16 +1051,32 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             lds_sync();
         }
     } else {
-        // Headers only; whole lists are read below.
-        if (t < S) {
-            const uint64_t h = t == c ? (kReady | ((uint64_t)flags << 32) | (uint64_t)(uint32_t)nout)
-                                      : ld_agent(&row_lists[(int64_t)t * kListStride]);
-            uni[t] = h;
-            if (!(h & kReady)) atomicOr((unsigned long long*)&sm.theta, 1ull << t);
+        // Whole lists (top-p rows, top-k rows over many lists): every
+        // list's header and first RT - 1 entries in one round of loads, all
+        // issued before any is used, kept in registers (hv); the headers go
+        // to srt (free until a merge ranks into it).  When every list fits,
+        // its entries are stored packed and ranked; otherwise the merge
+        // rounds below read the lists again.
+#pragma unroll
+        for (int u = 0; u < kUni / kBlock; ++u) {
+            const int idx = t + u * kBlock;
+            const int cc = idx >> RL, jj = idx & (RT - 1);
+            hv[u] = (cc < S && cc != c) ? ld_agent(&row_lists[(int64_t)cc * kListStride + jj]) : 0ull;
+            if (cc == c) hv[u] = jj == 0 ? hdr : (jj <= nout ? sm.cand[jj - 1] : 0ull);
+        }
+#pragma unroll
+        for (int u = 0; u < kUni / kBlock; ++u) {
+            const int idx = t + u * kBlock;
+            const int cc = idx >> RL, jj = idx & (RT - 1);
+            if (cc < S && jj == 0) {
+                srt[cc] = hv[u];
+                if (!(hv[u] & kReady)) atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
+            }
         }
         lds_sync();
     }
-    const int HW = spec ? R1 : 1;   // stride of the headers in uni
+    uint64_t* hdrs = spec ? uni : srt;   // the headers, stride HW
+    const int HW = spec ? R1 : 1;
     if (wv == 0) {
         // Headers-only mode: wait (bounded) for the lists not yet complete.
         const uint64_t redo = spec ? 0ull : sm.theta;
@@ -972,12 +1087,12 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                 if (h & kReady) break;
                 __builtin_amdgcn_s_sleep(1);
             }
-            uni[lane * HW] = h;
+            hdrs[lane * HW] = h;
             if (!(h & kReady)) sm.misc[3] = 1;
         }
         int n_c = 0, f_c = 0, m_c = 0;
         if (lane < S) {
-            const uint64_t h = uni[lane * HW];
+            const uint64_t h = hdrs[lane * HW];
             n_c = (int)(uint32_t)h;
             f_c = (int)((h >> 32) & 0xFF);
             m_c = min(n_c, r);
@@ -988,10 +1103,17 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         int fo = f_c;
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) fo |= __shfl_xor(fo, m, 64);
+        // Staged whole lists are ranked in place when no header was read
+        // again and every list fits its staged words.
+        const bool fits = lane >= S || n_c <= RT - 1;
+        const bool staged = !spec && redo == 0 && __ballot(!fits) == 0ull;
+        const int incl = wave_incl_scan_i32(n_c);
+        if (lane < S) sm.hist[lane] = incl - n_c;   // packed offset of each list
         if (lane == 0) {
             sm.misc[5] = N;
             sm.misc[4] = fo;
             sm.misc[1] = 0;   // "a list ran out"
+            sm.misc[6] = staged;
         }
     }
     lds_sync();
@@ -1009,7 +1131,6 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     const bool go_dense = status == TMS_ROW_OK && mode == MODE_TOPP &&
                           ((fo & FLAG_OVERFLOW) || min(N, K) > kToppCap);
 
-    uint64_t* srt = sm.big.m.surv;
     int n_acc = 0;
     bool full = !spec;
     if (status == TMS_ROW_OK && spec) {
@@ -1079,11 +1200,42 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         lds_sync();
         full = sm.misc[1] != 0;
     }
-    if (status == TMS_ROW_OK && full && !go_dense) {
+    const int keep_cap = mode == MODE_TOPP ? min(kToppCap, K) : K;
+    bool merged = false;
+    if (status == TMS_ROW_OK && !spec && !go_dense && sm.misc[6]) {
+        // The staged lists, packed in list order into uni; a word inside a
+        // list that still reads 0 sends the row to the merge rounds.
+        int bad = 0;
+#pragma unroll
+        for (int u = 0; u < kUni / kBlock; ++u) {
+            const int idx = t + u * kBlock;
+            const int cc = idx >> RL, jj = idx & (RT - 1);
+            if (cc < S && jj >= 1 && jj <= sm.list_n[cc]) {
+                bad |= hv[u] == 0ull;
+                uni[sm.hist[cc] + jj - 1] = hv[u];
+            }
+        }
+        if (__ballot(bad) && lane == 0) atomicOr(&sm.misc[2], 1);
+        lds_sync();
+        TMS_TR(11);
+        if (!sm.misc[2]) {
+            n_acc = min(N, keep_cap);
+            if (N <= 2 * kBlock) {
+                [[clang::always_inline]] bucket_rank<2>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
+            } else if (N <= 4 * kBlock) {
+                [[clang::always_inline]] bucket_rank<4>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
+            } else {
+                [[clang::always_inline]] bucket_rank<kUni / kBlock>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
+            }
+            merged = true;
+            lds_sync();
+            TMS_TR(12);
+        }
+    }
+    if (status == TMS_ROW_OK && full && !go_dense && !merged) {
         // Whole lists, in rounds: the running top list (surv[0..n_acc)) plus
         // as many chunk lists as fit in kUni, ranked by binary search against
         // each other.  Top-k rows read at most K entries a list.
-        const int keep_cap = mode == MODE_TOPP ? min(kToppCap, K) : K;
         if (t < S) sm.list_s[t] = mode == MODE_TOPP ? sm.list_n[t] : min(sm.list_n[t], K);
         n_acc = 0;
         int c_next = 0;
@@ -1126,8 +1278,11 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             const int nkeep = total < keep_cap ? total : keep_cap;
             // The staged lists' keys ranked together (the bucket counts go
             // to pbits, dead since the chunk phase).
-            if (total <= 2 * kBlock) bucket_rank<2>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
-            else bucket_rank<kUni / kBlock>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+            if (total <= 2 * kBlock) {
+                [[clang::always_inline]] bucket_rank<2>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+            } else {
+                [[clang::always_inline]] bucket_rank<kUni / kBlock>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+            }
             TMS_TR(12);
             c_next = sm.misc[7];
             n_acc = nkeep;
@@ -1146,97 +1301,101 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         write_row_error(a, row, status);
         return;
     }
-    if (go_dense) {
-        defer_dense(a, row);
-        return;
-    }
+    // One place runs the whole-row path (the lists are done with): rows
+    // that need it from the start, and top-p rows whose answer turns out to
+    // need the order past the held entries.
+    bool whole = go_dense;
+    if (!go_dense) {
+        if (mode == MODE_GREEDY) {
+            const int tok = (int)ckey_id(srt[0]);
+            if (t == 0) {
+                a.out_tokens[row] = tok;
+                a.out_status[row] = TMS_ROW_OK;
+                if (a.out_keep) a.out_keep[row] = 0;
+            }
+            for (int i = t; i < a.topk_cap; i += kBlock) {
+                if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
+                if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
+            }
+            return;
+        }
 
-    if (mode == MODE_GREEDY) {
-        const int tok = (int)ckey_id(srt[0]);
-        if (t == 0) {
-            a.out_tokens[row] = tok;
-            a.out_status[row] = TMS_ROW_OK;
-            if (a.out_keep) a.out_keep[row] = 0;
+        int n = n_acc;
+        if (mode == MODE_TOPK && N < K) {
+            // Fewer than K finite ids: the tail goes on with -inf entries in
+            // ascending id order, i.e. the ids in [0, K + N) missing from the
+            // (then complete) finite set; K + N < 2 * kTopkFast <= kBlock.
+            const int q = t;
+            int member = 0;
+            if (q < K + N)
+                for (int i = 0; i < N; ++i) member |= (int)ckey_id(srt[i]) == q;
+            const int gap = (q < K + N && !member && q < V) ? 1 : 0;
+            int tot;
+            const int p = block_excl_scan(gap, tot, sm);
+            if (gap && p < K - N) srt[N + p] = ckey(NEG_INF, (uint32_t)q);
+            lds_sync();
+            n = K;
         }
-        for (int i = t; i < a.topk_cap; i += kBlock) {
-            if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
-            if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
+        TMS_TR(7);
+        const float mx = ckey_val(srt[0]);
+        if (mx == __builtin_huge_valf()) {
+            if (defer_zero) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
+            write_row_error(a, row, TMS_ROW_NONFINITE);
+            return;
         }
-        return;
-    }
-
-    int n = n_acc;
-    if (mode == MODE_TOPK && N < K) {
-        // Fewer than K finite ids: the tail goes on with -inf entries in
-        // ascending id order, i.e. the ids in [0, K + N) missing from the
-        // (then complete) finite set; K + N < 2 * kTopkFast <= kBlock.
-        const int q = t;
-        int member = 0;
-        if (q < K + N)
-            for (int i = 0; i < N; ++i) member |= (int)ckey_id(srt[i]) == q;
-        const int gap = (q < K + N && !member && q < V) ? 1 : 0;
-        int tot;
-        const int p = block_excl_scan(gap, tot, sm);
-        if (gap && p < K - N) srt[N + p] = ckey(NEG_INF, (uint32_t)q);
-        lds_sync();
-        n = K;
-    }
-    TMS_TR(7);
-    const float mx = ckey_val(srt[0]);
-    if (mx == __builtin_huge_valf()) {
-        if (defer_zero) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
-        write_row_error(a, row, TMS_ROW_NONFINITE);
-        return;
-    }
-    if (mode == MODE_TOPK) {
-        if (wv == 0) {
-            uint32_t w0, w1;
-            row_uniform(a, row, P, w0, w1);
-            tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand, w0, w1);
+        if (mode == MODE_TOPK) {
+            if (wv == 0) {
+                uint32_t w0, w1;
+                row_uniform(a, row, P, w0, w1);
+                [[clang::always_inline]] tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand, w0, w1);
+            }
+            else
+                zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
+            return;
         }
-        else
-            zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
-        return;
-    }
-    // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
-    // The count of that prefix and every held entry's pr in one pass (pr
-    // past the prefix is never read).
-    double* pr = (double*)sm.big.m.uni;               // staging no longer needed
-    double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
-    {
-        int sig = 0;
-        for (int i = t; i < n; i += kBlock) {
-            const double d = (double)ckey_val(srt[i]) - (double)mx;
-            sig += d >= -(double)kSigSpan ? 1 : 0;
-            pr[i] = exp(d);
+        // Top-p rows: only the prefix within kSigSpan of the maximum is exact.
+        // The count of that prefix and every held entry's pr in one pass (pr
+        // past the prefix is never read).
+        double* pr = (double*)sm.big.m.uni;               // staging no longer needed
+        double* q = (double*)(sm.big.m.surv + kToppCap);  // past the sorted entries
+        {
+            int sig = 0;
+            for (int i = t; i < n; i += kBlock) {
+                const double d = (double)ckey_val(srt[i]) - (double)mx;
+                sig += d >= -(double)kSigSpan ? 1 : 0;
+                pr[i] = exp(d);
+            }
+            sig = wave_sum_dpp(sig);
+            if (lane == 0) sm.wave_i[wv] = sig;
+            if (t == 0) sm.nvalid = 0;
+            lds_sync();
+            n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
+            n = min(n, K);   // tmsample::sample sums over the top K only (tmsample.h:185-191)
         }
-        sig = wave_sum_dpp(sig);
-        if (lane == 0) sm.wave_i[wv] = sig;
-        if (t == 0) sm.nvalid = 0;
-        lds_sync();
-        n = sm.wave_i[0] + sm.wave_i[1] + sm.wave_i[2] + sm.wave_i[3];
-        n = min(n, K);   // tmsample::sample sums over the top K only (tmsample.h:185-191)
-    }
-    TMS_TR(14);
-    const int tp = tail_topp_block(a, row, P, srt, n, K, pr, sm);
-    TMS_TR(15);
-    if (tp == 2) {
-        // the sequential tail decides (or returns the probabilities)
-        if (wv == 0) {
-            TMS_TV(16, 1);
-            const bool lost = tail_topp(a, row, P, srt, n, K, pr, q);
-            if (lane == 0) sm.nvalid = lost;
+        TMS_TR(14);
+        const int tp = tail_topp_block(a, row, P, srt, n, K, pr, sm);
+        TMS_TR(15);
+        if (tp == 2) {
+            // the sequential tail decides (or returns the probabilities)
+            if (wv == 0) {
+                TMS_TV(16, 1);
+                bool lost;
+                [[clang::always_inline]] lost = tail_topp(a, row, P, srt, n, K, pr, q);
+                if (lane == 0) sm.nvalid = lost;
+            } else {
+                zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
+            }
         } else {
-            zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
+            if (t == 0) sm.nvalid = tp;
+            zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
         }
-    } else {
-        if (t == 0) sm.nvalid = tp;
-        zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
+        TMS_TR(8);
+        lds_sync();
+        whole = sm.nvalid != 0;
     }
-    TMS_TR(8);
-    lds_sync();
-    // The answer needs the order past the held entries: the whole row.
-    if (sm.nvalid) defer_dense(a, row);
+    if (whole) {
+        [[clang::always_inline]] dense_inline<T>(a, row, *reinterpret_cast<DenseLds*>(&sm.big));
+    }
 }
 
 }  // namespace tms
@@ -1295,7 +1454,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     const size_t off_tl = off_ss + nb * (2 * tms::kSpecMaxK + 1) * sizeof(tms_spec_stat);
     const size_t tl_chunks = (size_t)std::min(ctx->max_chunks, tms::kWideMaxChunksHost);
     const size_t off_dq = off_tl + nb * tl_chunks * tms::kWideListStride * sizeof(uint64_t);
-    const size_t off_hn = off_dq + 256 * (((tms::kDenseQueueHead + nb) * sizeof(uint32_t) + 255) / 256);
+    const size_t off_hn = off_dq + 256 * (((size_t)tms::kDenseSlotsMax * sizeof(uint32_t) + 255) / 256);
     const size_t off_hi = off_hn + 256 * ((nb * sizeof(int32_t) + 255) / 256);
     const size_t off_hv = off_hi + nb * tms::kHistMax * sizeof(int32_t);
     ctx->bytes = off_hv + nb * tms::kHistMax * sizeof(float);
@@ -1306,7 +1465,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     else if (hipDeviceSynchronize() != hipSuccess) rc = TMS_ERR_HIP;
     // The whole-row path's region: never read before it is written, so not
     // cleared.
-    ctx->dense_slots = std::min(max_batch, tms::kDenseGridMax);
+    ctx->dense_slots = std::min(max_batch, tms::kDenseSlotsMax);
     ctx->dense_bytes = (size_t)ctx->dense_slots * 2 * (size_t)max_vocab * sizeof(uint64_t);
     if (rc == TMS_OK && hipMalloc(&ctx->dense, ctx->dense_bytes) != hipSuccess) {
         ctx->dense = nullptr;
@@ -1326,7 +1485,7 @@ extern "C" int tms_create(int device, int max_batch, int max_vocab, tms_context*
     ctx->spec_parts = (uint64_t*)(p + off_sp);
     ctx->spec_stats = (tms_spec_stat*)(p + off_ss);
     ctx->tlists = (uint64_t*)(p + off_tl);
-    ctx->dqueue = (uint32_t*)(p + off_dq);
+    ctx->dlocks = (uint32_t*)(p + off_dq);
     ctx->ov_n = (int32_t*)(p + off_hn);
     ctx->ov_ids = (int32_t*)(p + off_hi);
     ctx->ov_vals = (float*)(p + off_hv);
@@ -1354,7 +1513,7 @@ extern "C" size_t tms_workspace_bytes(const tms_context* ctx) {
 }
 
 // Zero every workspace word the cross-workgroup protocols expect at zero
-// (counters, tickets, list and part words, the queue), keeping the all-ones
+// (counters, tickets, list and part words, the region locks), keeping the all-ones
 // mask row.  For recovery after a TMS_ROW_INTERNAL row, whose late words
 // may otherwise be taken as the next call's.
 static int reset_regions(void* ws, size_t ones_begin, size_t ones_end, size_t bytes, hipStream_t stream) {
@@ -1384,7 +1543,7 @@ struct SampleWs {
     uint32_t* ones;
     uint64_t* lists;
     uint64_t* tlists;
-    uint32_t* dqueue;
+    uint32_t* dlocks;
     uint64_t* dense;
     int dense_slots;
     int32_t* ov_n;         // the history pre-pass's lists
@@ -1437,18 +1596,19 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
     k.counters = w.counters;
     k.lists = w.lists;
     k.tlists = w.tlists;
-    // The whole-row pass follows any call without the top-k promise.
-    const bool dense_pass = a->row_kinds == TMS_ROWS_ANY;
-    k.dense = dense_pass ? w.dense : nullptr;
+    // Any row a chunked kernel cannot finish from its candidate lists is
+    // sampled whole by its own merger, in a region of the workspace taken
+    // by a lock (no second launch).
+    k.dense = w.dense;
     k.dense_stride = w.max_vocab;
-    k.dqueue = w.dqueue;
-    const int dense_grid = std::min(a->batch, w.dense_slots);
+    k.dlocks = w.dlocks;
+    k.dense_slots = w.dense_slots;
 #ifdef TMS_TRACE
     k.trace = g_tms_trace_host;
 #endif
     if (a->history && a->recent) {
         // The history pre-pass lists every row's touched ids with their
-        // final values; the general kernel and the whole-row pass take the
+        // final values; the general kernel and its whole-row path take the
         // list as the window (tms_hist.hip).
         if (a->dry_scale && a->dry_scale_stride <= 0) return TMS_ERR_INVALID_ARG;
         const int rc = tms_launch_history(k, a->history, a->dry_breaker, a->dry_scale, a->dry_scale_stride,
@@ -1460,7 +1620,7 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
         k.ov_vals = w.ov_vals;
         k.dense = w.dense;
         const dim3 grid((unsigned)(a->batch * k.S)), block(tms::kBlock);
-#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F>), grid, block, 0, stream, k)
+#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F, tms::kEpt>), grid, block, 0, stream, k)
         switch (a->dtype) {
             case TMS_DTYPE_F32:
                 if (fast) TMS_LAUNCH(float, true);
@@ -1476,8 +1636,7 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
                 break;
         }
 #undef TMS_LAUNCH
-        if (hipGetLastError() != hipSuccess) return TMS_ERR_HIP;
-        return tms_launch_dense(k, a->dtype, dense_grid, stream);
+        return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;
     }
     if (a->row_kinds == TMS_ROWS_TOPK && (!a->recent || a->recent_stride <= tms::kWideMaxWindow)) {
         // Every row greedy or top-k <= 128 (the caller's promise): the wide
@@ -1506,34 +1665,44 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
                 tms::KArgs kw = k;
                 kw.CE = ce;
                 kw.S = (a->vocab + ce - 1) / ce;
-                kw.dense = nullptr;   // rows that break the promise report TMS_ROW_UNSUPPORTED
                 return tms_launch_wide(kw, a->dtype, fast, a->batch, slots, stream);
             }
         }
     }
     // Everything else, including top-k batches whose grid does not fit the
-    // wide kernel's residency (rows that break the promise then report
-    // TMS_ROW_UNSUPPORTED: no whole-row pass follows a top-k call): the
-    // general kernel.
+    // wide kernel's residency: the general kernel.  Aligned 2-byte rows
+    // without a history window take its packed form when that needs fewer
+    // chunks a row (config 3's shape, B = 128 and V = 151936: 8 chunks
+    // instead of 10, so the 1,024 workgroups are resident at once).
+    const int s_packed = (a->vocab + tms::kBlock * tms::kEptPacked - 1) / (tms::kBlock * tms::kEptPacked);
+    const bool packed = fast && esz == 2 && !a->recent && s_packed < k.S;
+    if (packed) {
+        k.S = s_packed;
+        const int per_p = (a->vocab + k.S - 1) / k.S;
+        k.CE = (per_p + vec - 1) / vec * vec;
+    }
     const dim3 grid((unsigned)(a->batch * k.S)), block(tms::kBlock);
-#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F>), grid, block, 0, stream, k)
+#define TMS_LAUNCH(T, F) hipLaunchKernelGGL((tms::sample_kernel<T, F, tms::kEpt>), grid, block, 0, stream, k)
+#define TMS_LAUNCH_PACKED(T) hipLaunchKernelGGL((tms::sample_kernel<T, true, tms::kEptPacked>), grid, block, 0, stream, k)
     switch (a->dtype) {
         case TMS_DTYPE_F32:
             if (fast) TMS_LAUNCH(float, true);
             else TMS_LAUNCH(float, false);
             break;
         case TMS_DTYPE_F16:
-            if (fast) TMS_LAUNCH(_Float16, true);
+            if (packed) TMS_LAUNCH_PACKED(_Float16);
+            else if (fast) TMS_LAUNCH(_Float16, true);
             else TMS_LAUNCH(_Float16, false);
             break;
         default:
-            if (fast) TMS_LAUNCH(tms::Bf16, true);
+            if (packed) TMS_LAUNCH_PACKED(tms::Bf16);
+            else if (fast) TMS_LAUNCH(tms::Bf16, true);
             else TMS_LAUNCH(tms::Bf16, false);
             break;
     }
+#undef TMS_LAUNCH_PACKED
 #undef TMS_LAUNCH
-    if (hipGetLastError() != hipSuccess) return TMS_ERR_HIP;
-    return dense_pass ? tms_launch_dense(k, a->dtype, dense_grid, stream) : TMS_OK;
+    return hipGetLastError() == hipSuccess ? TMS_OK : TMS_ERR_HIP;
 }
 
 extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipStream_t stream) {
@@ -1545,7 +1714,7 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
     w.ones = ctx->ones;
     w.lists = ctx->lists;
     w.tlists = ctx->tlists;
-    w.dqueue = ctx->dqueue;
+    w.dlocks = ctx->dlocks;
     w.dense = ctx->dense;
     w.dense_slots = ctx->dense_slots;
     w.ov_n = ctx->ov_n;
@@ -1559,9 +1728,10 @@ extern "C" int tms_sample_batch(tms_context* ctx, const tms_sample_args* a, hipS
 // tms_sample_batch_noalloc runs the same kernels over `scratch`, a
 // file-scope device array of fixed size, instead of a context's workspace:
 // batches of up to kNoAllocRows rows of up to kNoAllocVocab ids, and one
-// region for the whole-row pass (its rows are taken one after another).
+// region for the whole-row path (taken by a lock: rows that need it run one
+// after another).
 // The array starts zeroed when the code object loads, and every launch
-// leaves its counters, lists and queue at zero again, as a context's
+// leaves its counters, lists and lock at zero again, as a context's
 // workspace does.  The all-ones mask row (for calls without a mask) is set
 // once per device.  In host code `scratch` names a host-side stand-in, so
 // its device address is looked up once per device (hipGetSymbolAddress,
@@ -1576,8 +1746,8 @@ constexpr size_t align32(size_t words) { return (words + 31) / 32 * 32; }   // u
 constexpr size_t kNaCounters = 0;
 constexpr size_t kNaLists = kNaCounters + align32((size_t)kNoAllocRows * tms::kCounterStride / 2);
 constexpr size_t kNaTlists = kNaLists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kListStride);
-constexpr size_t kNaQueue = kNaTlists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kWideListStride);
-constexpr size_t kNaHistN = kNaQueue + align32((tms::kDenseQueueHead + kNoAllocRows + 1) / 2);
+constexpr size_t kNaLocks = kNaTlists + align32((size_t)kNoAllocRows * kNoAllocChunks * tms::kWideListStride);
+constexpr size_t kNaHistN = kNaLocks + align32(1);   // one whole-row region lock
 constexpr size_t kNaHistIds = kNaHistN + align32(kNoAllocRows / 2);
 constexpr size_t kNaHistVals = kNaHistIds + (size_t)kNoAllocRows * tms::kHistMax / 2;
 constexpr size_t kNaOnes = kNaHistVals + (size_t)kNoAllocRows * tms::kHistMax / 2;
@@ -1639,7 +1809,7 @@ extern "C" int tms_sample_batch_noalloc(const tms_sample_args* a, hipStream_t st
     w.ones = (uint32_t*)(base + kNaOnes);
     w.lists = base + kNaLists;
     w.tlists = base + kNaTlists;
-    w.dqueue = (uint32_t*)(base + kNaQueue);
+    w.dlocks = (uint32_t*)(base + kNaLocks);
     w.dense = base + kNaDense;
     w.dense_slots = 1;
     w.ov_n = (int32_t*)(base + kNaHistN);

@@ -37,6 +37,7 @@ namespace tms {
 
 constexpr int kEpt = 64;                   // logits per thread held in registers
 constexpr int kChunk = kBlock * kEpt;      // ids per workgroup
+constexpr int kEptPacked = 80;             // the same for the packed stream (2-byte rows, no window)
 constexpr int kTopkFast = 128;             // largest K on the threshold path
 constexpr int kCand = 512;                 // chunk candidates held in LDS
 constexpr int kListStride = kCand + 2;     // u64 per published list: header + entries
@@ -52,8 +53,7 @@ constexpr float kSigSpan = 40.0f;          // exp(-40) < 2^-57: below this, no e
 constexpr uint64_t kReady = 1ull << 63;    // header bit: the list is complete
 constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per list
 constexpr int kReadRounds = 64;            // bound on the merger's re-reads of a sample
-constexpr int kDenseQueueHead = 64;        // u32 words before the whole-row queue's rows
-constexpr int kDenseGridMax = 256;         // workgroups of the whole-row pass
+constexpr int kDenseSlotsMax = 256;        // whole-row regions of a context
 constexpr int kHistMax = TMS_HISTORY_MAX_IDS; // ids one row's history pre-pass may list
 
 enum : int { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_TOPP = 2 };
@@ -82,11 +82,11 @@ struct KArgs {
     uint32_t* counters;    // [B] arrival tickets, reset by the merger
     uint64_t* lists;       // [B][S][kListStride]: header, entries; headers reset by the merger
     uint64_t* tlists;      // [B][S][kWideListStride]: the wide kernel's lists, zeroed by the merger
-    uint64_t* dense;       // [B][2 * dense_stride]: the whole-row pass's keys and sums; null when
-                           // the call runs no whole-row pass
+    uint64_t* dense;       // [dense_slots][2 * dense_stride]: the whole-row path's keys and
+                           // sums; null when the call has no whole-row path
     int64_t dense_stride;  // >= V
-    uint32_t* dqueue;      // [0] rows queued, [1] rows taken, [2] pass workgroups done,
-                           // [kDenseQueueHead + i] the queued rows
+    uint32_t* dlocks;      // [dense_slots]: 1 while a workgroup works in the region, else 0
+    int dense_slots;
     const float* ov_vals;  // [B][kHistMax] the history pre-pass's values, with `recent`,
                            // `n_recent` its id lists (n_recent -1: the row overflowed);
                            // null when the call has no pre-pass
@@ -148,7 +148,7 @@ struct Smem {
     int list_s[kMaxChunks];        // survivors of each chunk list
     int hist[256];
     int ncand;
-    int nvalid;                    // top-p tail: the row goes to the whole-row pass
+    int nvalid;                    // top-p tail: the row takes the whole-row path
     int misc[8];
     uint64_t theta;
 };
@@ -356,21 +356,6 @@ __device__ __forceinline__ void write_row_error(const KArgs& a, int row, int sta
     for (int i = t; i < a.topk_cap; i += kBlock) {
         if (ids) ids[i] = -1;
         if (probs) probs[i] = 0.0f;
-    }
-}
-
-// Hand row `row` to the whole-row pass that follows the launch (all
-// threads of the workgroup call this; thread 0 queues the row).  Without
-// that pass the row reports TMS_ROW_UNSUPPORTED.
-__device__ __forceinline__ void defer_dense(const KArgs& a, int row) {
-    if (!a.dense) {
-        write_row_error(a, row, TMS_ROW_UNSUPPORTED);
-        return;
-    }
-    if (threadIdx.x == 0) {
-        const uint32_t slot = __hip_atomic_fetch_add(&a.dqueue[0], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        a.dqueue[kDenseQueueHead + slot] = (uint32_t)row;
     }
 }
 
@@ -760,8 +745,6 @@ __device__ __forceinline__ int wave_min_nonneg(int v) {
 
 // Launches the wide top-k kernel (tms_wide.hip) over `batch` rows.
 int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream);
-// Launches the whole-row pass (tms_dense.hip) for the rows the kernel before it queued.
-int tms_launch_dense(const tms::KArgs& k, int dtype, int workgroups, hipStream_t stream);
 int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,
                        const float* dry_scale, int64_t dry_scale_stride, int dtype, int batch,
                        int32_t* ov_n, int32_t* ov_ids, float* ov_vals, hipStream_t stream);

@@ -853,10 +853,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     else if (fo & FLAG_NONFINITE) status = TMS_ROW_NONFINITE;
     else if (unsupported) status = TMS_ROW_UNSUPPORTED;
     else if (ntot == 0) status = TMS_ROW_ALL_MASKED;
-    if (status == TMS_ROW_UNSUPPORTED) {
-        defer_dense(a, row);   // the whole-row pass, or TMS_ROW_UNSUPPORTED without one
-        return;
-    }
     if (status != TMS_ROW_OK) {
         if (t == 0) {
             a.out_tokens[row] = -1;

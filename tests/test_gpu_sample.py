@@ -210,6 +210,43 @@ def test_cfg3_full_size_fp16_vs_oracle(sampler, orc, cap):
     check(g, want, cap)
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_packed_stream_rows_vs_oracle(sampler, orc, dtype):
+    """2-byte rows without a history window take the general kernel's packed
+    stream (20480 ids a chunk: V = 100000 in 5 chunks, not 7): greedy,
+    top-k (40, 128 and 300) and top-p rows, with a mask, a NaN row and an
+    all-masked row, equal the oracle over the widened values."""
+    rng = np.random.default_rng(7 if dtype == "f16" else 8)
+    B, V = 12, 100000
+    x32 = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    x32[:, ::97] += 6.0
+    if dtype == "f16":
+        xs = x32.astype(np.float16)
+        xw = xs.astype(np.float32)
+    else:
+        xs = workloads.to_bf16_bits(x32)
+        xw = workloads.bf16_bits_to_f32(xs)
+    xw = xw.copy()
+    if dtype == "f16":
+        xs[9, 5000] = np.nan
+    else:
+        xs[9, 5000] = 0x7FC0
+    xw[9, 5000] = np.nan
+    bits = rng.random((B, V)) < 0.6
+    bits[9, 5000] = True
+    bits[10] = False
+    mask = workloads.pack_bits(bits)
+    p = params_array(B, temperature=0.9, top_k=40, top_p=0.95, seed=np.arange(B) + 31)
+    p["greedy"][0] = 1
+    p["top_k"] = [40, 40, 128, 300, 0, 0, 40, 0, 50, 40, 40, 0]
+    p["top_p"][7] = 0.3
+    p["min_p"][6] = 0.02
+    want = orc.sample_batch(xw, p, mask=mask, topk_cap=24)
+    g = run_gpu(sampler, xs, p, mask=mask, topk_cap=24, dtype=dtype)
+    assert list(g["status"][9:11]) == [3, 2]
+    check(g, want, 24)
+
+
 @pytest.mark.parametrize("n_allowed", [70, 700, 1000])
 def test_topp_rows_many_entries(sampler, orc, n_allowed):
     """Top-p rows (top_k = 0) holding up to 1000 entries within 40 of the
@@ -550,8 +587,8 @@ def test_large_top_k_rows(sampler, orc, K, kind, cap):
 
 
 @pytest.mark.parametrize("cap", [0, 64, 2000])
-def test_dense_rows_whole_row_pass(sampler, orc, cap):
-    """Rows only the whole-row pass can finish: top_k = 0 over flat rows
+def test_dense_rows_whole_row_path(sampler, orc, cap):
+    """Rows only the whole-row path can finish: top_k = 0 over flat rows
     (tens of thousands of entries within 40 of the maximum) at V = 128256,
     with penalties and a mask; a row whose draw lands past the entries that
     move the sums (u just below 1 with top_p = 1); a min-p threshold below
@@ -616,6 +653,98 @@ def test_wide_kernel_error_rows(sampler, orc):
     torch.cuda.synchronize()
     assert list(out["status"].cpu().numpy()) == [0, 0]
     assert np.array_equal(out["tokens"].cpu().numpy(), want2["tokens"])
+
+
+@pytest.mark.parametrize("allowed", [60, 127, 140, 400])
+def test_topp_lists_around_the_staged_words(sampler, orc, allowed):
+    """Top-p rows over 4 chunks (V = 65536), the mask leaving about
+    `allowed` ids a chunk: lists that fit the merger's 127 staged entries
+    (ranked in place) and lists past them (the merge rounds), mixed in one
+    batch; every row equals the oracle."""
+    rng = np.random.default_rng(allowed)
+    B, V = 8, 65536
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    bits = rng.random((B, V)) < (allowed + rng.integers(-15, 15, (B, 1))) / 16384.0
+    mask = workloads.pack_bits(bits)
+    p = params_array(B, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(B) + 17)
+    p["top_p"][1::2] = 0.5
+    p["min_p"][3] = 0.05
+    want = orc.sample_batch(x, p, mask=mask, topk_cap=32)
+    g = run_gpu(sampler, x, p, mask=mask, topk_cap=32)
+    assert (g["status"] == 0).all()
+    check(g, want, 32)
+
+
+def test_whole_lists_over_more_than_16_chunks(orc):
+    """V = 300,000 (19 chunks, past the sampled merge's 16 lists): top-k
+    rows and a top-p row through the whole-list merge with the staged
+    headers; every row equals the oracle."""
+    import torch
+
+    from tensormark_amd import Sampler
+
+    rng = np.random.default_rng(19)
+    B, V = 4, 300000
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    p = params_array(B, temperature=0.8, top_k=40, top_p=0.95, seed=np.arange(B) + 5)
+    p["top_k"][2] = 0
+    bits = np.ones((B, V), bool)
+    bits[2] = rng.random(V) < 0.004
+    mask = workloads.pack_bits(bits)
+    want = orc.sample_batch(x, p, mask=mask, topk_cap=16)
+    s = Sampler(max_batch=4, max_vocab=V)
+    try:
+        out = s.sample(torch.from_numpy(x).to("cuda:0"), p, mask=torch.from_numpy(mask.view(np.int32)).to("cuda:0"),
+                       topk_cap=16)
+        torch.cuda.synchronize()
+        g = {k: v.cpu().numpy() for k, v in out.items()}
+    finally:
+        s.close()
+    assert (g["status"] == 0).all(), g["status"]
+    check(g, want, 16)
+
+
+def test_whole_row_regions_shared_by_more_rows_than_regions(sampler, orc):
+    """300 flat top-p rows, each needing the whole-row path, against the
+    context's 256 regions: rows r and r + 256 take turns on one region's
+    lock; every row equals the oracle."""
+    rng = np.random.default_rng(53)
+    B, V = 300, 5000
+    x = rng.normal(0.0, 0.5, (B, V)).astype(np.float32)
+    p = params_array(B, temperature=1.0, top_k=0, top_p=0.95, seed=np.arange(B) + 3)
+    want = orc.sample_batch(x, p, topk_cap=8)
+    g = run_gpu(sampler, x, p, topk_cap=8)
+    assert (g["status"] == 0).all()
+    check(g, want, 8)
+
+
+def test_broken_promise_rows_sampled_by_the_general_kernel(sampler, orc):
+    """A ROWS_TOPK call the wide kernel does not take (a 600-id window, past
+    its 1024): the general kernel samples the rows that break the promise
+    like any other (top_k = 0 over a flat row, which needs the whole-row
+    path, and top_k = 300), in the same launch."""
+    import torch
+
+    from tensormark_amd.sampler import ROWS_TOPK
+
+    rng = np.random.default_rng(41)
+    B, V, n = 6, 30000, 1100
+    x = rng.normal(0.0, 0.3, (B, V)).astype(np.float32)
+    x[:, :50] += 3.0
+    p = params_array(B, temperature=0.9, top_k=40, top_p=0.95, seed=np.arange(B) + 60)
+    p["top_k"][1] = 0          # flat row: thousands of entries within 40 of the maximum
+    p["top_p"][1] = 0.999
+    p["top_k"][3] = 300
+    p["repeat_penalty"] = 1.1
+    p["repeat_last_n"] = 64
+    recent = rng.integers(0, 80, (B, n)).astype(np.int32)
+    want = orc.sample_batch(x, p, recent=recent, topk_cap=16)
+    out = sampler.sample(torch.from_numpy(x).to("cuda:0"), p, recent=torch.from_numpy(recent).to("cuda:0"),
+                         topk_cap=16, row_kinds=ROWS_TOPK)
+    torch.cuda.synchronize()
+    g = {k: v.cpu().numpy() for k, v in out.items()}
+    assert (g["status"] == 0).all(), g["status"]
+    check(g, want, 16)
 
 
 def test_wide_kernel_rows_with_a_wide_topk_cap(sampler, orc):

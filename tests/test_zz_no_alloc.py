@@ -1,7 +1,7 @@
 """The allocation-free entry point (tms_sample_batch_noalloc) against
 tms_sample_batch: the same outputs, bit for bit, on two calls in a row, the
 second with a smaller batch and vocabulary, each over both row-kind hints
-(the top-k kernel and the general kernel with its whole-row pass)."""
+(the top-k kernel and the general kernel with its whole-row path)."""
 from __future__ import annotations
 
 import numpy as np
@@ -39,10 +39,12 @@ def test_noalloc_matches_context_entry_point(row_kinds):
         for i, w in enumerate(calls):
             p = w["params"].copy()
             if row_kinds == 0:
-                # general kernel: top-p rows, one dense enough for the whole-row pass
+                # general kernel: top-p rows, three dense enough for the
+                # whole-row path (they share the scratch's one region in turn)
                 p["top_k"][::3] = 0
-                w["logits"][1] = np.random.default_rng(i).normal(0, 0.5, w["logits"].shape[1])
-                p["top_k"][1] = 0
+                for r in (1, 4, 7):
+                    w["logits"][r] = np.random.default_rng(10 * i + r).normal(0, 0.5, w["logits"].shape[1])
+                    p["top_k"][r] = 0
             x = w["logits"]
             want = _run(s, x, p, w["recent"], w["mask"], False, 40, row_kinds)
             got = _run(s, x, p, w["recent"], w["mask"], True, 40, row_kinds)
