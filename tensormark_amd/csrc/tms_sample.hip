@@ -1099,7 +1099,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             sm.list_n[lane] = n_c;
             sm.list_s[lane] = m_c;
         }
-        const int N = wave_sum_dpp(n_c);
+        const int incl = wave_incl_scan_i32(n_c);
+        const int N = __shfl(incl, 63, 64);
         int fo = f_c;
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) fo |= __shfl_xor(fo, m, 64);
@@ -1107,7 +1108,6 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         // again and every list fits its staged words.
         const bool fits = lane >= S || n_c <= RT - 1;
         const bool staged = !spec && redo == 0 && __ballot(!fits) == 0ull;
-        const int incl = wave_incl_scan_i32(n_c);
         if (lane < S) sm.hist[lane] = incl - n_c;   // packed offset of each list
         if (lane == 0) {
             sm.misc[5] = N;
@@ -1223,9 +1223,9 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             if (N <= 2 * kBlock) {
                 [[clang::always_inline]] bucket_rank<2>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
             } else if (N <= 4 * kBlock) {
-                [[clang::always_inline]] bucket_rank<4>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
+                bucket_rank<4>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
             } else {
-                [[clang::always_inline]] bucket_rank<kUni / kBlock>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
+                bucket_rank<kUni / kBlock>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
             }
             merged = true;
             lds_sync();
@@ -1281,7 +1281,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             if (total <= 2 * kBlock) {
                 [[clang::always_inline]] bucket_rank<2>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
             } else {
-                [[clang::always_inline]] bucket_rank<kUni / kBlock>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
+                bucket_rank<kUni / kBlock>(uni, total, nkeep, srt, (int*)sm.pbits, sm);
             }
             TMS_TR(12);
             c_next = sm.misc[7];
@@ -1393,7 +1393,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         lds_sync();
         whole = sm.nvalid != 0;
     }
-    if (whole) {
+    if (__builtin_expect(whole, 0)) {
         [[clang::always_inline]] dense_inline<T>(a, row, *reinterpret_cast<DenseLds*>(&sm.big));
     }
 }
