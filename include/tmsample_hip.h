@@ -503,7 +503,9 @@ int tms_debug_philox(const uint32_t* in6, uint32_t* out4, int n, hipStream_t str
  * when two XCDs write halves of one line in one kernel, counts[2] kernels
  * started before their predecessor on the stream finished, counts[3]
  * workgroups w of a 64-workgroup grid not on XCD w mod n, counts[4] the XCD
- * count n. */
+ * count n, counts[5] trials whose roles found no workgroup on their XCD,
+ * counts[6] words lost when each of the two writers reads the line before
+ * writing its half (counts has at least 7 entries). */
 int tms_debug_ordering(int trials, int32_t* counts);
 int tms_debug_exp(const double* in, double* out, int n, int which, hipStream_t stream);
 

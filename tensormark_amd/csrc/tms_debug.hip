@@ -67,6 +67,23 @@ __global__ void line_write(uint64_t* p, uint64_t v, int a, int b, int* claim) {
     for (int i = off; i < 16; i += step) p[i] = v;
 }
 
+// As line_write, but each writer first reads the whole line (plain loads,
+// the line then valid in its XCD's L2) and writes only after its reads
+// returned: the access pattern of a workgroup that reads its neighbours'
+// records of a line and then stores its own.
+__global__ void line_read_write(uint64_t* p, uint64_t v, int a, int b, int* claim, uint64_t* sink) {
+    if (threadIdx.x != 0) return;
+    int off = -1;
+    if (claims(a, claim)) off = 0;
+    else if (claims(b, claim)) off = 1;
+    if (off < 0) return;
+    uint64_t s = 0;
+    for (int i = 0; i < 16; ++i) s += p[i];
+    const uint64_t w = v + (s == 0x5EEDull ? 1u : 0u);   // the stores wait for the loads
+    for (int i = off; i < 16; i += 2) p[i] = w;
+    if (s == 0x5EEDull) sink[0] = s;
+}
+
 // Back to back on one stream: every workgroup of the first kernel counts
 // itself after a short bounded pause; the second reads the count at once.
 __global__ void count_in(unsigned* ctr, int pause) {
@@ -95,9 +112,14 @@ __global__ void xcc_of(int* ids) {
 // counts[3]: workgroups w of a 64-workgroup grid not on XCD w mod (XCD
 //            count), the placement the sampler's row mapping assumes;
 // counts[4]: the XCD count seen;
-// counts[5]: trials of (a) and (b) not run because no workgroup of a grid
-//            landed on an XCD a role needs (the reader's result keeps its
-//            sentinel); they count as neither stale nor lost.
+// counts[5]: trials of (a), (b) and (d) not run because no workgroup of a
+//            grid landed on an XCD a role needs (the reader's result keeps
+//            its sentinel); they count as neither stale nor lost;
+// counts[6]: (d) as (b), but each writer reads the whole line before it
+//            writes its half: lines the next kernel read with a word lost.
+//            No sampler kernel stores into a line it has read with plain
+//            accesses while another workgroup stores into the same line, so
+//            this is reported, not required to be 0.
 // Synchronous; `trials` of each.
 extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
     if (!counts || trials <= 0) return TMS_ERR_INVALID_ARG;
@@ -124,7 +146,7 @@ extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
             rc = TMS_ERR_HIP;
         for (int i = 0; i < kGrid; ++i) nx = std::max(nx, hid[i] + 1);
     }
-    int stale = 0, lost = 0, overlap = 0, placed = 0, not_run = 0;
+    int stale = 0, lost = 0, overlap = 0, placed = 0, not_run = 0, lost_rw = 0;
     constexpr uint64_t kSentinel = ~0ull;   // `out` before a read: no reader ran
     if (rc == TMS_OK) {
         for (int i = 0; i < kGrid; ++i) placed += hid[i] != i % nx;
@@ -153,6 +175,17 @@ extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
                 hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
             if (sum == kSentinel) ++not_run;
             else lost += sum != 16ull * ((uint64_t)it + 1000000);
+            // (d) as (b), each writer reading the line first
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            hipLaunchKernelGGL(tms::line_read_write, dim3(kGrid), dim3(64), 0, s, line, (uint64_t)it + 2000000, 0,
+                               b, claim, out);
+            (void)hipMemsetAsync(claim, 0, 16 * sizeof(int), s);
+            (void)hipMemsetAsync(out, 0xFF, 8, s);
+            hipLaunchKernelGGL(tms::line_read, dim3(kGrid), dim3(64), 0, s, line, c2, claim, out);
+            if (hipMemcpyAsync(&sum, out, 8, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                hipStreamSynchronize(s) != hipSuccess) rc = TMS_ERR_HIP;
+            if (sum == kSentinel) ++not_run;
+            else lost_rw += sum != 16ull * ((uint64_t)it + 2000000);
         }
         // (c) back-to-back kernels
         if (rc == TMS_OK) {
@@ -173,6 +206,7 @@ extern "C" int tms_debug_ordering(int trials, int32_t* counts) {
     counts[3] = placed;
     counts[4] = nx;
     counts[5] = not_run;
+    counts[6] = lost_rw;
     if (s) (void)hipStreamDestroy(s);
     for (void* q : {(void*)line, (void*)out, (void*)claim, (void*)ids, (void*)bad, (void*)ctr})
         if (q) (void)hipFree(q);

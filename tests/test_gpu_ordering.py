@@ -6,6 +6,8 @@ workgroups on different XCDs (each XCD has its own L2) and counts violations:
 a reader kernel that sees a value older than the previous kernel's store, a
 store to one word of a 128-byte line that loses another workgroup's store to a
 neighbouring word, and two kernels on one stream whose executions overlap.
+It also counts lost words when each writer reads the line before writing its
+words: a pattern no sampler kernel uses, reported rather than asserted.
 It also reports the XCD count and whether workgroups land round-robin over
 the XCDs: the launches are shaped for that placement, but it only decides
 their speed, so it is reported, not asserted."""
@@ -30,9 +32,9 @@ def test_device_ordering_facts():
     counts = (C.c_int32 * 8)()
     rc = lib.tms_debug_ordering(64, counts)
     assert rc == 0, lib.tms_status_string(rc)
-    stale, lost, overlap, misplaced, xcds, not_run = list(counts)[:6]
+    stale, lost, overlap, misplaced, xcds, not_run, lost_rw = list(counts)[:7]
     print(f"ordering: stale={stale} lost={lost} overlap={overlap} misplaced={misplaced} xcds={xcds} "
-          f"not_run={not_run}")
+          f"not_run={not_run} lost_after_read={lost_rw}")
     if xcds < 3:
         pytest.skip(f"{xcds} XCD(s): the cross-XCD cases need three")
     assert not_run < 2 * 64, "no trial found its XCD roles"
