@@ -193,7 +193,7 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
 // only tail_topp can decide.  Every thread gets the same value.
 template <typename SM>
 __device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt, int n,
-                               int K, const double* pr, SM& sm) {
+                               int K, const double* pr, uint32_t w0, uint32_t w1, SM& sm) {
     static_assert(kToppCap <= kBlock * 4, "thread blocks of at most 5 entries");
     if (a.topk_cap && a.out_topk_probs) return 2;
     if (n < K && a.topk_cap > n && a.out_topk_ids) return 1;
@@ -293,8 +293,6 @@ __device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tm
             for (int j = 0; j < 5; ++j) mine = j == je ? c[j] : mine;
             sm.theta = __builtin_bit_cast(uint64_t, mine);   // free since the merge
         }
-        uint32_t w0, w1;
-        row_uniform(a, row, P, w0, w1);
         const double u = canonical(w0, w1);
         lds_sync();
         const double sum = __builtin_bit_cast(double, sm.theta);
@@ -975,6 +973,8 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     lds_sync();
     if (!sm.misc[0]) return;
     TMS_TR(5);
+    // The row's draw words, formed while the lists are read.
+    uint32_t rw0 = 0, rw1 = 0;
 
     // ================= merge: the last workgroup of the row =================
     // Top-k rows took each list's header and first r entries (r = K where
@@ -994,6 +994,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     const int RL = stage_log2(S), RT = 1 << RL;   // staged words per list (whole lists)
     uint64_t hv[kUni / kBlock];
     if (spec) {
+        if (mode != MODE_GREEDY) row_uniform(a, row, P, rw0, rw1);
         // Every word read must be set: a ready header, non-zero entries (the
         // writer padded its r slots).  Each thread checks its own words.
         int bad = 0;
@@ -1064,6 +1065,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             hv[u] = (cc < S && cc != c) ? ld_agent(&row_lists[(int64_t)cc * kListStride + jj]) : 0ull;
             if (cc == c) hv[u] = jj == 0 ? hdr : (jj <= nout ? sm.cand[jj - 1] : 0ull);
         }
+        if (mode != MODE_GREEDY) row_uniform(a, row, P, rw0, rw1);
 #pragma unroll
         for (int u = 0; u < kUni / kBlock; ++u) {
             const int idx = t + u * kBlock;
@@ -1201,7 +1203,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         full = sm.misc[1] != 0;
     }
     const int keep_cap = mode == MODE_TOPP ? min(kToppCap, K) : K;
-    bool merged = false;
+    bool merged = false, zeroed = false;
     if (status == TMS_ROW_OK && !spec && !go_dense && sm.misc[6]) {
         // The staged lists, packed in list order into uni; a word inside a
         // list that still reads 0 sends the row to the merge rounds.
@@ -1219,6 +1221,15 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         lds_sync();
         TMS_TR(11);
         if (!sm.misc[2]) {
+            // Every word read is consumed: back to zero for the next call
+            // now (the stores complete under the rank and the tail).
+#pragma unroll
+            for (int u = 0; u < kUni / kBlock; ++u) {
+                const int idx = t + u * kBlock;
+                const int cc = idx >> RL, jj = idx & (RT - 1);
+                if (cc < S && jj <= sm.list_n[cc]) st_agent(&row_lists[(int64_t)cc * kListStride + jj], (uint64_t)0);
+            }
+            zeroed = true;
             n_acc = min(N, keep_cap);
             if (N <= 2 * kBlock) {
                 [[clang::always_inline]] bucket_rank<2>(uni, N, n_acc, srt, (int*)sm.pbits, sm);
@@ -1295,7 +1306,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
     TMS_TR(9);
     const bool defer_zero = status == TMS_ROW_OK && (mode == MODE_TOPK || (mode == MODE_TOPP && !go_dense)) &&
                             !sm.misc[3];
-    if (!defer_zero && !sm.misc[3]) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
+    if (!defer_zero && !sm.misc[3] && !zeroed) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
     TMS_TR(10);
     if (status != TMS_ROW_OK) {
         write_row_error(a, row, status);
@@ -1339,17 +1350,15 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         TMS_TR(7);
         const float mx = ckey_val(srt[0]);
         if (mx == __builtin_huge_valf()) {
-            if (defer_zero) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
+            if (defer_zero && !zeroed) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
             write_row_error(a, row, TMS_ROW_NONFINITE);
             return;
         }
         if (mode == MODE_TOPK) {
             if (wv == 0) {
-                uint32_t w0, w1;
-                row_uniform(a, row, P, w0, w1);
-                [[clang::always_inline]] tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand, w0, w1);
+                [[clang::always_inline]] tail_topk(a, row, P, srt, n, K, (double*)sm.big.m.uni, (double*)sm.cand, rw0, rw1);
             }
-            else
+            else if (!zeroed)
                 zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
             return;
         }
@@ -1373,7 +1382,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             n = min(n, K);   // tmsample::sample sums over the top K only (tmsample.h:185-191)
         }
         TMS_TR(14);
-        const int tp = tail_topp_block(a, row, P, srt, n, K, pr, sm);
+        const int tp = tail_topp_block(a, row, P, srt, n, K, pr, rw0, rw1, sm);
         TMS_TR(15);
         if (tp == 2) {
             // the sequential tail decides (or returns the probabilities)
@@ -1382,12 +1391,12 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
                 bool lost;
                 [[clang::always_inline]] lost = tail_topp(a, row, P, srt, n, K, pr, q);
                 if (lane == 0) sm.nvalid = lost;
-            } else {
+            } else if (!zeroed) {
                 zero_lists(row_lists, S, r, sm.list_n, t - 64, kBlock - 64);
             }
         } else {
             if (t == 0) sm.nvalid = tp;
-            zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
+            if (!zeroed) zero_lists(row_lists, S, r, sm.list_n, t, kBlock);
         }
         TMS_TR(8);
         lds_sync();
