@@ -508,7 +508,7 @@ def test_decisions_on_exact_boundaries(sampler, orc, top_k):
         assert orc.canonical(int(draws[b, 0]), int(draws[b, 1])) == u
     mask = workloads.pack_bits(bits)
     # With 4 or 8 finite entries an 8-slot id list of a top_k = 0 row runs
-    # into the masked ids (-inf, in id order): the whole-row pass lists them.
+    # into the masked ids (-inf, in id order): the whole-row path lists them.
     for cap in (0, 8):
         want = orc.sample_batch(x, p, mask=mask, draws=draws, topk_cap=cap)
         g = run_gpu(sampler, x, p, mask=mask, draws=draws, topk_cap=cap)
@@ -542,7 +542,7 @@ def test_repeated_calls_reuse_workspace(sampler, orc):
 
 def test_dense_row_without_topk(sampler, orc):
     """top_k = 0 over a row whose every entry lies within 40 of the maximum:
-    the whole-row pass (full sort) samples it."""
+    the whole-row path (full sort) samples it."""
     rng = np.random.default_rng(12)
     x = rng.normal(0, 2, (2, 20000)).astype(np.float32)
     p = params_array(2, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(2))
