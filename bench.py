@@ -63,6 +63,9 @@ def parse():
                     help="pass no row-kind hint (the general kernel for every batch)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the in-run HBM traffic measurement (two rocprofv3 counter passes)")
+    ap.add_argument("--rotate-mb", type=int, default=768, metavar="MB",
+                    help="HBM-resident input copies to rotate through, in MB in all (default 768: "
+                         "above the 256 MB MALL)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="first run 3 plain device copies of MIB MiB (a known-size kernel that "
                          "calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -259,7 +262,11 @@ def measure_traffic(args):
     """HBM bytes per launch of the sampler, measured in this run: two child
     runs of this script under rocprofv3 (FETCH_SIZE, then WRITE_SIZE; one
     counter pass each), each with a device copy of 256 MiB first whose
-    counters calibrate the bytes.  Returns (bytes, note) or (None, reason)."""
+    counters calibrate the bytes.  The children rotate over 64 MB of input
+    copies, twice the L2 caches' 32 MB, so every launch misses L2 (the
+    counters count what L2 fetches, MALL hits included) while the copies'
+    set-up stays short under the profiler.  Returns (bytes, note) or (None,
+    reason)."""
     import csv
     import shutil
     import subprocess
@@ -275,7 +282,8 @@ def measure_traffic(args):
         cmd = [prof, "--pmc", ctr, "--output-format", "csv", "-d", out, "-o", "p", "--",
                sys.executable, os.path.abspath(__file__), "--config", str(args.config),
                "--steps", str(steps), "--warmup", str(warm), "--no-cpu", "--eager",
-               "--no-traffic", "--calib-copy", str(mib)] + (["--general"] if args.general else [])
+               "--no-traffic", "--calib-copy", str(mib), "--rotate-mb", "64"] + \
+            (["--general"] if args.general else [])
         env = dict(os.environ, TMPDIR="/tmp")
         try:
             r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True, timeout=300)
@@ -344,7 +352,7 @@ def main():
 
     stream = torch.cuda.Stream(device=dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
-    n_sets = 1 if args.no_rotate else max(1, -(-768 * 2**20 // algo_bytes))
+    n_sets = 1 if args.no_rotate else max(1, -(-args.rotate_mb * 2**20 // algo_bytes))
 
     def up(a_np, view=None):
         t = torch.from_numpy(np.ascontiguousarray(a_np if view is None else a_np.view(view)))
