@@ -704,6 +704,35 @@ def test_whole_lists_over_more_than_16_chunks(orc):
     check(g, want, 16)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_topk_rows_of_a_grid_in_several_rounds(sampler, orc, dtype):
+    """B = 80 rows of V = 262144 (1,280 workgroups of the general kernel, more
+    than four a CU, in two rounds of residency): top-k 1..128 rows with a
+    window, greedy and top-p rows, masked; every row equals the oracle."""
+    rng = np.random.default_rng(81 if dtype == "f32" else 82)
+    B, V = 80, 262144
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    x[:, rng.choice(V, 50, replace=False)] += 8.0
+    recent = rng.integers(0, V, (B, 200)).astype(np.int32)
+    recent[:, ::4] = rng.choice(V, 50)[rng.integers(0, 50, (B, 50))]
+    p = params_array(B, temperature=0.8, top_k=40, top_p=0.95, seed=np.arange(B) + 300,
+                     repeat_penalty=1.2, repeat_last_n=200)
+    p["top_k"] = np.resize([1, 7, 40, 100, 128, 40, 0, 40], B)
+    p["greedy"] = (np.arange(B) % 9 == 4).astype(np.int32)
+    p["min_p"][::5] = 0.05
+    bits = rng.random((B, V)) < 0.8
+    mask = workloads.pack_bits(bits)
+    if dtype == "bf16":
+        xs = workloads.to_bf16_bits(x)
+        xw = workloads.bf16_bits_to_f32(xs)
+    else:
+        xs = xw = x
+    want = orc.sample_batch(xw, p, recent=recent, mask=mask, topk_cap=16)
+    g = run_gpu(sampler, xs, p, recent=recent, mask=mask, topk_cap=16, dtype=dtype)
+    assert (g["status"] == 0).all(), g["status"]
+    check(g, want, 16)
+
+
 def test_whole_row_regions_shared_by_more_rows_than_regions(sampler, orc):
     """300 flat top-p rows, each needing the whole-row path, against the
     context's 256 regions: rows r and r + 256 take turns on one region's
