@@ -1070,18 +1070,16 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         for (int u = 0; u < kUni / kBlock; ++u) {
             const int idx = t + u * kBlock;
             const int cc = idx >> RL, jj = idx & (RT - 1);
-            if (cc < S && jj == 0) {
-                srt[cc] = hv[u];
-                if (!(hv[u] & kReady)) atomicOr((unsigned long long*)&sm.theta, 1ull << cc);
-            }
+            if (cc < S && jj == 0) srt[cc] = hv[u];
         }
         lds_sync();
     }
     uint64_t* hdrs = spec ? uni : srt;   // the headers, stride HW
     const int HW = spec ? R1 : 1;
     if (wv == 0) {
-        // Headers-only mode: wait (bounded) for the lists not yet complete.
-        const uint64_t redo = spec ? 0ull : sm.theta;
+        // Whole-list mode: wait (bounded) for the headers not yet ready
+        // (read from srt after the barrier above; one wave, no atomics).
+        const uint64_t redo = spec ? 0ull : __ballot(lane < S && !(hdrs[lane] & kReady));
         if (lane < S && ((redo >> lane) & 1)) {
             uint64_t h = 0;
             for (int it = 0; it < kPollCap; ++it) {
