@@ -1,9 +1,9 @@
 // tms_dense.h -- the exact full-row form of tmsample::sample
-// (tensormark/tmsample.h:177-200) for the rows the chunked kernels cannot
-// finish from their candidate lists: top-p rows (top_k = 0 or large) whose
+// (tensormark/tmsample.h:177-200) for the rows the general kernel cannot
+// finish from its candidate lists: top-p rows (top_k = 0 or large) whose
 // significant entries (v / T within 40 of the maximum) outnumber the list
-// capacity, a draw that lands past the last significant entry, and rows that
-// break the top-k kernel's row-kind hint.
+// capacity, a draw that lands past the last significant entry, id lists
+// longer than the held entries.
 //
 // The row's merger samples such a row itself, right where it finds it needs
 // the whole row (no second launch): 256 threads of its workgroup, over a
