@@ -247,6 +247,32 @@ def test_packed_stream_rows_vs_oracle(sampler, orc, dtype):
     check(g, want, 24)
 
 
+@pytest.mark.parametrize("V", [32776, 40960, 40968, 61448, 122880])
+def test_packed_stream_chunk_edges(sampler, orc, V):
+    """The packed stream's chunks (20480 ids) against vocabularies at and
+    just past their multiples, where the last chunk holds one vector or
+    the packed form saves a chunk (fp16, no window): greedy, top-k, top-p
+    and min-p rows with a mask; every row equals the oracle."""
+    rng = np.random.default_rng(V)
+    B = 6
+    x32 = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    x32[:, -8:] += 9.0   # the best ids in the last vector
+    x32[2, :8] += 12.0   # or the first
+    xs = x32.astype(np.float16)
+    xw = xs.astype(np.float32)
+    bits = rng.random((B, V)) < 0.7
+    bits[:, -8:] = True
+    mask = workloads.pack_bits(np.pad(bits, ((0, 0), (0, (-V) % 32))))
+    p = params_array(B, temperature=0.9, top_k=40, top_p=0.9, seed=np.arange(B) + 700)
+    p["greedy"][0] = 1
+    p["top_k"] = [40, 1, 40, 128, 0, 0]
+    p["top_p"][5] = 0.2
+    p["min_p"][3] = 0.1
+    want = orc.sample_batch(xw, p, mask=mask, topk_cap=12)
+    g = run_gpu(sampler, xs, p, mask=mask, topk_cap=12, dtype="f16")
+    check(g, want, 12)
+
+
 @pytest.mark.parametrize("n_allowed", [70, 700, 1000])
 def test_topp_rows_many_entries(sampler, orc, n_allowed):
     """Top-p rows (top_k = 0) holding up to 1000 entries within 40 of the
