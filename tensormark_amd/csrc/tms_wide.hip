@@ -472,6 +472,16 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     }
     lds_sync();
     const bool in_chunk = pn.on && t >= from && t < nrec && wid_raw >= e0 && wid_raw < e1;
+    // Every window position in the chunk loads its id's mask word and logit
+    // now, both at once and before the insert, so the owner's copy is in
+    // flight under the insert and the stream (the owner is known only after
+    // the insert; the other positions drop theirs).
+    uint32_t wmw = 0u;
+    float wx = NEG_INF;
+    if (in_chunk) {
+        wmw = mrow[wid_raw >> 5];
+        wx = Elt<T>::scalar(base + wid_raw);
+    }
     bool owner = false;
     int wslot = 0;
     if (in_chunk) {
@@ -490,11 +500,10 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         atomicAdd(&sm.wtab[sl], 1u);
         wslot = sl;
     }
-    // The owner's own copy of its id's masked logit, loaded now and used
-    // after the bound: the streaming thread only takes the id out of the
-    // stream, with no table lookup on its path.
-    float own_x = NEG_INF;
-    if (owner && ((mrow[wid_raw >> 5] >> (wid_raw & 31)) & 1u)) own_x = Elt<T>::scalar(base + wid_raw);
+    // The owner's own copy of its id's masked logit, used after the bound:
+    // the streaming thread only takes the id out of the stream, with no
+    // table lookup on its path.
+    const float own_x = (owner && ((wmw >> (wid_raw & 31)) & 1u)) ? wx : NEG_INF;
     WTR(1);
 
     // ---- pass 1, per slot as it lands: the mask folded into the words (an
