@@ -427,25 +427,34 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
 #pragma unroll
     for (int i = 0; i < kWin; ++i) own_off[i] = -1;
     if (pen_own) {
+        // The counts first, all four positions' atomics issued before any
+        // result is used (a branch on each result would wait out one LDS
+        // round trip per position), then the owners mark their entries.
+        int woff[kWin];
+        uint32_t wold[kWin];
 #pragma unroll
         for (int i = 0; i < kWin; ++i) {
             const int p = t + i * kBlock;
             const int id = (p >= from && p < nrec) ? wid[i] : -1;
             const bool in = id >= e0 && id < e1;
             const int off = in ? id - e0 : 0;
+            woff[i] = in ? off : -1;
             // read for every slot (clamped): the logit and its mask word
             own_v[i] = Elt<T>::scalar(base + e0 + off);
             own_m[i] = mrow[(e0 + off) >> 5];
-            if (in) {
-                const uint32_t sh = (off & 1) * 16;
-                const uint32_t add = ovm ? (uint32_t)(p + 1) : 1u;   // list position + 1, or a count
-                const uint32_t old = atomicAdd(&sm.big.cnt[off >> 1], add << sh);
-                if (((old >> sh) & 0xFFFFu) == 0) {
-                    own_off[i] = off;
-                    const int vv = off / VEC;
-                    const int bit = (vv / kBlock) * VEC + off % VEC;
-                    atomicOr(&sm.pbits[2 * (vv % kBlock) + (bit >> 5)], 1u << (bit & 31));
-                }
+            const uint32_t sh = (off & 1) * 16;
+            const uint32_t add = ovm ? (uint32_t)(p + 1) : 1u;   // list position + 1, or a count
+            wold[i] = 0u;
+            if (in) wold[i] = atomicAdd(&sm.big.cnt[off >> 1], add << sh);
+        }
+#pragma unroll
+        for (int i = 0; i < kWin; ++i) {
+            const int off = woff[i];
+            if (off >= 0 && ((wold[i] >> ((off & 1) * 16)) & 0xFFFFu) == 0) {
+                own_off[i] = off;
+                const int vv = off / VEC;
+                const int bit = (vv / kBlock) * VEC + off % VEC;
+                atomicOr(&sm.pbits[2 * (vv % kBlock) + (bit >> 5)], 1u << (bit & 31));
             }
         }
         lds_sync();
