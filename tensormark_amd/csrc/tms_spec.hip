@@ -335,19 +335,41 @@ __device__ void accept_tests(const SArgs& a, int b, SpecLds& L, int& status, int
         return;
     }
     acc = a.k;
-    for (int i = 0; i < a.k; ++i) {
-        const tms_spec_stat ts = L.srow[i], ds = L.srow[a.k + 1 + i];
-        if (ts.status) { status = ts.status; return; }
-        if (ds.status) { status = ds.status; return; }
-        const int x = L.stok[i];
-        if (x < 0 || x >= a.V) { status = TMS_ROW_BAD_PARAMS; return; }
-        double r;
-        if (ds.ex == 0) r = ts.ex > 0 ? 1.0 : 0.0;
-        else r = ((double)ts.ex * (double)ds.Z) / ((double)ds.ex * (double)ts.Z);
-        if (L.su[i] < r) continue;
+    // Lane i < k of every wave evaluates position i (the same operations as
+    // a loop over i would); the lowest position that is not an accept
+    // decides, as the first exit of that loop would.
+    const int lane = t & 63;
+    int code = 0;   // 0: accepted, 1: rejected, 2: the row's status sv
+    int sv = TMS_ROW_OK;
+    if (lane < a.k) {
+        const tms_spec_stat ts = L.srow[lane], ds = L.srow[a.k + 1 + lane];
+        const int x = L.stok[lane];
+        if (ts.status) {
+            code = 2;
+            sv = ts.status;
+        } else if (ds.status) {
+            code = 2;
+            sv = ds.status;
+        } else if (x < 0 || x >= a.V) {
+            code = 2;
+            sv = TMS_ROW_BAD_PARAMS;
+        } else {
+            double r;
+            if (ds.ex == 0) r = ts.ex > 0 ? 1.0 : 0.0;
+            else r = ((double)ts.ex * (double)ds.Z) / ((double)ds.ex * (double)ts.Z);
+            code = L.su[lane] < r ? 0 : 1;
+        }
+    }
+    const uint64_t stop = __ballot(lane < a.k && code != 0);
+    if (stop) {
+        const int i = __builtin_ctzll(stop);
+        const int ci = __shfl(code, i, 64);
+        if (ci == 2) {
+            status = __shfl(sv, i, 64);
+            return;
+        }
         acc = i;
         rej = i;
-        break;
     }
     if (rej < 0 && !a.lazy && L.srow[a.k].status) status = L.srow[a.k].status;
 }
