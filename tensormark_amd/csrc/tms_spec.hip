@@ -740,6 +740,17 @@ void spec_row_kernel(SArgs a) {
     uint4 q[NS];
 #pragma unroll
     for (int sl = 0; sl < NS; ++sl) q[sl] = *(const uint4*)(row + (int64_t)min(t + sl * kRowT, nv - 1) * VEC);
+    // The draft token's logit (draft rows; target row i takes draft i's
+    // token), loaded now, after the stream's loads: it is in flight under
+    // the max and the sums, and its weight is formed at the end.
+    const int di = i < a.k ? i : (i > a.k ? i - a.k - 1 : -1);
+    bool xin = false;
+    float xv = 0.0f;
+    if (t == 0 && di >= 0) {
+        const int x = a.tokens[(int64_t)b * a.k + di];
+        xin = x >= 0 && x < a.V;
+        if (xin) xv = Elt<T>::scalar(row + x);
+    }
     float mx = -__builtin_huge_valf();
     int nf = 0;
     if (div) row_max<T, NS, kRowT, true>(q, nv, temp, mx, nf);
@@ -756,12 +767,7 @@ void spec_row_kernel(SArgs a) {
         z = div ? row_z<T, NS, kRowT, true>(q, nv, temp, md, L.tab) : row_z<T, NS, kRowT, false>(q, nv, temp, md, L.tab);
     z = block_sum_i64<kRowW>(z, L.shl);
     if (t == 0) {
-        const int di = i < a.k ? i : (i > a.k ? i - a.k - 1 : -1);
-        int64_t ex = 0;
-        if (st == TMS_ROW_OK && di >= 0) {
-            const int x = a.tokens[(int64_t)b * a.k + di];
-            if (x >= 0 && x < a.V) ex = weight(Elt<T>::scalar(row + x), temp, md, L.tab);
-        }
+        const int64_t ex = (st == TMS_ROW_OK && xin) ? weight(xv, temp, md, L.tab) : 0;
         uint64_t* w = (uint64_t*)(a.stats + (int64_t)b * (2 * a.k + 1) + i);
         st_agent(&w[0], (uint64_t)__float_as_uint(mx) | ((uint64_t)(uint32_t)st << 32));
         st_agent(&w[1], (uint64_t)z);
