@@ -65,6 +65,16 @@ __device__ __forceinline__ uint32_t hdr_bound(uint64_t h) { return (uint32_t)h; 
 __device__ __forceinline__ int hdr_n(uint64_t h) { return (int)((h >> 32) & 0xFFFF); }
 __device__ __forceinline__ int hdr_flags(uint64_t h) { return (int)((h >> 48) & 0xFF); }
 
+// Where the window bitmap keeps chunk offset `off`: thread-major, so that the
+// thread that streams an id finds all of its ids' bits in one word.  Slot j,
+// thread t, entry e (off = VEC (j NT + t) + e) is bit j VEC + e of word t.
+template <int VEC, int NT>
+__device__ __forceinline__ void wbit_pos(uint32_t off, uint32_t& word, uint32_t& bit) {
+    const uint32_t r = off % (VEC * NT);
+    word = r / VEC;
+    bit = (off / (VEC * NT)) * VEC + r % VEC;
+}
+
 // First table slot of a chunk offset (multiplicative hash, 11 bits).
 __device__ __forceinline__ int hash_slot(uint32_t off) { return (int)((off * 0x9E3779B1u) >> 21); }
 
@@ -74,7 +84,7 @@ __device__ uint32_t kNoDraws[2] = {0u, 0u};
 __device__ int32_t kNoHistory[1] = {-1};
 
 struct Smem {
-    uint32_t wbits[1024];           // window ids of the chunk, one bit per id (<= 32768 ids)
+    uint32_t wbits[1024];           // window ids of the chunk, thread-major (wbit_pos)
     uint32_t wtab[kHash];           // window ids: chunk offset << kCntBits | occurrences, or kEmpty
     alignas(16) union {
         struct {
@@ -301,8 +311,11 @@ __device__ __forceinline__ int radix_chunk(const T* base, const uint32_t* mrow, 
     const float NEG_INF = -__builtin_huge_valf();
     auto key_at = [&](int id, uint64_t& k) {
         if (!((mrow[id >> 5] >> (id & 31)) & 1u)) return false;
-        const int off = id - e0;
-        if (win && ((sm.wbits[off >> 5] >> (off & 31)) & 1u)) return false;
+        if (win) {
+            uint32_t wd, bt;
+            wbit_pos<16 / sizeof(T), NT>((uint32_t)(id - e0), wd, bt);
+            if ((sm.wbits[wd] >> bt) & 1u) return false;
+        }
         const float v = Elt<T>::scalar(base + id);
         if (!(v > NEG_INF)) return false;
         k = ckey(divide ? v / temp : v, (uint32_t)id);
@@ -377,7 +390,8 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NV = kSlots * VEC;         // stream values per thread
     constexpr int kChunkIds = kT * NV;       // ids a chunk can hold
-    static_assert(kChunkIds / 32 <= 1024, "window bitmap");
+    static_assert(kT <= 1024 && kSlots * VEC <= 32, "window bitmap: a word a thread");
+    static_assert(kT == 1024, "bound: eight lanes a group maximum");
     __shared__ Smem sm;
     const float NEG_INF = -__builtin_huge_valf();
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -461,7 +475,7 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     //      occurrence, then frequency/presence) and offers it as a candidate.
     //      No load beyond the stream.
     if (pn.on) {
-        for (int i = t; i < kChunkIds / 32; i += kT) sm.wbits[i] = 0u;
+        sm.wbits[t] = 0u;
         for (int i = t; i < kHash; i += kT) sm.wtab[i] = kEmpty;
     }
     if (t == 0) {
@@ -486,7 +500,9 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     int wslot = 0;
     if (in_chunk) {
         const uint32_t off = (uint32_t)(wid_raw - e0);
-        atomicOr(&sm.wbits[off >> 5], 1u << (off & 31));
+        uint32_t wd, bt;
+        wbit_pos<VEC, kT>(off, wd, bt);
+        atomicOr(&sm.wbits[wd], 1u << bt);
         int sl = hash_slot(off);
         for (int probe = 0; probe < kHash; ++probe) {   // 2048 slots for at most 1024 ids
             const uint32_t old = atomicCAS(&sm.wtab[sl], kEmpty, off << kCntBits);
@@ -530,19 +546,13 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     //      owner forms the penalised value from its own load); the few
     //      threads holding one form their maximum again.
     if (pn.on) {
-        bool again = false;
+        const uint32_t wt = sm.wbits[t];   // the thread's own ids (bits past the chunk stay 0)
+        if (wt) {   // rare
 #pragma unroll
-        for (int j = 0; j < kSlots; ++j) {
-            const int off = VEC * (j * kT + t);
-            const int lim = e1 - e0 - off;
-            const uint32_t vmask = lim > 0 ? (1u << min(lim, VEC)) - 1u : 0u;
-            const uint32_t wb = (sm.wbits[off >> 5] >> (off & 31)) & vmask;
-            if (wb) {   // rare
-                again = true;
-                raw[j] = fold_bits<T>(raw[j], ~wb & ((1u << VEC) - 1u));
+            for (int j = 0; j < kSlots; ++j) {
+                const uint32_t wb = (wt >> (j * VEC)) & ((1u << VEC) - 1u);
+                if (wb) raw[j] = fold_bits<T>(raw[j], ~wb & ((1u << VEC) - 1u));
             }
-        }
-        if (again) {
             m = NEG_INF;
 #pragma unroll
             for (int j = 0; j < kSlots; ++j)
@@ -569,11 +579,13 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         asm volatile("" : "+v"(raw[j].x), "+v"(raw[j].y), "+v"(raw[j].z), "+v"(raw[j].w));
 
     // ---- bound: the maxima of the 128 groups of G = NT / 128 lanes (DPP,
-    //      on order keys), then the K-th largest of those (wave 0, a
-    //      bisection with ballot counts).  K groups, each with a distinct entry at or above
-    //      it, bound the chunk's K-th value from below.  Per wave this costs
-    //      a few instructions: at two workgroups per CU every instruction all
-    //      waves execute costs about 13 ns.
+    //      on order keys), then the K-th largest of those, found by rank
+    //      counting over every lane.  K groups, each with a distinct entry at
+    //      or above it, bound the chunk's K-th value from below.  The group
+    //      maxima are stored with their low 7 key bits replaced by 127 - the
+    //      group's index, so they are distinct, ties going to the lower
+    //      index; clearing those bits again leaves the K-th largest group
+    //      maximum rounded down by under 2^7 key units, still a lower bound.
     const uint32_t mkey = nf ? 0u : okey(m);
     {
         constexpr int G = kT / 128;
@@ -581,7 +593,8 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         if constexpr (G >= 2) g = max(g, dpp_u32<0x111, 0xF, true>(0u, g));   // row_shr:1
         if constexpr (G >= 4) g = max(g, dpp_u32<0x112, 0xF, true>(0u, g));   // row_shr:2
         if constexpr (G >= 8) g = max(g, dpp_u32<0x114, 0xF, true>(0u, g));   // row_shr:4
-        if ((lane & (G - 1)) == G - 1) sm.gmax[wv * (64 / G) + lane / G] = g;   // lanes Gq .. Gq + G - 1
+        const int gi = wv * (64 / G) + lane / G;
+        if ((lane & (G - 1)) == G - 1) sm.gmax[gi] = (g & ~127u) | (uint32_t)(127 - gi);   // lanes Gq .. Gq + G - 1
     }
     const uint64_t nfw = __ballot(nf);
     if (lane == 0) sm.wnf[wv] = nfw ? 1 : 0;
@@ -595,29 +608,26 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
             flags |= (q.x | q.y | q.z | q.w) ? FLAG_NONFINITE : 0;
         }
     }
-    if (!skip && (wv == 0 || (wv == 1 && S > 1))) {
-        // wave 0: the chunk's bound for K groups; wave 1, meanwhile: for
-        // ceil(K / S) groups (S chunks holding that many each hold K), which
-        // only the merger's pruning uses, to 16 bits
-        const uint32_t g0 = sm.gmax[lane], g1 = sm.gmax[lane + 64];
-        // the top 20 key bits: the bound rounds down to a multiple of 2^12
-        // (at most 2^-11 relative below the exact K-th group maximum), which
-        // keeps it a lower bound
-        auto bisect = [&](auto lo, int kg) {
-            uint32_t th = 0;
+    if (!skip) {
+        // group maximum i = t / 8 is ranked by its eight lanes, lane p
+        // counting the larger ones among groups 16p .. 16p + 15; the one of
+        // rank K - 1 is the bound (and the one of rank ceil(K / S) - 1, to
+        // 16 bits, the bound for ceil(K / S) groups, which only the
+        // merger's pruning uses)
+        const int gi = t >> 3, p = t & 7;
+        const uint32_t x = sm.gmax[gi];
+        const uint4* g4 = (const uint4*)(sm.gmax + 16 * p);
+        uint4 y[4];
 #pragma unroll
-            for (int bit = 31; bit >= decltype(lo)::value; --bit) {
-                const uint32_t cand = th | (1u << bit);
-                if (__popcll(__ballot(g0 >= cand)) + __popcll(__ballot(g1 >= cand)) >= kg) th = cand;
-            }
-            return th;
-        };
-        if (wv == 0) {
-            const uint32_t th = bisect(std::integral_constant<int, 12>{}, K);
-            if (lane == 0) sm.tkey = th;
-        } else {
-            const uint32_t th = bisect(std::integral_constant<int, 16>{}, (K + S - 1) / S);
-            if (lane == 0) sm.tkey_rm = th;
+        for (int q = 0; q < 4; ++q) y[q] = g4[q];
+        int r = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            r += (y[q].x > x ? 1 : 0) + (y[q].y > x ? 1 : 0) + (y[q].z > x ? 1 : 0) + (y[q].w > x ? 1 : 0);
+        r = group_sum(r, 8);
+        if (p == 0) {
+            if (r == K - 1) sm.tkey = x & ~127u;
+            if (S > 1 && r == (K + S - 1) / S - 1) sm.tkey_rm = x & 0xFFFF0000u;
         }
     }
     lds_sync();
