@@ -17,10 +17,11 @@
 //             frequency/presence).
 //   pass 1    per 16-byte slot: mask bit (and not a window id) -> value,
 //             else -inf; the thread's maximum; NaN / +inf flagged.
-//   bound     the maxima of 128 groups of lanes (DPP); wave 0 bisects for the
-//             K-th largest, which bounds the chunk's K-th value from below (K
-//             groups, each with a distinct entry, reach it); wave 1 does the
-//             same for ceil(K / S) groups, for the merger's pruning.
+//   bound     the maxima of 128 groups of lanes (DPP), ranked by counting on
+//             every lane (eight lanes a group maximum); the K-th largest
+//             bounds the chunk's K-th value from below (K groups, each with a
+//             distinct entry, reach it); the ceil(K / S)-th largest gives the
+//             merger's pruning bound.
 //   select    every entry whose v / T can reach the bound's quotient is a
 //             candidate (the division runs on candidates only): hot lanes
 //             stage their words in LDS and each wave appends its takes.  Up
@@ -389,7 +390,6 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     static_assert(kW * kSlots <= kWaveSlots, "hot-lane staging");
     constexpr int VEC = Elt<T>::kVec;
     constexpr int NV = kSlots * VEC;         // stream values per thread
-    constexpr int kChunkIds = kT * NV;       // ids a chunk can hold
     static_assert(kT <= 1024 && kSlots * VEC <= 32, "window bitmap: a word a thread");
     static_assert(kT == 1024, "bound: eight lanes a group maximum");
     __shared__ Smem sm;
