@@ -53,7 +53,7 @@ constexpr int kHot = 8;             // lanes a wave examines from LDS (more: eve
 constexpr int kCap = 1024;          // chunk candidates held in LDS
 constexpr int kPad = 256;           // slack after a ranked list (rank_place reads past it)
 constexpr int kList = 128;          // a chunk's candidates published unranked up to this many
-constexpr int kMW = 4;             // waves of the merge after the compaction (one a SIMD)
+constexpr int kMW = 8;             // waves of the merge after the compaction (two a SIMD)
 static_assert(kLStride >= 1 + kKMax && kLStride >= 1 + kList && kList >= kKMax && kList <= 128, "list layout");
 
 // Header word: ready bit, flags (bits 48-55), list length (bits 32-47),
@@ -843,10 +843,12 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
     if (t == 0 && S > 1) st_agent(&a.counters[row * kCounterStride], 0u);
     if (wv < S && lane == 0) sm.mn[wv] = ncc;
     lds_sync();
-    // From here the merge runs on waves 0 .. max(S, 4) - 1 (the list holders
-    // for the compaction, four for the rank), then on waves 0 .. 3: the
-    // others leave, so each instruction of the merge is issued by at most a
-    // wave or so a SIMD instead of four.
+    // From here the merge runs on waves 0 .. max(S, kMW) - 1 (the list
+    // holders for the compaction, eight for the rank), then on waves
+    // 0 .. kMW - 1: the others leave, so each instruction of the merge is
+    // issued by two waves or so a SIMD instead of four.  Eight rank a short
+    // list in half the dependent LDS reads of four (0.15 us on config 2);
+    // all sixteen were slower again.
     if (wv >= (S > kMW ? S : kMW)) return;
 
     WTR(7);
