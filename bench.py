@@ -334,7 +334,7 @@ def main():
     import torch
 
     from tensormark_amd import Sampler
-    from tensormark_amd.sampler import ROWS_ANY, row_kinds_of
+    from tensormark_amd.sampler import ROWS_ANY, ROWS_SPARSE_MASK, mask_is_sparse, row_kinds_of
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
@@ -359,6 +359,7 @@ def main():
         return t.to(dev)
 
     keep = []   # device buffers the argument records point at
+    kinds_name = None
     if args.config == 4:
         from tensormark_amd.sampler import SpecArgs
 
@@ -390,8 +391,15 @@ def main():
         mask0 = None if w.get("mask") is None else up(w["mask"], np.int32)
         s = Sampler(B, V)
         params = s.params_tensor(w["params"])
-        # the caller's row-kind hint, from the host-side parameters
-        kinds = ROWS_ANY if args.general else row_kinds_of(w["params"])
+        # the caller's row-kind hint, from the host-side parameters and masks
+        # (a grammar engine knows how many ids each mask allows)
+        if args.general:
+            kinds = ROWS_ANY
+        elif w.get("mask") is not None and mask_is_sparse(w["mask"]):
+            kinds = ROWS_SPARSE_MASK
+        else:
+            kinds = row_kinds_of(w["params"])
+        kinds_name = {0: "any", 1: "topk", 2: "sparse_mask"}[kinds]
         out = {n: torch.empty(B, dtype=torch.int32, device=dev) for n in ("tokens", "status", "keep")}
         recs = []
         for i in range(n_sets):
@@ -463,6 +471,7 @@ def main():
         "dtype": dt_name,
         "data": "synthetic (seeded numpy; no model)",
         "config": {"workload": name, "batch": B, "vocab": V, "launch": "graph" if graph else "eager",
+                   "row_kinds": kinds_name,
                    "input_sets": n_sets, "hbm_resident_bytes": n_sets * algo_bytes,
                    "wall_s": round(wall, 4)},
         "hbm_gbps": round(achieved / 1e9, 1),

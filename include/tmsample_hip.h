@@ -83,8 +83,20 @@ enum {
 /* tms_sample_args.row_kinds: what the caller knows of its rows. */
 enum {
     TMS_ROWS_ANY = 0,    /* no promise: the general kernel */
-    TMS_ROWS_TOPK = 1    /* every row greedy, or top-k with 1 <= top_k <= 128 */
+    TMS_ROWS_TOPK = 1,   /* every row greedy, or top-k with 1 <= top_k <= 128 */
+    TMS_ROWS_SPARSE_MASK = 2   /* the masks allow few ids a row (at most
+                                  TMS_SPARSE_MAX_IDS expected): only the allowed
+                                  logits are read.  Any row kind; a row with more
+                                  allowed ids is still sampled exactly, over the
+                                  whole row and more slowly.  Taken when `mask` is
+                                  given, `history` is not, and vocab <=
+                                  TMS_SPARSE_MAX_VOCAB; otherwise the general
+                                  kernel */
 };
+
+/* Allowed ids a row the sparse-mask kernel holds, and its largest vocab. */
+#define TMS_SPARSE_MAX_IDS 2048
+#define TMS_SPARSE_MAX_VOCAB 262144
 
 enum {
     TMS_DTYPE_F32 = 0,
@@ -166,7 +178,8 @@ typedef struct tms_sample_args {
                                  top-k ids, -1 padded */
     float* out_topk_probs;    /* device, [batch][topk_cap], nullable:
                                  pr / z of the same entries */
-    uint32_t row_kinds;       /* TMS_ROWS_ANY, or TMS_ROWS_TOPK: the caller promises
+    uint32_t row_kinds;       /* TMS_ROWS_SPARSE_MASK: see the enum.
+                                 TMS_ROWS_ANY, or TMS_ROWS_TOPK: the caller promises
                                  every row is greedy or has 1 <= top_k <= 128, and
                                  the library may take its top-k kernel (it does when
                                  batch x chunks <= 1024 workgroups).  Every other

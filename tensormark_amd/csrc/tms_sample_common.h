@@ -55,6 +55,8 @@ constexpr int kPollCap = 1 << 20;          // bound on the merger's wait per lis
 constexpr int kReadRounds = 64;            // bound on the merger's re-reads of a sample
 constexpr int kDenseSlotsMax = 256;        // whole-row regions of a context
 constexpr int kHistMax = TMS_HISTORY_MAX_IDS; // ids one row's history pre-pass may list
+constexpr int kSparseMaxVocab = TMS_SPARSE_MAX_VOCAB;   // vocab of the sparse-mask kernel (its mask in LDS)
+static_assert(kUni == TMS_SPARSE_MAX_IDS, "the sparse-mask kernel holds kUni ids");
 
 enum : int { MODE_GREEDY = 0, MODE_TOPK = 1, MODE_TOPP = 2 };
 enum : int { FLAG_NONFINITE = 1, FLAG_OVERFLOW = 2 };
@@ -745,6 +747,8 @@ __device__ __forceinline__ int wave_min_nonneg(int v) {
 
 // Launches the wide top-k kernel (tms_wide.hip) over `batch` rows.
 int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream);
+// Launches the sparse-mask kernel (tms_sparse.hip), one workgroup a row.
+int tms_launch_sparse(const tms::KArgs& k, int dtype, int batch, hipStream_t stream);
 int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,
                        const float* dry_scale, int64_t dry_scale_stride, int dtype, int batch,
                        int32_t* ov_n, int32_t* ov_ids, float* ov_vals, hipStream_t stream);

@@ -23,7 +23,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmsample_hip.so")
 
 TMS_OK = 0
-ROWS_ANY, ROWS_TOPK = 0, 1
+ROWS_ANY, ROWS_TOPK, ROWS_SPARSE_MASK = 0, 1, 2
 ROW_OK, ROW_BAD_PARAMS, ROW_ALL_MASKED, ROW_NONFINITE, ROW_UNSUPPORTED = 0, 1, 2, 3, 4
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -227,6 +227,18 @@ def row_kinds_of(params: np.ndarray) -> int:
     return ROWS_TOPK if bool(np.all(ok)) else ROWS_ANY
 
 
+SPARSE_MAX_IDS = 2048   # TMS_SPARSE_MAX_IDS
+
+
+def mask_is_sparse(mask: np.ndarray) -> bool:
+    """Whether every row of a host [B, W] uint32 allowed-bit mask allows at
+    most SPARSE_MAX_IDS ids: the caller's ground for ROWS_SPARSE_MASK (a
+    grammar engine knows each row's allowed count when it builds the mask)."""
+    m = np.ascontiguousarray(mask, dtype=np.uint32)
+    counts = np.unpackbits(m.view(np.uint8), axis=1).sum(axis=1)
+    return bool(np.all(counts <= SPARSE_MAX_IDS))
+
+
 def load_library(path: str = LIB_PATH) -> C.CDLL:
     """Load the HIP library; raises if it was not built."""
     global _LIB
@@ -399,7 +411,7 @@ class Sampler:
 
         ``params`` is a device uint8 tensor from params_tensor() (or a numpy
         ROW_DTYPE array, uploaded here).  ``row_kinds`` is the hint of
-        tms_sample_args (ROWS_ANY / ROWS_TOPK); by default it is derived from
+        tms_sample_args (ROWS_ANY / ROWS_TOPK / ROWS_SPARSE_MASK); by default it is derived from
         numpy params (ROWS_ANY for device params), and a Sampler created with
         kernel="general" always passes ROWS_ANY.  ``noalloc`` takes the
         context-free entry point tms_sample_batch_noalloc (its static
