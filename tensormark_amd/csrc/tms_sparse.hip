@@ -235,22 +235,42 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
     }
 
     // ---- the allowed ids in entry order (thread, then word), then their
-    //      logits; with a window, each word and its first entry index go to
-    //      LDS for the history lookups
+    //      logits.  Word i of every lane in turn: each lane whose word is
+    //      non-zero is expanded by the whole wave, half-wave by half-wave
+    //      (lane j of a half takes bit j), so no lane loops over its bits.
+    //      With a window, each word and its first entry index go to LDS for
+    //      the history lookups.
     {
         int e = tb;
+        const int half = lane >> 5, bitj = lane & 31;
 #pragma unroll
         for (int i = 0; i < kWpt; ++i) {
             const int w = t + i * kNT;
-            uint32_t x = mwr[i];
+            const uint32_t x = mwr[i];
             if (pn.on && w < W) {
                 sm.mw[w] = x;
                 sm.wpre[w] = (uint16_t)e;
             }
-            while (x) {
-                sm.ids[e++] = (uint32_t)(w * 32 + __builtin_ctz(x));
-                x &= x - 1u;
+            uint64_t nz = __ballot(x != 0u);
+            while (nz) {
+                // up to two non-zero lanes at once: the lowest to half 0,
+                // the next to half 1
+                const int l0 = __builtin_ctzll(nz);
+                nz &= nz - 1ull;
+                const int l1 = nz ? __builtin_ctzll(nz) : l0;
+                if (nz) nz &= nz - 1ull;
+                const int src = half ? l1 : l0;
+                const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)x, l0);
+                const uint32_t x1 = (uint32_t)__builtin_amdgcn_readlane((int)x, l1);
+                const int e0 = __builtin_amdgcn_readlane(e, l0), e1 = __builtin_amdgcn_readlane(e, l1);
+                const uint32_t xs = half ? x1 : x0;
+                const int es = half ? e1 : e0;
+                const bool take = (half == 0 || l1 != l0) && ((xs >> bitj) & 1u);
+                if (take)
+                    sm.ids[es + __popc(xs & ((1u << bitj) - 1u))] =
+                        (uint32_t)(((src + (wv << 6) + i * kNT) << 5) + bitj);
             }
+            e += __popc(x);
         }
     }
     if (pn.on)
