@@ -86,3 +86,25 @@ def test_ctypes_layouts_match_the_c_header(tmp_path):
     assert int(got["tms_history_params"]) == sampler.HISTORY_DTYPE.itemsize
     for f in sampler.HISTORY_DTYPE.names:
         assert int(got[f"tms_history_params.{f}"]) == sampler.HISTORY_DTYPE.fields[f][1], f
+
+
+def test_row_kind_constants_and_sparse_mask_hint():
+    """The Python mirrors of the row-kind enum and the sparse-mask limit equal
+    the header's, and mask_is_sparse counts allowed ids per row (the hint a
+    caller derives from its host masks)."""
+    src = open(os.path.join(ROOT, "include", "tmsample_hip.h")).read()
+    assert re.search(r"TMS_ROWS_SPARSE_MASK\s*=\s*(\d+)", src).group(1) == str(sampler.ROWS_SPARSE_MASK)
+    assert re.search(r"TMS_ROWS_TOPK\s*=\s*(\d+)", src).group(1) == str(sampler.ROWS_TOPK)
+    assert re.search(r"#define TMS_SPARSE_MAX_IDS\s+(\d+)", src).group(1) == str(sampler.SPARSE_MAX_IDS)
+    import numpy as np
+
+    from tensormark_amd import workloads
+
+    bits = np.zeros((3, 4096), bool)
+    bits[0, :2048] = True          # exactly the limit
+    bits[1, ::2] = True            # 2048 again, spread out
+    bits[2, :10] = True
+    assert sampler.mask_is_sparse(workloads.pack_bits(bits))
+    bits[2, :2049] = True          # one row past it
+    assert not sampler.mask_is_sparse(workloads.pack_bits(bits))
+    assert sampler.mask_is_sparse(workloads.cfg3()["mask"])
