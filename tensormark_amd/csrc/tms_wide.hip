@@ -516,51 +516,38 @@ __attribute__((amdgpu_waves_per_eu(kSlots == 4 ? 8 : NT / 256, 8))) void topk_wi
         atomicAdd(&sm.wtab[sl], 1u);
         wslot = sl;
     }
-    // The owner's own copy of its id's masked logit, used after the bound:
-    // the streaming thread only takes the id out of the stream, with no
-    // table lookup on its path.
-    const float own_x = (owner && ((wmw >> (wid_raw & 31)) & 1u)) ? wx : NEG_INF;
+    // The window table is complete before the stream lands (the history
+    // positions were loaded first): each thread reads the bits of its own
+    // entries once, and pass 1 takes window ids out with the mask.
+    uint32_t wt = 0u;
+    if (pn.on) {
+        lds_sync();
+        wt = sm.wbits[t];   // bits past the chunk stay 0
+    }
     WTR(1);
 
-    // ---- pass 1, per slot as it lands: the mask folded into the words (an
-    //      entry the mask leaves out becomes the -inf pattern of its type in
-    //      place), and the thread's IEEE maximum, which keeps a NaN, so one
-    //      test of it finds any NaN or +inf.  Two to three instructions an
-    //      entry: at two workgroups per CU every per-entry instruction costs
-    //      the CU 32 K lane slots.  Pass 1 reads no LDS, so it does not wait
-    //      for the window table.
+    // ---- pass 1, per slot as it lands: the mask and the window ids folded
+    //      into the words (an entry the mask leaves out, or a window id,
+    //      becomes the -inf pattern of its type in place; a window id's owner
+    //      forms its penalised value from its own load), and the thread's
+    //      IEEE maximum, which keeps a NaN, so one test of it finds any NaN
+    //      or +inf.  Two to three instructions an entry.
     float m = NEG_INF;
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
         const int off = VEC * (j * kT + t);
         const int lim = e1 - e0 - off;   // ids of this slot inside the chunk
         const uint32_t vmask = lim > 0 ? (1u << min(lim, VEC)) - 1u : 0u;
-        raw[j] = fold_bits<T>(raw[j], (mw[j] >> (off & 31)) & vmask);
+        raw[j] = fold_bits<T>(raw[j], (mw[j] >> (off & 31)) & vmask & ~(wt >> (j * VEC)));
 #pragma unroll
         for (int e = 0; e < VEC; e += 2)
             m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(elt<T>(raw[j], e), elt<T>(raw[j], e + 1)));
     }
     WTRD(16, m);
-    lds_sync();   // the window table is complete
-    // ---- window ids out of the stream: each becomes -inf in place (its
-    //      owner forms the penalised value from its own load); the few
-    //      threads holding one form their maximum again.
-    if (pn.on) {
-        const uint32_t wt = sm.wbits[t];   // the thread's own ids (bits past the chunk stay 0)
-        if (wt) {   // rare
-#pragma unroll
-            for (int j = 0; j < kSlots; ++j) {
-                const uint32_t wb = (wt >> (j * VEC)) & ((1u << VEC) - 1u);
-                if (wb) raw[j] = fold_bits<T>(raw[j], ~wb & ((1u << VEC) - 1u));
-            }
-            m = NEG_INF;
-#pragma unroll
-            for (int j = 0; j < kSlots; ++j)
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) m = __builtin_elementwise_maximum(m, elt<T>(raw[j], e));
-        }
-    }
     WTRD(17, m);
+    // The owner's own copy of its id's masked logit, used after the bound
+    // (its load was issued after the stream's, so it is read after pass 1).
+    const float own_x = (owner && ((wmw >> (wid_raw & 31)) & 1u)) ? wx : NEG_INF;
     const bool nf = !(m < __builtin_huge_valf()) && m != NEG_INF;   // NaN or +inf
     // The row's ticket, now that the chunk's data is in: its round trip
     // overlaps the selection.  The last chunk of the row to get here merges;
