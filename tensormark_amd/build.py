@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libtmsample_hip.so")
-SOURCES = ["tms_sample.hip", "tms_wide.hip", "tms_sparse.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
+SOURCES = ["tms_sample.hip", "tms_wide.hip", "tms_sparse.hip", "tms_rows.hip", "tms_hist.hip", "tms_chain.hip", "tms_spec.hip", "tms_debug.hip", "tms_history.cpp", "tms_grammar.cpp", "tms_filter.cpp"]
 
 # -ffp-contract=off keeps every a*b+c as two rounded operations, so the
 # device arithmetic matches the host checker bit for bit.  Packed-FP32 ops
@@ -65,7 +65,7 @@ def _run(cmd: list, verbose: bool) -> str:
 # one read of the row into scratch traffic; the general kernel launched its
 # workgroups measurably slower with any scratch (B = 1024, V = 256000 bf16:
 # 243.5 against 232.3 us with 32 bytes a lane).
-NO_SCRATCH = ("tms_wide.hip", "tms_spec.hip", "tms_sample.hip", "tms_sparse.hip")
+NO_SCRATCH = ("tms_wide.hip", "tms_spec.hip", "tms_sample.hip", "tms_sparse.hip", "tms_rows.hip")
 
 
 def _check_no_scratch(src: str, remarks: str) -> None:

@@ -516,4 +516,79 @@ __device__ void dense_inline(const KArgs& a, int row, DenseLds& L) {
     if (threadIdx.x == 0) __hip_atomic_store(&a.dlocks[slot], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Greedy over the whole row, for a kernel that cannot hold the row's
+// candidates: the largest key of the penalised value (no temperature),
+// lowest id among equals, NaN / +inf and all-masked rows reported; window
+// counts (positions [from, nrec) of the row's history) in a region of the
+// workspace taken by its lock.  The first 256 threads of the workgroup.
+template <typename T>
+__device__ void dense_greedy(const KArgs& a, int row, const Pen& pn0, int from, int nrec, DenseLds& L) {
+    const int t = threadIdx.x;
+    const int V = a.V;
+    const T* base = (const T*)a.logits + (int64_t)row * a.row_stride;
+    const uint32_t* mrow = a.mask + (int64_t)row * a.mask_stride;
+    Pen pn = pn0;
+    int slot = -1;
+    if (pn.on) {
+        if (!a.dense) {
+            write_row_error(a, row, TMS_ROW_UNSUPPORTED);
+            return;
+        }
+        if (t == 0) L.misc[7] = take_dense_slot(a.dlocks, a.dense_slots, row);
+        dense_sync();
+        slot = L.misc[7];
+        dense_sync();
+        if (slot < 0) {
+            write_row_error(a, row, TMS_ROW_INTERNAL);
+            return;
+        }
+    }
+    uint32_t* C = pn.on ? (uint32_t*)(a.dense + (int64_t)slot * 2 * a.dense_stride) : nullptr;
+    if (pn.on) dense_count_window(C, V, a.recent + (int64_t)row * a.recent_stride, from, nrec, false);
+    uint64_t best = 0ull;
+    int bad = 0;
+    for (int i = t; i < V; i += kBlock) {
+        const float v = dense_lg(base, mrow, C, i, pn, 1.0f, false);
+        bad |= __builtin_amdgcn_class(v, 0x203);   // NaN or +inf
+        if (v != -__builtin_huge_valf()) {
+            const uint64_t k = ckey(v, (uint32_t)i);
+            best = k > best ? k : best;
+        }
+    }
+    if (pn.on) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        dense_sync();
+        if (t == 0) __hip_atomic_store(&a.dlocks[slot], 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    best = wave_max_u64_dpp(best);
+    bad = __any(bad != 0);
+    if ((t & 63) == 0) {
+        L.wave_d[t >> 6] = __longlong_as_double((long long)best);
+        L.wave_i[t >> 6] = bad;
+    }
+    dense_sync();
+    uint64_t b = 0ull;
+    int anyb = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const uint64_t x = (uint64_t)__double_as_longlong(L.wave_d[w]);
+        b = x > b ? x : b;
+        anyb |= L.wave_i[w];
+    }
+    if (anyb || b == 0ull) {
+        write_row_error(a, row, anyb ? TMS_ROW_NONFINITE : TMS_ROW_ALL_MASKED);
+        return;
+    }
+    const int tok = (int)ckey_id(b);
+    if (t == 0) {
+        a.out_tokens[row] = tok;
+        a.out_status[row] = TMS_ROW_OK;
+        if (a.out_keep) a.out_keep[row] = 0;
+    }
+    for (int i = t; i < a.topk_cap; i += kBlock) {
+        if (a.out_topk_ids) a.out_topk_ids[(int64_t)row * a.topk_cap + i] = i == 0 ? tok : -1;
+        if (a.out_topk_probs) a.out_topk_probs[(int64_t)row * a.topk_cap + i] = i == 0 ? 1.0f : 0.0f;
+    }
+}
+
 }  // namespace tms

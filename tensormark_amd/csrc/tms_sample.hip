@@ -683,6 +683,24 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
         }
         if (!anynf && !bad_params && (fallback || n > kCand)) {
             if (mode == MODE_TOPK) {
+                if (pn.on) {
+                    // The candidate staging wrote over the window counts in
+                    // sm.big; the radix select reads the penalised values
+                    // through them, so they are counted again.
+                    uint4* c4 = (uint4*)sm.big.cnt;
+                    lds_sync();
+                    for (int i = t; i < kChunk / 8; i += kBlock) c4[i] = make_uint4(0, 0, 0, 0);
+                    lds_sync();
+                    for (int p = from + t; p < nrec; p += kBlock) {
+                        const int id = hist[p];
+                        if (id >= e0 && id < e1) {
+                            const int off = id - e0;
+                            const uint32_t add = ovm ? (uint32_t)(p + 1) : 1u;
+                            atomicAdd(&sm.big.cnt[off >> 1], add << ((off & 1) * 16));
+                        }
+                    }
+                    lds_sync();
+                }
                 nout = radix_slow<T>(base, mrow, e0, e1, K, temp, divide, pn.on, pn.rep_on, pn.fp_on, pn.rep,
                                      pn.freq, pn.pres, pn.ov, sm);
                 [[clang::always_inline]] sort_cand(nout, sm);
@@ -1447,6 +1465,12 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
                 return tms_launch_wide(kw, a->dtype, fast, a->batch, slots, stream);
             }
         }
+    }
+    if (a->row_kinds == TMS_ROWS_TOPK && fast && (!a->recent || a->recent_stride <= 1024) &&
+        a->batch >= device_cus()) {
+        // Top-k batches with a row for every CU: one workgroup a row streams
+        // the whole row (B = 1024, V = 256000 bf16: no chunk merges).
+        return tms_launch_rows(k, a->dtype, a->batch, stream);
     }
     // Everything else, including top-k batches whose grid does not fit the
     // wide kernel's residency: the general kernel.  Aligned 2-byte rows

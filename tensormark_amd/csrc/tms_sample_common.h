@@ -747,6 +747,8 @@ __device__ __forceinline__ int wave_min_nonneg(int v) {
 
 // Launches the wide top-k kernel (tms_wide.hip) over `batch` rows.
 int tms_launch_wide(const tms::KArgs& k, int dtype, bool fast, int batch, int slots, hipStream_t stream);
+// Launches the row-stream kernel (tms_rows.hip), one workgroup a row.
+int tms_launch_rows(const tms::KArgs& k, int dtype, int batch, hipStream_t stream);
 // Launches the sparse-mask kernel (tms_sparse.hip), one workgroup a row.
 int tms_launch_sparse(const tms::KArgs& k, int dtype, int batch, hipStream_t stream);
 int tms_launch_history(const tms::KArgs& k, const tms_history_params* hp, const uint8_t* breaker,

@@ -145,26 +145,6 @@ struct Smem {
 #define WTV(i, val) ((void)0)
 #endif
 
-// 16-byte nontemporal load: the logits are read exactly once per call.
-__device__ __forceinline__ uint4 ld_nt(const void* p) {
-    typedef unsigned u4v __attribute__((ext_vector_type(4)));
-    const u4v q = __builtin_nontemporal_load((const u4v*)p);
-    return make_uint4(q.x, q.y, q.z, q.w);
-}
-
-// Element e of a 16-byte slot, widened exactly to fp32.
-template <typename T>
-__device__ __forceinline__ float elt(const uint4& q, int e) {
-    if constexpr (sizeof(T) == 4) {
-        return __uint_as_float(e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w);
-    } else {
-        const uint32_t w = (e >> 1) == 0 ? q.x : (e >> 1) == 1 ? q.y : (e >> 1) == 2 ? q.z : q.w;
-        const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
-        if constexpr (__is_same(T, Bf16)) return __uint_as_float(h << 16);
-        else return Elt<_Float16>::h2f(h);
-    }
-}
-
 // Reductions over the 64 lanes of a wave by DPP (no LDS round trips):
 // butterflies within 16-lane rows (quad_perm, half-row and row mirrors),
 // then across rows (row_bcast:15 and :31 towards lane 63, read there).
@@ -359,27 +339,6 @@ __device__ __forceinline__ int radix_chunk(const T* base, const uint32_t* mrow, 
     lds_sync();
     return min(sm.ncand, K);
 }
-
-// The entries of a 16-byte slot whose bit in `bits` is clear become the
-// -inf pattern of their type (two instructions a 32-bit word).
-template <typename T>
-__device__ __forceinline__ uint4 fold_bits(const uint4& q, uint32_t bits) {
-    constexpr int VEC = Elt<T>::kVec;
-    uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t keep;
-        if constexpr (VEC == 4) {
-            keep = (uint32_t)__builtin_amdgcn_sbfe((int)bits, i, 1);
-        } else {
-            keep = ((uint32_t)__builtin_amdgcn_sbfe((int)bits, 2 * i, 1) & 0xFFFFu) |
-                   ((uint32_t)__builtin_amdgcn_sbfe((int)bits, 2 * i + 1, 1) << 16);
-        }
-        w[i] = (w[i] & keep) | (Elt<T>::kNegInfWord & ~keep);
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
 
 // NT threads of kSlots 16-byte slots each: (1024, 4) two workgroups per
 // CU; (1024, 8), fp32, one workgroup per CU.
