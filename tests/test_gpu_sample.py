@@ -854,3 +854,35 @@ def test_tie_fixture_rows(sampler, orc):
         want = orc.sample_batch(x, prm, draws=draws, topk_cap=k)
         got = run_gpu(sampler, x, prm, draws=draws, topk_cap=k)
         check(got, want, k)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_massive_ties_with_window_penalties(sampler, orc, dtype):
+    """Rows whose entries all tie, with window penalties: the chunk's
+    candidates overflow and its exact radix select reads the penalised values
+    through the window counts, which it counts again (the candidate staging
+    shares their LDS).  Top-k 100 at T = 2.5: the top 100 are the lowest
+    allowed ids outside the window."""
+    rng = np.random.default_rng({"f32": 61, "f16": 62, "bf16": 63}[dtype])
+    B, V = 4, 40000
+    x32 = np.full((B, V), 1.25, np.float32)
+    x32[1, 1::2] = 1.0
+    if dtype == "f16":
+        xs = x32.astype(np.float16)
+    elif dtype == "bf16":
+        xs = workloads.to_bf16_bits(x32)
+    else:
+        xs = x32
+    bits = rng.random((B, ((V + 31) // 32) * 32)) < 0.85
+    bits[:, V:] = False
+    mask = workloads.pack_bits(bits)
+    recent = rng.integers(0, 200, (B, 512)).astype(np.int32)
+    p = params_array(B, temperature=2.5, top_k=100, top_p=0.9, seed=np.arange(B) + 77)
+    p["repeat_penalty"] = [1.05, 1.3, 1.0, 1.05]
+    p["repeat_last_n"] = [512, 64, 512, 8]
+    p["frequency_penalty"] = [0.1, 0.0, 0.2, 0.0]
+    want = orc.sample_batch(x32 if dtype == "f32" else (xs.astype(np.float32) if dtype == "f16"
+                                                        else workloads.bf16_bits_to_f32(xs)),
+                            p, recent=recent, mask=mask, topk_cap=16)
+    g = run_gpu(sampler, xs, p, recent=recent, mask=mask, topk_cap=16, dtype=dtype)
+    check(g, want, 16)
