@@ -7,10 +7,11 @@
 // in the general kernel, each paying a chunk's selection and a share of a
 // row merge after its 32 KB stream.  Here the 1,024 workgroups are resident
 // at once (four a CU), each keeps two passes of loads in flight (double
-// buffering in registers: 2 x 2 slots of 16 bytes a thread), and a row's
-// selection work runs while the other workgroups of its CU stream.
+// buffering in registers: 2 x 4 slots of 16 bytes a thread, 2 x 3 for fp32),
+// and a row's selection work runs while the other workgroups of its CU
+// stream.
 //
-//   window    history positions (at most 1024) into an LDS hash keyed by id
+//   window    history positions (at most 512) into an LDS hash keyed by id
 //             that counts occurrences; the first position holding an id
 //             owns it, loads the id's logit and mask word, and offers the
 //             penalised value (tmsample.h:58-61, then frequency/presence) as
@@ -43,14 +44,13 @@
 namespace tms {
 namespace rows {
 
-constexpr int kPS = 2;              // 16-byte slots a thread per pass (per buffer)
 constexpr int kBuf = 1024;          // candidate buffer
-constexpr int kCompactAt = kBuf / 2;
+constexpr int kCompactAt = kBuf / 4;
 constexpr int kHashR = 2048;        // window table slots (at most 1024 ids)
 constexpr int kCntR = 11;           // occurrence count bits of a table word
 constexpr uint32_t kEmptyR = 0xFFFFFFFFu;
 constexpr uint32_t kOwnerBit = 0x80000000u;   // candidate id word: an owner's penalised entry
-constexpr int kMaxWindow = 1024;
+constexpr int kMaxWindow = 512;
 constexpr int kKMax = kTopkFast;    // the top-k promise: 1 <= top_k <= 128
 
 struct Smem {
@@ -109,7 +109,10 @@ template <typename T>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void row_kernel(KArgs a) {
     __shared__ Smem sm;
     constexpr int VEC = Elt<T>::kVec;
-    constexpr int PI = kBlock * kPS * VEC;   // ids a pass
+    // 16-byte slots a thread per pass (per buffer): four for 2-byte types,
+    // three for fp32, within the 128 registers of four workgroups a CU
+    constexpr int PS = sizeof(T) == 4 ? 3 : 4;
+    constexpr int PI = kBlock * PS * VEC;   // ids a pass
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int row = blockIdx.x;
     const int V = a.V;
@@ -127,13 +130,14 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         const int p = t + i * kBlock;
         hid[i] = (hrow && p < rs) ? hrow[p] : -1;
     }
-    uint4 A[kPS], B[kPS];
-    uint32_t mA[kPS], mB[kPS];
-    auto load = [&](uint4 (&buf)[kPS], uint32_t (&mw)[kPS], int p) {
+    uint4 A[PS], B[PS];
+    uint32_t mA[PS], mB[PS];
+    const bool masked = a.mask_stride != 0;   // 0: no caller mask (the all-ones row)
+    auto load = [&](uint4 (&buf)[PS], uint32_t (&mw)[PS], int p) {
 #pragma unroll
-        for (int j = 0; j < kPS; ++j) {
+        for (int j = 0; j < PS; ++j) {
             const int off = p * PI + VEC * (j * kBlock + t);
-            mw[j] = mrow[min(off, V - 1) >> 5];
+            mw[j] = masked ? mrow[min(off, V - 1) >> 5] : ~0u;
             buf[j] = ld_nt(base + min(off, V - VEC));
         }
     };
@@ -222,32 +226,45 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
     float gbv = NEG_INF;                // greedy: the thread's best value
     uint32_t gbi = 0xFFFFFFFFu;         //   and its (lowest) id
     float vlo = __builtin_huge_valf();  // top-k: no candidate before the bound
-    auto process = [&](uint4 (&buf)[kPS], uint32_t (&mw)[kPS], int p) {
+    auto process = [&](uint4 (&buf)[PS], uint32_t (&mw)[PS], int p) {
+        const bool first = p == 0;   // pass 0: window bits, the bound
         float pm = NEG_INF;
+        float smx[PS];   // each slot's maximum
 #pragma unroll
-        for (int j = 0; j < kPS; ++j) {
+        for (int j = 0; j < PS; ++j) {
             const int off = p * PI + VEC * (j * kBlock + t);
             const int lim = V - off;
-            uint32_t bits = lim > 0 ? (mw[j] >> (off & 31)) & ((1u << min(lim, VEC)) - 1u) : 0u;
-            if (p == 0) bits &= ~(wt >> (j * VEC));
-            buf[j] = fold_bits<T>(buf[j], bits);
+            // the fold only where a bit can be clear: a caller mask, pass 0's
+            // window ids, the row's last pass
+            if (masked || (first && wt) || p == NP - 1) {
+                uint32_t bits = lim > 0 ? (mw[j] >> (off & 31)) & ((1u << min(lim, VEC)) - 1u) : 0u;
+                if (first) bits &= ~(wt >> (j * VEC));
+                buf[j] = fold_bits<T>(buf[j], bits);
+            }
+            float sx = NEG_INF;
 #pragma unroll
             for (int e = 0; e < VEC; e += 2)
-                pm = __builtin_elementwise_maximum(pm, __builtin_elementwise_maximum(elt<T>(buf[j], e), elt<T>(buf[j], e + 1)));
-            if (track) {
+                sx = __builtin_elementwise_maximum(sx, __builtin_elementwise_maximum(elt<T>(buf[j], e), elt<T>(buf[j], e + 1)));
+            pm = __builtin_elementwise_maximum(pm, sx);
+            smx[j] = sx;
+            if (track && sx > gbv) {   // rare once the best has risen
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    const float x = elt<T>(buf[j], e);
-                    if (x > gbv) {   // ids grow along the thread's entries: the first is the lowest
-                        gbv = x;
-                        gbi = (uint32_t)(off + e);
-                    }
+                for (int e = VEC - 1; e >= 0; --e) {
+                    // the slot's first entry equal to its maximum: its lowest id
+                    if (elt<T>(buf[j], e) == sx) gbi = (uint32_t)(off + e);
                 }
+                gbv = sx;
             }
         }
         m = __builtin_elementwise_maximum(m, pm);
         if (!select) return;
-        if (p == 0) {
+        // The widened values are formed again from the words where they are
+        // used next (holding 2-byte entries widened would double their
+        // registers).
+#pragma unroll
+        for (int j = 0; j < PS; ++j)
+            asm volatile("" : "+v"(buf[j].x), "+v"(buf[j].y), "+v"(buf[j].z), "+v"(buf[j].w));
+        if (first) {
             // ---- bound: the K-th largest of the 128 group maxima (two lanes
             //      a group, order keys with the low 7 bits replaced by 127 -
             //      the group, so they are distinct), by rank counting
@@ -273,14 +290,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
             vlo = vlo_of(tk < 0x00800000u ? NEG_INF : okey_inv(tk), temp, divide);
         }
         // ---- candidates: entries at or above vlo, appended to the buffer
+        //      (slot by slot, only the slots whose maximum reaches vlo)
         if (__ballot(pm >= vlo)) {
-            if (pm >= vlo) {
 #pragma unroll
-                for (int j = 0; j < kPS; ++j) {
-                    const int off = p * PI + VEC * (j * kBlock + t);
+            for (int jj = 0; jj < PS; ++jj) {
+                if (smx[jj] >= vlo) {
+                    const int off = p * PI + VEC * (jj * kBlock + t);
 #pragma unroll
                     for (int e = 0; e < VEC; ++e) {
-                        const float x = elt<T>(buf[j], e);
+                        const float x = elt<T>(buf[jj], e);
                         if (x >= vlo) {
                             const int at = atomicAdd(&sm.ncand, 1);
                             if (at < kBuf) sm.cand[at] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(off + e);
@@ -373,9 +391,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         lds_sync();
     };
 
-    // A compaction check after every pair of passes (a barrier): a pair's
-    // appends stay below half the buffer (pass 0's bound keeps about 5% of
-    // its entries, later bounds far fewer), so they never meet a full one.
+    // A compaction check after every pair of passes (a barrier), at a
+    // quarter of the buffer: pass 0's bound keeps about 2-6% of its 8192
+    // entries (bf16 ties included), so the first pair appends up to about
+    // 500 (config 5's worst row: 492) and is compacted at once; later bounds
+    // keep far fewer.  Compacting at half the buffer let that row reach 1041
+    // candidates after its second pair, and the whole-row path (1.8 ms for
+    // the call).
     auto check = [&]() {
         if (select) {
             lds_sync();

@@ -1466,7 +1466,7 @@ static int sample_launch(const SampleWs& w, const tms_sample_args* a, hipStream_
             }
         }
     }
-    if (a->row_kinds == TMS_ROWS_TOPK && fast && (!a->recent || a->recent_stride <= 1024) &&
+    if (a->row_kinds == TMS_ROWS_TOPK && fast && (!a->recent || a->recent_stride <= 512) &&
         a->batch >= device_cus()) {
         // Top-k batches with a row for every CU: one workgroup a row streams
         // the whole row (B = 1024, V = 256000 bf16: no chunk merges).
