@@ -7,7 +7,7 @@
 // in the general kernel, each paying a chunk's selection and a share of a
 // row merge after its 32 KB stream.  Here the 1,024 workgroups are resident
 // at once (four a CU), each keeps two passes of loads in flight (double
-// buffering in registers: 2 x 4 slots of 16 bytes a thread, 2 x 3 for fp32),
+// buffering in registers: 2 x 3 slots of 16 bytes a thread),
 // and a row's selection work runs while the other workgroups of its CU
 // stream.
 //
@@ -20,8 +20,10 @@
 //             compaction (a hash lookup per candidate).
 //   pass      per 16-byte slot: the mask folded in (-inf in place), the
 //             thread's IEEE maximum (NaN / +inf); greedy rows keep each
-//             thread's best (value, lowest id); top-k rows append the entries
-//             at or above vlo to an LDS buffer.
+//             thread's best (value, lowest id); top-k rows stage the slots
+//             whose maximum reaches vlo in LDS, and after the next pass's
+//             loads are issued append their entries at or above vlo to an
+//             LDS buffer.
 //   bound     after pass 0: the K-th largest of its 128 group maxima (two
 //             lanes a group), by rank counting, bounds the row's K-th value
 //             from below; vlo is that bound less the margin that keeps every
@@ -51,6 +53,7 @@ constexpr int kCntR = 11;           // occurrence count bits of a table word
 constexpr uint32_t kEmptyR = 0xFFFFFFFFu;
 constexpr uint32_t kOwnerBit = 0x80000000u;   // candidate id word: an owner's penalised entry
 constexpr int kMaxWindow = 512;
+constexpr int kStg = 64;            // hot slots a wave stages (a full area is drained at once)
 constexpr int kKMax = kTopkFast;    // the top-k promise: 1 <= top_k <= 128
 
 struct Smem {
@@ -67,6 +70,8 @@ struct Smem {
     float wave_f[kWaves];
     int wave_i[kWaves];
     uint64_t theta;
+    alignas(16) uint4 stg[kWaves][kStg];     // per wave: the words of its hot slots
+    uint32_t sid[kWaves][kStg];              // and each one's first id
     int ncand, onf, over;
     uint32_t tkey;
     int misc[4];
@@ -109,9 +114,9 @@ template <typename T>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void row_kernel(KArgs a) {
     __shared__ Smem sm;
     constexpr int VEC = Elt<T>::kVec;
-    // 16-byte slots a thread per pass (per buffer): four for 2-byte types,
-    // three for fp32, within the 128 registers of four workgroups a CU
-    constexpr int PS = sizeof(T) == 4 ? 3 : 4;
+    // 16-byte slots a thread per pass (per buffer), within the 128
+    // registers of four workgroups a CU (four spill with the staging)
+    constexpr int PS = 3;
     constexpr int PI = kBlock * PS * VEC;   // ids a pass
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int row = blockIdx.x;
@@ -226,6 +231,24 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
     float gbv = NEG_INF;                // greedy: the thread's best value
     uint32_t gbi = 0xFFFFFFFFu;         //   and its (lowest) id
     float vlo = __builtin_huge_valf();  // top-k: no candidate before the bound
+    int nstg = 0;                       // the wave's staged hot slots (uniform)
+    // The staged slots' entries at or above vlo into the buffer: the wave
+    // takes 64 entries a step, one LDS atomic for all of a step's takes.
+    auto drain = [&]() {
+        if (!nstg) return;
+        __builtin_amdgcn_wave_barrier();
+        const T* hv = (const T*)&sm.stg[wv][0];
+        for (int q = lane; q < nstg * VEC; q += 64) {
+            const float x = Elt<T>::scalar(hv + q);
+            if (x >= vlo) {
+                const int at = atomicAdd(&sm.ncand, 1);
+                if (at < kBuf) sm.cand[at] = ((uint64_t)__float_as_uint(x) << 32) | (sm.sid[wv][q / VEC] + (uint32_t)(q % VEC));
+            }
+        }
+        nstg = 0;
+        __builtin_amdgcn_wave_barrier();
+    };
+
     auto process = [&](uint4 (&buf)[PS], uint32_t (&mw)[PS], int p) {
         const bool first = p == 0;   // pass 0: window bits, the bound
         float pm = NEG_INF;
@@ -289,22 +312,25 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
             const uint32_t tk = sm.tkey;
             vlo = vlo_of(tk < 0x00800000u ? NEG_INF : okey_inv(tk), temp, divide);
         }
-        // ---- candidates: entries at or above vlo, appended to the buffer
-        //      (slot by slot, only the slots whose maximum reaches vlo)
+        // ---- candidates: the slots whose maximum reaches vlo go to the
+        //      wave's staging area (no wait), and drain() appends their
+        //      entries after the next pass's loads are issued (or at once,
+        //      when a slot's hot lanes would not fit the area).
         if (__ballot(pm >= vlo)) {
 #pragma unroll
             for (int jj = 0; jj < PS; ++jj) {
-                if (smx[jj] >= vlo) {
-                    const int off = p * PI + VEC * (jj * kBlock + t);
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) {
-                        const float x = elt<T>(buf[jj], e);
-                        if (x >= vlo) {
-                            const int at = atomicAdd(&sm.ncand, 1);
-                            if (at < kBuf) sm.cand[at] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)(off + e);
-                        }
-                    }
+                const bool hot = smx[jj] >= vlo;
+                const uint64_t hb = __ballot(hot);
+                if (!hb) continue;
+                if (nstg + __popcll(hb) > kStg) drain();   // the area is full: empty it first
+                const int off = p * PI + VEC * (jj * kBlock + t);
+                const int pos = nstg + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(hb >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)hb, 0u));
+                if (hot) {
+                    sm.stg[wv][pos] = buf[jj];
+                    sm.sid[wv][pos] = (uint32_t)off;
                 }
+                nstg += __popcll(hb);
             }
         }
     };
@@ -407,9 +433,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
     for (int p = 0; p < NP; p += 2) {
         process(A, mA, p);
         if (p + 2 < NP) load(A, mA, p + 2);
+        drain();
         if (p + 1 < NP) {
             process(B, mB, p + 1);
             if (p + 3 < NP) load(B, mB, p + 3);
+            drain();
         }
         if (p == 0) {
             // the owners' penalised values (their loads were issued after
