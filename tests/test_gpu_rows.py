@@ -61,7 +61,7 @@ def rows_case(dtype, seed, V=40000):
     bits[9, 777] = bits[10, 31] = True   # the NaN and +inf are allowed
     bits[12] = False            # all masked
     bits[13, :] = False
-    bits[13, [5, 9000, 39999]] = True   # fewer finite ids than K
+    bits[13, [5, V // 4, V - 1]] = True   # fewer finite ids than K
     mask = workloads.pack_bits(bits)
     recent = rng.integers(0, V, (B, 512)).astype(np.int32)
     recent[:, ::9] = rng.integers(0, 4096, (B, (512 + 8) // 9))   # window ids in pass 0 too
@@ -115,3 +115,34 @@ def test_rows_kernel_no_mask_no_window(sampler, orc):
     want = orc.sample_batch(x, p)
     g = run(sampler, x, p, dtype="f32")
     check(g, want)
+
+
+@pytest.mark.parametrize("dtype,V", [("f32", 50020), ("f16", 50024), ("bf16", 33032)])
+def test_rows_kernel_ragged_vocab(sampler, orc, dtype, V):
+    """Vocabularies that end inside a mask word and inside a pass (33032 ids
+    of bf16 are five passes of 6144 and part of a sixth): the last pass's
+    mask fold and the ids past V."""
+    xs, xw, p, mask, recent, n_recent = rows_case(dtype, 70 + V % 97, V=V)
+    want = orc.sample_batch(xw, p, recent=recent, n_recent=n_recent, mask=mask, topk_cap=16)
+    g = run(sampler, xs, p, dtype=dtype, recent=recent, n_recent=n_recent, mask=mask, topk_cap=16)
+    check(g, want, 16)
+
+
+def test_rows_hint_past_the_window_limit(sampler, orc):
+    """A history window wider than the row-stream kernel's 512 positions:
+    the call takes the general kernel under the same hint and still equals
+    the oracle."""
+    rng = np.random.default_rng(81)
+    V, W = 20000, 600
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    recent = rng.integers(0, V, (B, W)).astype(np.int32)
+    recent[:, ::5] = recent[:, :1]
+    n_recent = rng.integers(0, W + 1, B).astype(np.int32)
+    p = params_array(B, temperature=0.9, top_k=40, top_p=0.95, seed=np.arange(B) + 5100)
+    p["greedy"] = rng.random(B) < 0.3
+    p["repeat_penalty"] = 1.2
+    p["repeat_last_n"] = W
+    p["frequency_penalty"] = 0.1
+    want = orc.sample_batch(x, p, recent=recent, n_recent=n_recent, topk_cap=8)
+    g = run(sampler, x, p, dtype="f32", recent=recent, n_recent=n_recent, topk_cap=8)
+    check(g, want, 8)

@@ -150,3 +150,27 @@ def test_sparse_edge_cases(sampler, orc, name):
         want = orc.sample_batch(x, p, recent=recent, mask=mask, topk_cap=cap)
         g = run(sampler, x, p, mask=mask, recent=recent, topk_cap=cap)
         check(g, want, cap)
+
+
+def test_sparse_hint_past_the_vocabulary_limit(orc):
+    """A vocabulary wider than the sparse-mask kernel's 262,144 ids: the
+    call takes the general kernel under the same hint and still equals the
+    oracle."""
+    from tensormark_amd import Sampler
+
+    rng = np.random.default_rng(91)
+    B, V = 4, 262144 + 96
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    mask = sparse_mask(rng, B, V, [50, 400, 7, 1000], runs=True)
+    bits = np.unpackbits(mask.view(np.uint8), bitorder="little").reshape(B, -1)
+    bits[:, V - 20:V] = True   # allowed ids past the kernel's limit
+    mask = workloads.pack_bits(bits)
+    p = params_array(B, temperature=1.0, top_k=0, top_p=0.9, seed=np.arange(B) + 31)
+    p["top_k"][1] = 40
+    s = Sampler(max_batch=B, max_vocab=V)
+    try:
+        want = orc.sample_batch(x, p, mask=mask, topk_cap=16)
+        g = run(s, x, p, mask=mask, topk_cap=16)
+        check(g, want, 16)
+    finally:
+        s.close()
