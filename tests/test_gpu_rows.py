@@ -146,3 +146,32 @@ def test_rows_hint_past_the_window_limit(sampler, orc):
     want = orc.sample_batch(x, p, recent=recent, n_recent=n_recent, topk_cap=8)
     g = run(sampler, x, p, dtype="f32", recent=recent, n_recent=n_recent, topk_cap=8)
     check(g, want, 8)
+
+
+@pytest.mark.parametrize("V", [100, 1000, 3076])
+def test_rows_kernel_short_rows(sampler, orc, V):
+    """Batches too large for the wide kernel's residency with rows shorter
+    than one pass (3,072 fp32 ids) or just past it: most threads hold no id,
+    and K can exceed the finite ids."""
+    rng = np.random.default_rng(V)
+    Bs = 600
+    x = rng.normal(0.0, 2.0, (Bs, V)).astype(np.float32)
+    x[0] = 0.5   # all ties
+    bits = rng.random((Bs, ((V + 31) // 32) * 32)) < 0.7
+    bits[:, V:] = False
+    bits[1] = False
+    bits[2, :] = False
+    bits[2, [0, V - 1]] = True
+    mask = workloads.pack_bits(bits)
+    W = 64
+    recent = rng.integers(-3, V + 3, (Bs, W)).astype(np.int32)
+    p = params_array(Bs, temperature=0.8, top_k=40, top_p=0.9, seed=np.arange(Bs) + 700)
+    p["greedy"] = rng.random(Bs) < 0.3
+    p["top_k"] = rng.choice([1, 5, 40, 128], size=Bs)
+    p["repeat_penalty"] = 1.3
+    p["repeat_last_n"] = W
+    p["presence_penalty"] = 0.2
+    want = orc.sample_batch(x, p, recent=recent, mask=mask, topk_cap=8)
+    g = run(sampler, x, p, dtype="f32", recent=recent, mask=mask, topk_cap=8)
+    assert g["status"][1] == 2
+    check(g, want, 8)
