@@ -19,8 +19,9 @@
 //             through a thread-major bitmap and later passes at each
 //             compaction (a hash lookup per candidate).
 //   pass      per 16-byte slot: the mask folded in (-inf in place), the
-//             thread's IEEE maximum (NaN / +inf); greedy rows keep each
-//             thread's best (value, lowest id); top-k rows stage the slots
+//             thread's IEEE maximum (NaN / +inf); greedy rows without a
+//             window keep each thread's best (value, lowest id); other rows
+//             (greedy ones as K = 1) stage the slots
 //             whose maximum reaches vlo in LDS, and after the next pass's
 //             loads are issued append their entries at or above vlo to an
 //             LDS buffer.
@@ -28,7 +29,8 @@
 //             lanes a group), by rank counting, bounds the row's K-th value
 //             from below; vlo is that bound less the margin that keeps every
 //             entry whose quotient by T can tie with it.
-//   compact   when the buffer passes half its size, and after the last pass:
+//   compact   after every pair of passes once the buffer is a quarter full,
+//             and after the last pass:
 //             two 8-bit histogram levels of the candidates' order keys find
 //             a value with at least K candidates at or above it, which
 //             raises vlo; entries below the new vlo leave.
@@ -586,7 +588,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
 
 // Launch of the row-stream kernel for tms_sample_batch: one workgroup a row
 // (16-byte aligned rows, vocab a multiple of the vector width, a window of
-// at most 1024 positions; the host checks).
+// at most kMaxWindow = 512 positions; the host checks).
 int tms_launch_rows(const tms::KArgs& k, int dtype, int batch, hipStream_t stream) {
     const dim3 grid((unsigned)batch), block(tms::kBlock);
     switch (dtype) {
