@@ -5,21 +5,25 @@
 // A masked-out id is -inf before anything else (tensormark/llama_chat.cpp
 // GrammarFilter::apply, then tmsample::sample), so it takes no part in the
 // penalties, the top-k, the softmax sums or the draw except as a -inf entry:
-// the row's answer depends on the allowed ids' logits alone.  One 256-thread
-// workgroup a row:
+// the row's answer depends on the allowed ids' logits alone.  One
+// 1024-thread workgroup a row:
 //
 //   mask      the row's mask words into registers (thread t: words t,
-//             t + 256, ..., every load issued at once); each thread's
-//             allowed count and a block scan give every entry's index;
-//   gather    the allowed ids in LDS, then their logits, up to eight loads
-//             a thread issued together;
+//             t + 1024, ..., at most kWpt, every load issued at once); each
+//             thread's allowed count and a 16-wave scan give every entry's
+//             index;
+//   ids       each wave's non-zero words expanded half-wave by half-wave
+//             (lane j of a half takes bit j), two words a step, into the
+//             allowed ids in LDS; then their logits, at most kGpt loads a
+//             thread issued together;
 //   window    history counts per allowed entry (an id's entry index from its
 //             word's prefix and a popcount), the compounding penalty
 //             (tmsample.h:58-61), then frequency/presence;
-//   select    greedy: the largest key; sampled rows: keys (v / T, then lowest
-//             id) ranked by bucket_rank, then the fp64 tail of
-//             tmsample::sample (tmsample.h:184-199): tail_topk for top-k <=
-//             128, else the top-p block tail.
+//   select    greedy: the largest key; sampled rows, on waves 0-3 (the
+//             others leave): keys (v / T, then lowest id) ranked by
+//             bucket_rank, then the fp64 tail of tmsample::sample
+//             (tmsample.h:184-199): tail_topk for top-k <= 128, else the
+//             top-p block tail.
 //
 // A row with more than kSparseCap allowed ids, a top-p row with more than
 // kToppCap finite entries, or an answer that needs the order past the held
