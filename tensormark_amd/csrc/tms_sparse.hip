@@ -57,6 +57,7 @@ struct Smem {
     uint64_t wave_k[kNW];
     float wave_f[kWaves];
     int wave_i[kNW];
+    int wave_z[kNW];
     uint64_t theta;
     int misc[4];
 };
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
     //      leaving after the keys.
     const uint32_t tail_bits = (V & 31) ? (1u << (V & 31)) - 1u : ~0u;
     uint32_t mwr[kWpt];
-    int c = 0;
+    int c = 0, cz = 0;
 #pragma unroll
     for (int i = 0; i < kWpt; ++i) {
         const int w = t + i * kNT;
@@ -108,20 +109,29 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
         if (w == W - 1) x &= tail_bits;
         mwr[i] = x;
         c += __popc(x);
+        cz += x ? 1 : 0;
     }
-    // the thread's first entry index: a scan over the 16 waves
-    int n = 0, tb = 0;
+    // the thread's first entry index and its first slot in the list of
+    // non-zero words: scans over the 16 waves
+    int n = 0, tb = 0, nzw = 0, zb = 0;
     {
         const int inc = wave_incl_scan_i32(c);
-        if (lane == 63) sm.wave_i[wv] = inc;
+        const int incz = wave_incl_scan_i32(cz);
+        if (lane == 63) {
+            sm.wave_i[wv] = inc;
+            sm.wave_z[wv] = incz;
+        }
         lds_sync();
 #pragma unroll
         for (int i = 0; i < kNW; ++i) {
-            const int x = sm.wave_i[i];
+            const int x = sm.wave_i[i], z = sm.wave_z[i];
             tb += i < wv ? x : 0;
+            zb += i < wv ? z : 0;
             n += x;
+            nzw += z;
         }
         tb += inc - c;
+        zb += incz - cz;
         lds_sync();
     }
 
@@ -165,14 +175,17 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
     }
 
     // ---- the allowed ids in entry order (thread, then word), then their
-    //      logits.  Word i of every lane in turn: each lane whose word is
-    //      non-zero is expanded by the whole wave, half-wave by half-wave
-    //      (lane j of a half takes bit j), so no lane loops over its bits.
-    //      With a window, each word and its first entry index go to LDS for
-    //      the history lookups.
+    //      logits.  The non-zero words go to a list (word, its index, its
+    //      first entry index), and the workgroup's 32 half-waves expand the
+    //      list's words in turn (lane j of a half takes bit j), so no lane
+    //      loops over its bits or its zero words.  With a window, each word
+    //      and its first entry index go to LDS for the history lookups.
     {
-        int e = tb;
-        const int half = lane >> 5, bitj = lane & 31;
+        // n <= kSparseCap here, so at most that many non-zero words, each
+        // entry index below 2^11 and each word index below 2^13
+        static_assert(kSparseCap <= 2048 && kMaxWords <= 8192, "list word packing");
+        uint64_t* wl = sm.keys;   // dead until the keys are formed
+        int e = tb, z = zb;
 #pragma unroll
         for (int i = 0; i < kWpt; ++i) {
             const int w = t + i * kNT;
@@ -181,26 +194,16 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
                 sm.mw[w] = x;
                 sm.wpre[w] = (uint16_t)e;
             }
-            uint64_t nz = __ballot(x != 0u);
-            while (nz) {
-                // up to two non-zero lanes at once: the lowest to half 0,
-                // the next to half 1
-                const int l0 = __builtin_ctzll(nz);
-                nz &= nz - 1ull;
-                const int l1 = nz ? __builtin_ctzll(nz) : l0;
-                if (nz) nz &= nz - 1ull;
-                const int src = half ? l1 : l0;
-                const uint32_t x0 = (uint32_t)__builtin_amdgcn_readlane((int)x, l0);
-                const uint32_t x1 = (uint32_t)__builtin_amdgcn_readlane((int)x, l1);
-                const int e0 = __builtin_amdgcn_readlane(e, l0), e1 = __builtin_amdgcn_readlane(e, l1);
-                const uint32_t xs = half ? x1 : x0;
-                const int es = half ? e1 : e0;
-                const bool take = (half == 0 || l1 != l0) && ((xs >> bitj) & 1u);
-                if (take)
-                    sm.ids[es + __popc(xs & ((1u << bitj) - 1u))] =
-                        (uint32_t)(((src + (wv << 6) + i * kNT) << 5) + bitj);
-            }
+            if (x) wl[z++] = ((uint64_t)x << 32) | (uint32_t)((w << 11) | e);
             e += __popc(x);
+        }
+        lds_sync();
+        const int bitj = lane & 31;
+        for (int q = t >> 5; q < nzw; q += kNT / 32) {
+            const uint64_t d = wl[q];
+            const uint32_t x = (uint32_t)(d >> 32), we = (uint32_t)d;
+            if ((x >> bitj) & 1u)
+                sm.ids[(we & 2047u) + __popc(x & ((1u << bitj) - 1u))] = ((we >> 11) << 5) + (uint32_t)bitj;
         }
     }
     if (pn.on)
