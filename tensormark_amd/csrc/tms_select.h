@@ -23,38 +23,50 @@ namespace tms {
 // reordered; cnt holds kBuckets ints of scratch.  Correct for any keys;
 // massive ties (one bucket holding most keys) only cost time.  Keys equal
 // to 0 (never a real key) are absent: unranked and not counted.
+//
+// kGiven: the caller passes the keys' quotient range [qmin, qmax] (any
+// range keeps the bucket function monotone; the true one spreads the keys)
+// and has zeroed cnt[0..kBuckets) before a barrier, which saves the range's
+// reduction and its barrier.
 constexpr int kBuckets = 2 * kBlock;
-template <int kPer, typename SM>   // keys per thread: n <= kPer * kBlock
-__device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int* cnt, SM& sm) {
+template <int kPer, bool kGiven = false, typename SM>   // keys per thread: n <= kPer * kBlock
+__device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int* cnt, SM& sm,
+                            float qmax_in = 0.0f, float qmin_in = 0.0f) {
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    if constexpr (!kGiven) {
 #pragma unroll
-    for (int u = 0; u < kBuckets / kBlock; ++u) cnt[t * (kBuckets / kBlock) + u] = 0;
+        for (int u = 0; u < kBuckets / kBlock; ++u) cnt[t * (kBuckets / kBlock) + u] = 0;
+    }
     uint64_t k[kPer];
     float qhi = -__builtin_huge_valf(), qlo_neg = -__builtin_huge_valf();
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
         const int i = t + u * kBlock;
         k[u] = i < n ? keys[i] : 0ull;
-        if (k[u] != 0ull) {
+        if (!kGiven && k[u] != 0ull) {
             const float q = ckey_val(k[u]);
             qhi = fmaxf(qhi, q);
             qlo_neg = fmaxf(qlo_neg, -q);
         }
     }
-    qhi = wave_max_f32_dpp(qhi);
-    qlo_neg = wave_max_f32_dpp(qlo_neg);
-    if (lane == 0) {
-        sm.wave_f[wv] = qhi;
-        sm.wave_k[wv] = __float_as_uint(qlo_neg);
-    }
-    lds_sync();
-    float qmax = sm.wave_f[0], qmin_neg = __uint_as_float((uint32_t)sm.wave_k[0]);
+    float qmax = qmax_in, qmin = qmin_in;
+    if constexpr (!kGiven) {
+        qhi = wave_max_f32_dpp(qhi);
+        qlo_neg = wave_max_f32_dpp(qlo_neg);
+        if (lane == 0) {
+            sm.wave_f[wv] = qhi;
+            sm.wave_k[wv] = __float_as_uint(qlo_neg);
+        }
+        lds_sync();
+        float qmin_neg = __uint_as_float((uint32_t)sm.wave_k[0]);
+        qmax = sm.wave_f[0];
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) {
-        qmax = fmaxf(qmax, sm.wave_f[i]);
-        qmin_neg = fmaxf(qmin_neg, __uint_as_float((uint32_t)sm.wave_k[i]));
+        for (int i = 1; i < kWaves; ++i) {
+            qmax = fmaxf(qmax, sm.wave_f[i]);
+            qmin_neg = fmaxf(qmin_neg, __uint_as_float((uint32_t)sm.wave_k[i]));
+        }
+        qmin = -qmin_neg;
     }
-    const float qmin = -qmin_neg;
     const float span = qmax - qmin;
     // a span that is 0, or not finite, puts every key in bucket 0
     const float scale = (span > 0.0f && span <= FLT_MAX) ? (float)(kBuckets - 1) / span : 0.0f;

@@ -58,6 +58,7 @@ struct Smem {
     float wave_f[kWaves];
     int wave_i[kNW];
     int wave_z[kNW];
+    float wave_q[kNW];               // the least finite key quotient per wave
     uint64_t theta;
     int misc[4];
 };
@@ -232,6 +233,7 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
     }
     int bad = 0, fin = 0;
     uint64_t gbest = 0ull;
+    float qlo = __builtin_huge_valf();
 #pragma unroll
     for (int j = 0; j < kGpt; ++j) {
         const int e = t + j * kNT;
@@ -248,6 +250,7 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
             uint64_t key = 0ull;
             if (x != -__builtin_huge_valf()) {
                 key = ckey(divide ? x / temp : x, sm.ids[e]);
+                qlo = fminf(qlo, ckey_val(key));
                 ++fin;
             }
             gbest = key > gbest ? key : gbest;
@@ -258,20 +261,25 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
     bad = __any(bad != 0);
     fin = wave_sum_dpp(fin);
     gbest = wave_max_u64_dpp(gbest);
+    qlo = -wave_max_f32_dpp(-qlo);
     if (lane == 0) {
         sm.wave_i[wv] = bad ? -1 : fin;
         sm.wave_k[wv] = gbest;
+        sm.wave_q[wv] = qlo;
     }
+    if (t < kBuckets) sm.pbits[t] = 0;   // bucket_rank's counts, zeroed before its atomics
     lds_sync();
     int N = 0;
     bool nonfin = false;
     uint64_t best = 0ull;
+    float qmin = __builtin_huge_valf();
 #pragma unroll
     for (int w = 0; w < kNW; ++w) {
         const int x = sm.wave_i[w];
         nonfin |= x < 0;
         N += x < 0 ? 0 : x;
         best = sm.wave_k[w] > best ? sm.wave_k[w] : best;
+        qmin = fminf(qmin, sm.wave_q[w]);
     }
     if (t >= kBlock) return;   // from here waves 0-3 (the leavers drop out of the barriers)
     lds_sync();   // the totals are read before bucket_rank writes wave_k again
@@ -307,12 +315,14 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
         // ---- rank: the top min(N, K) keys (zero keys are absent) into srt
         const int nkeep = min(N, K);
         sm.keys[n] = 0ull;   // bucket_rank reads whole 16-byte words
+        // the range of the finite keys' quotients, from the block totals
+        const float qmax = ckey_val(best);
         if (n <= 2 * kBlock) {
-            [[clang::always_inline]] bucket_rank<2>(sm.keys, n, nkeep, sm.srt, sm.pbits, sm);
+            [[clang::always_inline]] bucket_rank<2, true>(sm.keys, n, nkeep, sm.srt, sm.pbits, sm, qmax, qmin);
         } else if (n <= 4 * kBlock) {
-            [[clang::always_inline]] bucket_rank<4>(sm.keys, n, nkeep, sm.srt, sm.pbits, sm);
+            [[clang::always_inline]] bucket_rank<4, true>(sm.keys, n, nkeep, sm.srt, sm.pbits, sm, qmax, qmin);
         } else {
-            [[clang::always_inline]] bucket_rank<kPer>(sm.keys, n, nkeep, sm.srt, sm.pbits, sm);
+            [[clang::always_inline]] bucket_rank<kPer, true>(sm.keys, n, nkeep, sm.srt, sm.pbits, sm, qmax, qmin);
         }
         lds_sync();
         uint32_t w0, w1;
