@@ -1164,7 +1164,7 @@ __global__ __launch_bounds__(kBlock, 3) void sample_kernel(KArgs a) {
             n = min(n, K);   // tmsample::sample sums over the top K only (tmsample.h:185-191)
         }
         TMS_TR(14);
-        const int tp = tail_topp_block(a, row, P, srt, n, K, pr, rw0, rw1, sm);
+        const int tp = tail_topp_block(a, row, P, srt, n, K, pr, q, rw0, rw1, sm);
         TMS_TR(15);
         if (tp == 2) {
             // the sequential tail decides (or returns the probabilities)

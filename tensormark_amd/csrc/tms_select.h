@@ -119,7 +119,8 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
 
 // The top-p tail from block prefix sums (every thread of the workgroup),
 // for n <= kToppCap entries pr[0..n) in LDS (srt, K, P as in tail_topp).
-// Thread t holds the entries [t * per, t * per + per), per =
+// Every prefix also goes to pre[0..n) (LDS, room for n doubles, apart
+// from pr). Thread t holds the entries [t * per, t * per + per), per =
 // ceil(n / kBlock) rounded up to odd (<= 5: an odd stride keeps the
 // threads' 8-byte reads on distinct banks), and a prefix is its sequential
 // partial sum within the thread, plus the exclusive scan of the thread
@@ -135,13 +136,13 @@ __device__ void bucket_rank(uint64_t* keys, int n, int nkeep, uint64_t* out, int
 // threshold, and any call that returns per-entry probabilities, takes the
 // sequential tail_topp.  The min-p cut compares the same pr values, so it is
 // exact here.  The decisions (first index at or above a threshold,
-// definitely or within the margin) meet in LDS: four barriers in place of
+// definitely or within the margin) meet in LDS: three barriers in place of
 // one wave's serial chains.  Returns 0 when the row is written, 1 when the
 // answer needs the order past the held entries (the whole-row path), 2 when
 // only tail_topp can decide.  Every thread gets the same value.
 template <typename SM>
 __device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tms_row_params& P, const uint64_t* srt, int n,
-                               int K, const double* pr, uint32_t w0, uint32_t w1, SM& sm) {
+                               int K, const double* pr, double* pre, uint32_t w0, uint32_t w1, SM& sm) {
     static_assert(kToppCap <= kBlock * 4, "thread blocks of at most 5 entries");
     if (a.topk_cap && a.out_topk_probs) return 2;
     if (n < K && a.topk_cap > n && a.out_topk_ids) return 1;
@@ -170,7 +171,10 @@ __device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tm
         z += v;
     }
 #pragma unroll
-    for (int j = 0; j < 5; ++j) c[j] = base + (excl + c[j]);
+    for (int j = 0; j < 5; ++j) {
+        c[j] = base + (excl + c[j]);
+        if (j < per && b0 + j < n) pre[b0 + j] = c[j];   // read after the next barrier
+    }
     constexpr double kRelP = (4.0 * kToppCap + 64.0) * 0x1p-53;
     constexpr double kAbs = 1e-300;
     constexpr int kNone = 1 << 30;
@@ -233,17 +237,10 @@ __device__ __forceinline__ int tail_topp_block(const KArgs& a, int row, const tm
     const int lim = keep < n ? keep : n;
     int tokidx = 0;
     if (ok && keep >= 2) {
-        // sum = the prefix at lim - 1, from the thread that holds it
-        const int e = lim - 1, le = e / per, je = e - le * per;
-        if (t == le) {
-            double mine = 0.0;
-#pragma unroll
-            for (int j = 0; j < 5; ++j) mine = j == je ? c[j] : mine;
-            sm.theta = __builtin_bit_cast(uint64_t, mine);   // free since the merge
-        }
+        // sum = the prefix at lim - 1 (every prefix went to pre before
+        // block_min3's barrier)
         const double u = canonical(w0, w1);
-        lds_sync();
-        const double sum = __builtin_bit_cast(double, sm.theta);
+        const double sum = pre[lim - 1];
         // cp at keep - 1 is 1.0 exactly (> u): only indices before it are
         // decided from the prefixes
         const int dl = min(lim, keep - 1);

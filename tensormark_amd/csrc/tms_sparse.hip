@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
         ns = min(ns, K);
         lds_sync();
         row_uniform(a, row, P, w0, w1);
-        const int tp = tail_topp_block(a, row, P, sm.srt, ns, K, sm.pr, w0, w1, sm);
+        const int tp = tail_topp_block(a, row, P, sm.srt, ns, K, sm.pr, sm.q, w0, w1, sm);
         if (tp == 2) {
             if (wv == 0) {
                 bool lost;
