@@ -57,7 +57,8 @@ struct Smem {
     uint64_t wave_k[kNW];
     float wave_f[kWaves];
     int wave_i[kNW];
-    int wave_z[kNW];
+    int wave_s[kNW];                 // the mask scan's per-wave counts (written once)
+    int wave_z[kNW];                 //   and non-zero words
     float wave_q[kNW];               // the least finite key quotient per wave
     uint64_t theta;
     int misc[4];
@@ -119,13 +120,13 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
         const int inc = wave_incl_scan_i32(c);
         const int incz = wave_incl_scan_i32(cz);
         if (lane == 63) {
-            sm.wave_i[wv] = inc;
+            sm.wave_s[wv] = inc;
             sm.wave_z[wv] = incz;
         }
         lds_sync();
 #pragma unroll
         for (int i = 0; i < kNW; ++i) {
-            const int x = sm.wave_i[i], z = sm.wave_z[i];
+            const int x = sm.wave_s[i], z = sm.wave_z[i];
             tb += i < wv ? x : 0;
             zb += i < wv ? z : 0;
             n += x;
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(kNT) void sparse_kernel(KArgs a) {
         }
         tb += inc - c;
         zb += incz - cz;
-        lds_sync();
+        // no barrier: nothing writes wave_s or wave_z again
     }
 
     const bool greedy = P.greedy != 0;
