@@ -755,8 +755,25 @@ void spec_row_kernel(SArgs a) {
     int nf = 0;
     if (div) row_max<T, NS, kRowT, true>(q, nv, temp, mx, nf);
     else row_max<T, NS, kRowT, false>(q, nv, temp, mx, nf);
-    mx = block_max_f32<kRowW>(mx, L.shf);   // also orders the table's LDS writes
-    nf = block_or<kRowW>(nf, L.misc);
+    // The row's maximum and NaN/+inf flag in one exchange: each wave's pair
+    // in LDS words written once, so one barrier (which also orders the
+    // table's LDS writes) and none after the reads.
+    {
+        const float wm = wave_max_f32(mx);
+        const int wn = __any(nf) ? 1 : 0;
+        if ((t & 63) == 0) {
+            L.shf[t >> 6] = wm;
+            L.misc[t >> 6] = wn;
+        }
+        lds_sync();
+        mx = L.shf[0];
+        nf = L.misc[0];
+#pragma unroll
+        for (int i = 1; i < kRowW; ++i) {
+            mx = fmaxf(mx, L.shf[i]);
+            nf |= L.misc[i];
+        }
+    }
     int st = TMS_ROW_OK;
     if (nf) st = TMS_ROW_NONFINITE;
     else if (mx == -__builtin_huge_valf()) st = TMS_ROW_ALL_MASKED;
@@ -765,7 +782,15 @@ void spec_row_kernel(SArgs a) {
     int64_t z = 0;
     if (st == TMS_ROW_OK)
         z = div ? row_z<T, NS, kRowT, true>(q, nv, temp, md, L.tab) : row_z<T, NS, kRowT, false>(q, nv, temp, md, L.tab);
-    z = block_sum_i64<kRowW>(z, L.shl);
+    {   // Z: each wave's share in LDS words written once (one barrier)
+        const int64_t wz = wave_sum_i64(z);
+        if ((t & 63) == 0) L.shl[t >> 6] = wz;
+        lds_sync();
+        z = 0;
+        if (t == 0)
+#pragma unroll
+            for (int i = 0; i < kRowW; ++i) z += L.shl[i];
+    }
     if (t == 0) {
         const int64_t ex = (st == TMS_ROW_OK && xin) ? weight(xv, temp, md, L.tab) : 0;
         uint64_t* w = (uint64_t*)(a.stats + (int64_t)b * (2 * a.k + 1) + i);
