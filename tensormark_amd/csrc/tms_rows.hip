@@ -66,7 +66,8 @@ struct Smem {
     uint32_t wtab[kHashR];                   // id << kCntR | occurrences, or kEmptyR
     uint32_t wbits[kBlock];                  // pass 0 window ids, thread-major
     alignas(16) uint32_t gmax[128];          // pass 0 group maxima (order keys)
-    int hist[256];
+    int hist[256];                           // compaction level 1 (zero between compactions)
+    int hist2[256];                          //   and level 2
     int pbits[kBuckets];                     // bucket_rank's counts
     uint64_t wave_k[kWaves];
     float wave_f[kWaves];
@@ -184,6 +185,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         sm.onf = 0;
         sm.over = 0;
     }
+    sm.hist[t] = 0;
+    sm.hist2[t] = 0;
     if (pn.on) {
         sm.wbits[t] = 0u;
         for (int i = t; i < kHashR; i += kBlock) sm.wtab[i] = kEmptyR;
@@ -341,8 +344,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
     //      order keys find tau with at least K candidates at or above it;
     //      vlo rises to vlo_of(tau) and the entries below leave.  Stream
     //      copies of window ids leave too (their owners' entries stay).
-    auto compact = [&]() {
-        lds_sync();
+    //      The histograms are zero on entry (each is cleared after its last
+    //      read), and the count is cleared once every thread has read it.
+    auto compact = [&](bool synced) {
+        if (!synced) lds_sync();
         const int nc = min(sm.ncand, kBuf);
         if (sm.ncand > kBuf && t == 0) sm.over = 1;
         uint64_t c[kBuf / kBlock];
@@ -359,18 +364,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
                 if (dup) c[u] = 0ull;
             }
         }
-        sm.hist[t] = 0;
-        lds_sync();
 #pragma unroll
         for (int u = 0; u < kBuf / kBlock; ++u)
             if (kk[u]) atomicAdd(&sm.hist[kk[u] >> 24], 1);
         lds_sync();
+        if (t == 0) sm.ncand = 0;   // read by every thread before the barrier
         // wave 0: the bin where the count from the top first reaches K
-        auto pick = [&](int above0, int* out) {
+        auto pick = [&](int above0, int* out, const int* hist) {
             int h[4], s = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                h[i] = sm.hist[255 - (4 * lane + i)];
+                h[i] = hist[255 - (4 * lane + i)];
                 s += h[i];
             }
             int above = above0 + wave_incl_scan_i32(s) - s;
@@ -388,27 +392,26 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
                 above += h[i];
             }
         };
-        if (wv == 0) pick(0, sm.misc);
+        if (wv == 0) pick(0, sm.misc, sm.hist);
         lds_sync();
         const int b1 = sm.misc[0], above1 = sm.misc[1];
+        sm.hist[t] = 0;   // read by pick before the barrier
         uint32_t tau = 0u;
         if (b1 >= 0) {
-            sm.hist[t] = 0;
-            lds_sync();
 #pragma unroll
             for (int u = 0; u < kBuf / kBlock; ++u)
-                if (kk[u] && (int)(kk[u] >> 24) == b1) atomicAdd(&sm.hist[(kk[u] >> 16) & 0xFF], 1);
+                if (kk[u] && (int)(kk[u] >> 24) == b1) atomicAdd(&sm.hist2[(kk[u] >> 16) & 0xFF], 1);
             lds_sync();
-            if (wv == 0) pick(above1, sm.misc + 2);
+            if (wv == 0) pick(above1, sm.misc + 2, sm.hist2);
             lds_sync();
             tau = ((uint32_t)b1 << 24) | ((uint32_t)max(sm.misc[2], 0) << 16);
+            sm.hist2[t] = 0;
         }
         // at least K candidates have a key >= tau, so the row's K-th value is
         // at least okey_inv(tau); keys below 0x00800000 decode to -inf or NaN
         const float nv = vlo_of(tau < 0x00800000u ? NEG_INF : okey_inv(tau), temp, divide);
         vlo = fmaxf(vlo, nv);
-        if (t == 0) sm.ncand = 0;
-        lds_sync();
+        // the count was cleared before the last barrier
 #pragma unroll
         for (int u = 0; u < kBuf / kBlock; ++u) {
             if (c[u] && __uint_as_float((uint32_t)(c[u] >> 32)) >= vlo) {
@@ -429,7 +432,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
     auto check = [&]() {
         if (select) {
             lds_sync();
-            if (sm.ncand > kCompactAt) compact();
+            if (sm.ncand > kCompactAt) compact(true);
         }
     };
     for (int p = 0; p < NP; p += 2) {
@@ -471,7 +474,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         sm.wave_k[wv] = best;
         sm.wave_i[wv] = (anynf ? 1 : 0) | (anyfin ? 2 : 0);
     }
-    if (select) compact();
+    if (select) compact(false);
     lds_sync();
     uint64_t gb = 0ull;
     int fl = 0;
